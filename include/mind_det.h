@@ -1,0 +1,162 @@
+/*
+ * mind_det.h -- C ABI of libmind_det_hip.so: MIND's deterministic integer and
+ * Q16.16 linear-algebra intrinsics as hand-written HIP kernels for MI355X
+ * (gfx950).  Every result is bit-identical to the reference CPU kernels.
+ *
+ * Citations are into star-ga/mind v0.10.2.  Arithmetic contract:
+ *   int8 GEMM : C[i,j] = (int32) sum_k A[i,k]*B[k,j]              (exact, wrapped)
+ *   Q16 GEMM  : C[i,j] = (int32) sum_k ((int64)A[i,k]*B[k,j] >>arith 16)
+ *   int16     : (int32) sum (int64)a*b                            (exact, wrapped)
+ *   Q16 GEMV  : y[i]   = (int32) sum_k ((int64)W[i,k]*x[k] >>arith 16)
+ * All matrices are dense row-major; B is K x N (not transposed) unless a
+ * symbol says otherwise.
+ *
+ * Layer 1 and 2 keep the reference's i64 "Option C" ABI: every pointer is an
+ * int64_t address of HOST memory, the call is synchronous, and it returns 0
+ * on success.  A NULL pointer or an empty shape returns 0 and writes nothing
+ * (Track A convention, runtime-support/mind_intrinsics.c:1537-1539).  A
+ * negative return is a device failure or an invalid shape (dimension
+ * outside [0, 2^31)); det_last_error() describes it.
+ */
+#ifndef MIND_DET_H
+#define MIND_DET_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* error codes (negative returns) */
+#define DET_ERR_ARG (-22)
+#define DET_ERR_HIP (-5)
+#define DET_ERR_DEVICE (-19)
+
+/* op selectors for the workspace-explicit entry points */
+#define DET_OP_I8 1
+#define DET_OP_I16 2
+#define DET_OP_Q16 3
+
+/* ------------------------------------------------------------------------
+ * Layer 1: the reference's intrinsic symbols (arity table
+ * src/type_checker/mod.rs:2266-2332).
+ * ---------------------------------------------------------------------- */
+
+/* Replaces __mind_blas_matmul_mm_i8_v: src/type_checker/mod.rs:2304,
+ * src/mlir/lowering.rs:2918-2925 (dispatch), :7687-7797, :8371-9265. */
+int64_t __mind_blas_matmul_mm_i8_v(int64_t a, int64_t b, int64_t c, int64_t m, int64_t k, int64_t n);
+/* Replaces __mind_blas_matmul_mm_i8_mt_v: src/mlir/lowering.rs:2935-2942,
+ * :10368-10700 (owner-computes row bands; here one GPU grid). */
+int64_t __mind_blas_matmul_mm_i8_mt_v(int64_t a, int64_t b, int64_t c, int64_t m, int64_t k, int64_t n);
+/* Replaces __mind_blas_matmul_mm_q16_v: src/type_checker/mod.rs:2316,
+ * src/mlir/lowering.rs:2864-2871, :9300-9410. */
+int64_t __mind_blas_matmul_mm_q16_v(int64_t a, int64_t b, int64_t c, int64_t m, int64_t k, int64_t n);
+/* Replaces __mind_blas_matmul_mm_q16_mt_v: src/mlir/lowering.rs:2879-2891,
+ * :10019-10340. */
+int64_t __mind_blas_matmul_mm_q16_mt_v(int64_t a, int64_t b, int64_t c, int64_t m, int64_t k, int64_t n);
+/* Replaces __mind_blas_gemv_q16_mt(w, x, y, m, k): src/type_checker/mod.rs:2332,
+ * src/mlir/lowering.rs:2901-2907, :9822-9997. */
+int64_t __mind_blas_gemv_q16_mt(int64_t w, int64_t x, int64_t y, int64_t m, int64_t k);
+/* Replaces __mind_blas_matmul_rmajor_q16_v(w, x, y, rows, cols):
+ * src/mlir/lowering.rs:2847-2852, :6675-7035. */
+int64_t __mind_blas_matmul_rmajor_q16_v(int64_t w, int64_t x, int64_t y, int64_t rows, int64_t cols);
+/* Replaces __mind_blas_matmul_rmajor_i16_v(w, x, y, rows, cols):
+ * src/type_checker/mod.rs:2285, src/mlir/lowering.rs:2948-2953, :10723-11150. */
+int64_t __mind_blas_matmul_rmajor_i16_v(int64_t w, int64_t x, int64_t y, int64_t rows, int64_t cols);
+/* Replaces __mind_blas_dot_q16(a, b, len) -> (int64)(int32)sum:
+ * runtime-support/mind_intrinsics.c:1537-1547.  Returns the value. */
+int64_t __mind_blas_dot_q16(int64_t a, int64_t b, int64_t len);
+/* Replaces __mind_blas_dot_q16_v (the vector-dialect twin of the above):
+ * src/mlir/lowering.rs:5695-5860. */
+int64_t __mind_blas_dot_q16_v(int64_t a, int64_t b, int64_t len);
+
+/* ------------------------------------------------------------------------
+ * Layer 2: the harness wrappers the reference benches and golden gate
+ * dlsym (tests/cross_substrate_identity.rs:70-150, xnode_driver.c:123-125).
+ * ---------------------------------------------------------------------- */
+/* gemmi8: benches/det_matmul_i8.rs:120-129 */
+int64_t gemmi8(int64_t a, int64_t b, int64_t c, int64_t m, int64_t k, int64_t n);
+/* gemmi8mt: tests/cross_substrate_identity.rs:106-108 */
+int64_t gemmi8mt(int64_t a, int64_t b, int64_t c, int64_t m, int64_t k, int64_t n);
+/* gemmqmm (fused Q16, B is K x N): tests/cross_substrate_identity.rs:142-150 */
+int64_t gemmqmm(int64_t a, int64_t b, int64_t c, int64_t m, int64_t k, int64_t n);
+/* gemmq: Q16 GEMM with B given TRANSPOSED as bt[N][K] (the gemv-composed
+ * form): tests/cross_substrate_identity.rs:82-94 */
+int64_t gemmq(int64_t a, int64_t bt, int64_t c, int64_t m, int64_t k, int64_t n);
+/* mmq / mmi16: tests/cross_substrate_identity.rs:76-81 */
+int64_t mmq(int64_t w, int64_t x, int64_t y, int64_t rows, int64_t cols);
+int64_t mmi16(int64_t w, int64_t x, int64_t y, int64_t rows, int64_t cols);
+/* gemvq: benches/det_gemv_q16_mt.rs:90-94 */
+int64_t gemvq(int64_t catalog, int64_t query, int64_t scores, int64_t m, int64_t k);
+/* dotq: tests/cross_substrate_identity.rs:70-72 */
+int64_t dotq(int64_t a, int64_t b, int64_t n);
+
+/* ------------------------------------------------------------------------
+ * Layer 3: typed entry points of this build.
+ * ---------------------------------------------------------------------- */
+/* Host-pointer, synchronous.  Same contract as layer 1.  det_matmul_i16 is
+ * the int16 GEMM whose every element is the reference int16 dot
+ * (benches/det_matmul_i16.rs:218-224); the reference only has the GEMV. */
+int64_t det_matmul_i8(const int8_t *a, const int8_t *b, int32_t *c, int64_t m, int64_t k, int64_t n);
+int64_t det_matmul_i16(const int16_t *a, const int16_t *b, int32_t *c, int64_t m, int64_t k, int64_t n);
+int64_t det_matmul_q16(const int32_t *a, const int32_t *b, int32_t *c, int64_t m, int64_t k, int64_t n);
+int64_t det_gemv_q16(const int32_t *w, const int32_t *x, int32_t *y, int64_t m, int64_t k);
+/* nb independent queries: x is [nb][k], y is [nb][m]; equals nb calls of
+ * __mind_blas_gemv_q16_mt (the reference takes one query per call). */
+int64_t det_gemv_q16_batched(const int32_t *w, const int32_t *x, int32_t *y, int64_t m, int64_t k, int64_t nb);
+int64_t det_gemv_i16(const int16_t *w, const int16_t *x, int32_t *y, int64_t m, int64_t k);
+
+/* Device-pointer, asynchronous on `stream` (a hipStream_t; NULL = default
+ * stream).  Inputs must stay valid until the stream reaches the call.  The
+ * i16 / q16 forms use a per-device workspace arena owned by the library
+ * (grown with hipMalloc on demand; calls are ordered on it with an event);
+ * det_matmul_ws_dev takes the workspace from the caller instead. */
+int64_t det_matmul_i8_dev(const int8_t *a, const int8_t *b, int32_t *c, int64_t m, int64_t k, int64_t n,
+                          void *stream);
+int64_t det_matmul_i16_dev(const int16_t *a, const int16_t *b, int32_t *c, int64_t m, int64_t k, int64_t n,
+                           void *stream);
+int64_t det_matmul_q16_dev(const int32_t *a, const int32_t *b, int32_t *c, int64_t m, int64_t k, int64_t n,
+                           void *stream);
+int64_t det_gemv_q16_dev(const int32_t *w, const int32_t *x, int32_t *y, int64_t m, int64_t k, int64_t nb,
+                         void *stream);
+int64_t det_gemv_i16_dev(const int16_t *w, const int16_t *x, int32_t *y, int64_t m, int64_t k, void *stream);
+/* Workspace bytes op (DET_OP_*) needs at this shape (0 for int8). */
+int64_t det_workspace_bytes(int64_t op, int64_t m, int64_t k, int64_t n);
+int64_t det_matmul_ws_dev(int64_t op, const void *a, const void *b, int32_t *c, int64_t m, int64_t k, int64_t n,
+                          void *ws, int64_t ws_bytes, void *stream);
+
+/* Runtime helpers (thin wrappers over HIP, so a caller needs no HIP headers). */
+const char *det_last_error(void);
+const char *det_version(void);
+int64_t det_device_count(void);
+int64_t det_set_device(int64_t d);
+/* info[6]: CUs, max engine clock kHz, global memory bytes, LDS bytes per
+ * workgroup, memory clock kHz, memory bus width bits. */
+int64_t det_device_info(int64_t *info, char *name, int64_t name_len);
+int64_t det_malloc(void **p, int64_t bytes);
+int64_t det_free(void *p);
+int64_t det_memcpy_htod(void *dst, const void *src, int64_t bytes);
+int64_t det_memcpy_dtoh(void *dst, const void *src, int64_t bytes);
+int64_t det_memset_dev(void *dst, int64_t byte, int64_t bytes);
+int64_t det_device_sync(void);
+int64_t det_stream_create(void **s);
+int64_t det_stream_destroy(void *s);
+int64_t det_stream_sync(void *s);
+int64_t det_event_create(void **e);
+int64_t det_event_destroy(void *e);
+int64_t det_event_record(void *e, void *s);
+int64_t det_event_elapsed_ms(void *start, void *stop, float *ms);
+
+/* Seeded input generators of the reference bench harness (LCG
+ * benches/det_matmul_q16.rs:196-209; draw A then B). */
+void det_gen_i8(uint64_t seed, int8_t *a, int64_t na, int8_t *b, int64_t nb);
+void det_gen_i16(uint64_t seed, int16_t *a, int64_t na, int16_t *b, int64_t nb);
+void det_gen_q16(uint64_t seed, int shift, int32_t *a, int64_t na, int32_t *b, int64_t nb);
+void det_gen_q16_sat(uint64_t seed, int shift, int32_t *a, int64_t na, int32_t *b, int64_t nb);
+void det_gen_i8_gauss(uint64_t seed, int8_t *x, int64_t n);
+void det_gen_i8_sym127(uint64_t seed, int8_t *w, int64_t n);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* MIND_DET_H */

@@ -1,0 +1,448 @@
+// det_abi.hip -- the extern "C" boundary of libmind_det_hip.so.
+//
+// Three layers, all C-ABI, no torch or HIP types in any signature:
+//  1. The reference's own intrinsic symbols with its i64 "Option C" ABI
+//     (every pointer passed as int64_t, return 0 on success):
+//     __mind_blas_matmul_mm_i8_v, ..._q16_v, gemv, rmajor, dot
+//     (arity table: reference src/type_checker/mod.rs:2266-2332).  They take
+//     HOST pointers, like the reference, and are synchronous: H2D, kernel,
+//     D2H on a library-owned stream, then return.
+//  2. The harness symbols the reference benches / gate dlsym (gemmi8,
+//     gemmqmm, gemmq, mmq, mmi16, gemvq, dotq...: tests/cross_substrate_
+//     identity.rs:70-150, benches/det_*.rs), same ABI.
+//  3. det_*: typed C entry points, host-pointer and device-pointer (_dev,
+//     asynchronous on a caller stream) forms, plus the small runtime the
+//     harness needs (device memory, copies, streams, events, errors).
+//
+// Errors: the reference's kernels never fail and return 0; here a HIP
+// failure or an invalid argument returns a negative code and records a
+// message readable through det_last_error() (thread-local), like the
+// reference's mind_last_error (src/ffi/mod.rs:173).  A NULL pointer or a
+// non-positive size with nothing to compute follows the reference's Track A
+// convention and returns 0 (runtime-support/mind_intrinsics.c:1537-1539).
+#include <cstring>
+#include <mutex>
+#include <string>
+
+#include "det_common.h"
+#include "det_kernels.h"
+#include "../../include/mind_det.h"
+
+namespace {
+
+thread_local std::string g_err;
+
+constexpr int MAX_DEV = 64;
+constexpr int64_t DIM_MAX = 0x7fffffff;
+
+// Per-device state.  `mu` serialises the host-pointer entry points on that
+// device (like the reference's dispatch lock, runtime-support/
+// mind_intrinsics.c:1976) and guards growth of the two device arenas.
+struct DevState {
+    std::mutex mu;
+    hipStream_t stream = nullptr;      // library stream for host-pointer calls
+    void *io = nullptr;                // staging for host-pointer operands
+    size_t io_bytes = 0;
+    void *ws = nullptr;                // limb-GEMM workspace
+    size_t ws_bytes = 0;
+    hipEvent_t ws_free = nullptr;      // recorded after the last workspace user
+};
+DevState g_dev[MAX_DEV];
+
+int64_t set_err(int64_t code, const std::string &msg) {
+    g_err = msg;
+    return code;
+}
+
+int cur_device(int64_t *rc) {
+    int d = 0;
+    hipError_t e = hipGetDevice(&d);
+    if (e != hipSuccess) {
+        *rc = det_fail_hip(e, "hipGetDevice");
+        return -1;
+    }
+    if (d < 0 || d >= MAX_DEV) {
+        *rc = set_err(DET_ERR_DEVICE, "device ordinal out of range");
+        return -1;
+    }
+    return d;
+}
+
+size_t align256(size_t x) { return (x + 255) & ~(size_t)255; }
+
+// Grow-only device buffer.  Growth waits for the device first, so a buffer
+// still read by queued work is never freed underneath it.
+int64_t ensure(void **buf, size_t *have, size_t need) {
+    if (need <= *have) return 0;
+    DET_HIP_CHECK(hipDeviceSynchronize());
+    if (*buf) DET_HIP_CHECK(hipFree(*buf));
+    *buf = nullptr;
+    *have = 0;
+    DET_HIP_CHECK(hipMalloc(buf, need));
+    *have = need;
+    return 0;
+}
+
+int64_t ensure_stream(DevState &d) {
+    if (!d.stream) DET_HIP_CHECK(hipStreamCreateWithFlags(&d.stream, hipStreamNonBlocking));
+    if (!d.ws_free) DET_HIP_CHECK(hipEventCreateWithFlags(&d.ws_free, hipEventDisableTiming));
+    return 0;
+}
+
+bool bad_dims(int64_t m, int64_t k, int64_t n) {
+    return m < 0 || k < 0 || n < 0 || m > DIM_MAX || k > DIM_MAX || n > DIM_MAX;
+}
+
+// Zero an int32 buffer (used for K == 0: the exact sum over no terms).
+__global__ void fill_zero_i32(int32_t *p, size_t n) {
+    const size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i < n) p[i] = 0;
+}
+
+hipError_t zero_i32(int32_t *p, size_t n, hipStream_t s) {
+    if (n == 0) return hipSuccess;
+    hipLaunchKernelGGL(fill_zero_i32, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, s, p, n);
+    return hipGetLastError();
+}
+
+// ---------------------------------------------------------------- device ops
+enum class Op { I8, I16, Q16, Q16_BT };
+
+size_t elem_bytes(Op op) { return op == Op::I8 ? 1 : op == Op::I16 ? 2 : 4; }
+
+// Launch one GEMM on device pointers.  `ws` must hold the limb workspace for
+// I16 / Q16 (ignored for I8).
+int64_t gemm_dev(Op op, const void *A, const void *B, void *C, int64_t m, int64_t k, int64_t n, void *ws,
+                 hipStream_t s) {
+    const int M = (int)m, N = (int)n, K = (int)k;
+    if (K == 0) DET_HIP_CHECK(zero_i32((int32_t *)C, (size_t)m * n, s));
+    else if (op == Op::I8)
+        DET_HIP_CHECK(det::launch_gemm_i8((const int8_t *)A, (const int8_t *)B, (int32_t *)C, M, N, K, s));
+    else if (op == Op::I16)
+        DET_HIP_CHECK(det::launch_gemm_i16((const int16_t *)A, (const int16_t *)B, (int32_t *)C, M, N, K, ws, s));
+    else
+        DET_HIP_CHECK(det::launch_gemm_q16((const int32_t *)A, (const int32_t *)B, (int32_t *)C, M, N, K,
+                                           op == Op::Q16_BT, ws, s));
+    return 0;
+}
+
+size_t ws_need(Op op, int64_t m, int64_t k, int64_t n) {
+    if (op == Op::I8 || k == 0) return 0;
+    return op == Op::I16 ? det::i16_workspace_bytes((int)m, (int)n, (int)k)
+                         : det::q16_workspace_bytes((int)m, (int)n, (int)k);
+}
+
+// Device-pointer GEMM using the library workspace arena (ordered after the
+// arena's previous user through the ws_free event).
+int64_t gemm_dev_arena(Op op, const void *A, const void *B, void *C, int64_t m, int64_t k, int64_t n,
+                       hipStream_t s) {
+    if (bad_dims(m, k, n)) return set_err(DET_ERR_ARG, "dimension out of range [0, 2^31)");
+    if (m == 0 || n == 0) return 0;
+    if (!A || !B || !C) return set_err(DET_ERR_ARG, "null device pointer");
+    const size_t need = ws_need(op, m, k, n);
+    if (need == 0) return gemm_dev(op, A, B, C, m, k, n, nullptr, s);
+    int64_t rc = 0;
+    const int d = cur_device(&rc);
+    if (d < 0) return rc;
+    DevState &ds = g_dev[d];
+    std::lock_guard<std::mutex> lock(ds.mu);
+    if ((rc = ensure_stream(ds))) return rc;
+    if ((rc = ensure(&ds.ws, &ds.ws_bytes, need))) return rc;
+    DET_HIP_CHECK(hipStreamWaitEvent(s, ds.ws_free, 0));
+    if ((rc = gemm_dev(op, A, B, C, m, k, n, ds.ws, s))) return rc;
+    DET_HIP_CHECK(hipEventRecord(ds.ws_free, s));
+    return 0;
+}
+
+// Host-pointer GEMM: stage, launch, copy back, wait.
+int64_t gemm_host(Op op, int64_t a, int64_t b, int64_t c, int64_t m, int64_t k, int64_t n) {
+    if (bad_dims(m, k, n)) return set_err(DET_ERR_ARG, "dimension out of range [0, 2^31)");
+    if (m == 0 || n == 0) return 0;
+    if (!c || ((!a || !b) && k > 0)) return 0;   // Track A: NULL -> 0, nothing written
+    int64_t rc = 0;
+    const int d = cur_device(&rc);
+    if (d < 0) return rc;
+    DevState &ds = g_dev[d];
+    std::lock_guard<std::mutex> lock(ds.mu);
+    if ((rc = ensure_stream(ds))) return rc;
+    const size_t eb = elem_bytes(op);
+    const size_t bytes_a = (size_t)m * k * eb, bytes_b = (size_t)k * n * eb, bytes_c = (size_t)m * n * 4;
+    const size_t off_b = align256(bytes_a), off_c = off_b + align256(bytes_b);
+    if ((rc = ensure(&ds.io, &ds.io_bytes, off_c + align256(bytes_c)))) return rc;
+    if ((rc = ensure(&ds.ws, &ds.ws_bytes, ws_need(op, m, k, n)))) return rc;
+    char *io = (char *)ds.io;
+    hipStream_t s = ds.stream;
+    if (bytes_a) DET_HIP_CHECK(hipMemcpyAsync(io, (const void *)a, bytes_a, hipMemcpyHostToDevice, s));
+    if (bytes_b) DET_HIP_CHECK(hipMemcpyAsync(io + off_b, (const void *)b, bytes_b, hipMemcpyHostToDevice, s));
+    if ((rc = gemm_dev(op, io, io + off_b, io + off_c, m, k, n, ds.ws, s))) return rc;
+    DET_HIP_CHECK(hipMemcpyAsync((void *)c, io + off_c, bytes_c, hipMemcpyDeviceToHost, s));
+    DET_HIP_CHECK(hipStreamSynchronize(s));
+    return 0;
+}
+
+// Host-pointer GEMV family (Q16 batched, int16).
+int64_t gemv_host(bool q16, int64_t w, int64_t x, int64_t y, int64_t m, int64_t k, int64_t nb) {
+    if (bad_dims(m, k, nb)) return set_err(DET_ERR_ARG, "dimension out of range [0, 2^31)");
+    if (m == 0 || nb == 0) return 0;
+    if (!y || ((!w || !x) && k > 0)) return 0;
+    int64_t rc = 0;
+    const int d = cur_device(&rc);
+    if (d < 0) return rc;
+    DevState &ds = g_dev[d];
+    std::lock_guard<std::mutex> lock(ds.mu);
+    if ((rc = ensure_stream(ds))) return rc;
+    const size_t eb = q16 ? 4 : 2;
+    const size_t bytes_w = (size_t)m * k * eb, bytes_x = (size_t)nb * k * eb, bytes_y = (size_t)nb * m * 4;
+    const size_t off_x = align256(bytes_w), off_y = off_x + align256(bytes_x);
+    if ((rc = ensure(&ds.io, &ds.io_bytes, off_y + align256(bytes_y)))) return rc;
+    char *io = (char *)ds.io;
+    hipStream_t s = ds.stream;
+    if (bytes_w) DET_HIP_CHECK(hipMemcpyAsync(io, (const void *)w, bytes_w, hipMemcpyHostToDevice, s));
+    if (bytes_x) DET_HIP_CHECK(hipMemcpyAsync(io + off_x, (const void *)x, bytes_x, hipMemcpyHostToDevice, s));
+    if (k == 0) DET_HIP_CHECK(zero_i32((int32_t *)(io + off_y), (size_t)nb * m, s));
+    else if (q16)
+        DET_HIP_CHECK(det::launch_gemv_q16((const int32_t *)io, (const int32_t *)(io + off_x),
+                                           (int32_t *)(io + off_y), (int)m, (int)k, (int)nb, s));
+    else
+        DET_HIP_CHECK(det::launch_gemv_i16((const int16_t *)io, (const int16_t *)(io + off_x),
+                                           (int32_t *)(io + off_y), (int)m, (int)k, s));
+    DET_HIP_CHECK(hipMemcpyAsync((void *)y, io + off_y, bytes_y, hipMemcpyDeviceToHost, s));
+    DET_HIP_CHECK(hipStreamSynchronize(s));
+    return 0;
+}
+
+}  // namespace
+
+extern "C" int64_t det_fail_hip(hipError_t e, const char *what) {
+    g_err = std::string(what) + ": " + hipGetErrorString(e);
+    return DET_ERR_HIP;
+}
+
+extern "C" int64_t det_fail(int64_t code, const char *msg) { return set_err(code, msg); }
+
+// ====================================================================== layer 1
+extern "C" {
+
+int64_t __mind_blas_matmul_mm_i8_v(int64_t a, int64_t b, int64_t c, int64_t m, int64_t k, int64_t n) {
+    return gemm_host(Op::I8, a, b, c, m, k, n);
+}
+int64_t __mind_blas_matmul_mm_i8_mt_v(int64_t a, int64_t b, int64_t c, int64_t m, int64_t k, int64_t n) {
+    return gemm_host(Op::I8, a, b, c, m, k, n);
+}
+int64_t __mind_blas_matmul_mm_q16_v(int64_t a, int64_t b, int64_t c, int64_t m, int64_t k, int64_t n) {
+    return gemm_host(Op::Q16, a, b, c, m, k, n);
+}
+int64_t __mind_blas_matmul_mm_q16_mt_v(int64_t a, int64_t b, int64_t c, int64_t m, int64_t k, int64_t n) {
+    return gemm_host(Op::Q16, a, b, c, m, k, n);
+}
+int64_t __mind_blas_gemv_q16_mt(int64_t w, int64_t x, int64_t y, int64_t m, int64_t k) {
+    return gemv_host(true, w, x, y, m, k, 1);
+}
+int64_t __mind_blas_matmul_rmajor_q16_v(int64_t w, int64_t x, int64_t y, int64_t rows, int64_t cols) {
+    return gemv_host(true, w, x, y, rows, cols, 1);
+}
+int64_t __mind_blas_matmul_rmajor_i16_v(int64_t w, int64_t x, int64_t y, int64_t rows, int64_t cols) {
+    return gemv_host(false, w, x, y, rows, cols, 1);
+}
+int64_t __mind_blas_dot_q16(int64_t a, int64_t b, int64_t len) {
+    if (len <= 0 || !a || !b) return 0;
+    int32_t out = 0;
+    if (gemv_host(true, a, b, (int64_t)(intptr_t)&out, 1, len, 1) != 0) return 0;
+    return (int64_t)out;
+}
+int64_t __mind_blas_dot_q16_v(int64_t a, int64_t b, int64_t len) { return __mind_blas_dot_q16(a, b, len); }
+
+// ====================================================================== layer 2
+int64_t gemmi8(int64_t a, int64_t b, int64_t c, int64_t m, int64_t k, int64_t n) {
+    return __mind_blas_matmul_mm_i8_v(a, b, c, m, k, n);
+}
+int64_t gemmi8mt(int64_t a, int64_t b, int64_t c, int64_t m, int64_t k, int64_t n) {
+    return __mind_blas_matmul_mm_i8_mt_v(a, b, c, m, k, n);
+}
+int64_t gemmqmm(int64_t a, int64_t b, int64_t c, int64_t m, int64_t k, int64_t n) {
+    return __mind_blas_matmul_mm_q16_v(a, b, c, m, k, n);
+}
+int64_t gemmq(int64_t a, int64_t bt, int64_t c, int64_t m, int64_t k, int64_t n) {
+    return gemm_host(Op::Q16_BT, a, bt, c, m, k, n);
+}
+int64_t mmq(int64_t w, int64_t x, int64_t y, int64_t rows, int64_t cols) {
+    return __mind_blas_matmul_rmajor_q16_v(w, x, y, rows, cols);
+}
+int64_t mmi16(int64_t w, int64_t x, int64_t y, int64_t rows, int64_t cols) {
+    return __mind_blas_matmul_rmajor_i16_v(w, x, y, rows, cols);
+}
+int64_t gemvq(int64_t catalog, int64_t query, int64_t scores, int64_t m, int64_t k) {
+    return __mind_blas_gemv_q16_mt(catalog, query, scores, m, k);
+}
+int64_t dotq(int64_t a, int64_t b, int64_t n) { return __mind_blas_dot_q16_v(a, b, n); }
+
+// ====================================================================== layer 3
+int64_t det_matmul_i8(const int8_t *a, const int8_t *b, int32_t *c, int64_t m, int64_t k, int64_t n) {
+    return gemm_host(Op::I8, (int64_t)a, (int64_t)b, (int64_t)c, m, k, n);
+}
+int64_t det_matmul_i16(const int16_t *a, const int16_t *b, int32_t *c, int64_t m, int64_t k, int64_t n) {
+    return gemm_host(Op::I16, (int64_t)a, (int64_t)b, (int64_t)c, m, k, n);
+}
+int64_t det_matmul_q16(const int32_t *a, const int32_t *b, int32_t *c, int64_t m, int64_t k, int64_t n) {
+    return gemm_host(Op::Q16, (int64_t)a, (int64_t)b, (int64_t)c, m, k, n);
+}
+int64_t det_gemv_q16(const int32_t *w, const int32_t *x, int32_t *y, int64_t m, int64_t k) {
+    return gemv_host(true, (int64_t)w, (int64_t)x, (int64_t)y, m, k, 1);
+}
+int64_t det_gemv_q16_batched(const int32_t *w, const int32_t *x, int32_t *y, int64_t m, int64_t k, int64_t nb) {
+    return gemv_host(true, (int64_t)w, (int64_t)x, (int64_t)y, m, k, nb);
+}
+int64_t det_gemv_i16(const int16_t *w, const int16_t *x, int32_t *y, int64_t m, int64_t k) {
+    return gemv_host(false, (int64_t)w, (int64_t)x, (int64_t)y, m, k, 1);
+}
+
+int64_t det_matmul_i8_dev(const int8_t *a, const int8_t *b, int32_t *c, int64_t m, int64_t k, int64_t n,
+                          void *stream) {
+    return gemm_dev_arena(Op::I8, a, b, c, m, k, n, (hipStream_t)stream);
+}
+int64_t det_matmul_i16_dev(const int16_t *a, const int16_t *b, int32_t *c, int64_t m, int64_t k, int64_t n,
+                           void *stream) {
+    return gemm_dev_arena(Op::I16, a, b, c, m, k, n, (hipStream_t)stream);
+}
+int64_t det_matmul_q16_dev(const int32_t *a, const int32_t *b, int32_t *c, int64_t m, int64_t k, int64_t n,
+                           void *stream) {
+    return gemm_dev_arena(Op::Q16, a, b, c, m, k, n, (hipStream_t)stream);
+}
+
+int64_t det_workspace_bytes(int64_t op, int64_t m, int64_t k, int64_t n) {
+    if (bad_dims(m, k, n) || m == 0 || n == 0) return 0;
+    if (op == DET_OP_I16) return (int64_t)ws_need(Op::I16, m, k, n);
+    if (op == DET_OP_Q16) return (int64_t)ws_need(Op::Q16, m, k, n);
+    return 0;
+}
+
+int64_t det_matmul_ws_dev(int64_t op, const void *a, const void *b, int32_t *c, int64_t m, int64_t k, int64_t n,
+                          void *ws, int64_t ws_bytes, void *stream) {
+    if (bad_dims(m, k, n)) return set_err(DET_ERR_ARG, "dimension out of range [0, 2^31)");
+    if (m == 0 || n == 0) return 0;
+    if (!a || !b || !c) return set_err(DET_ERR_ARG, "null device pointer");
+    Op o;
+    if (op == DET_OP_I8) o = Op::I8;
+    else if (op == DET_OP_I16) o = Op::I16;
+    else if (op == DET_OP_Q16) o = Op::Q16;
+    else return set_err(DET_ERR_ARG, "unknown op");
+    if (ws_bytes < 0 || (size_t)ws_bytes < ws_need(o, m, k, n) || (ws_need(o, m, k, n) && !ws))
+        return set_err(DET_ERR_ARG, "workspace too small (see det_workspace_bytes)");
+    return gemm_dev(o, a, b, c, m, k, n, ws, (hipStream_t)stream);
+}
+
+int64_t det_gemv_q16_dev(const int32_t *w, const int32_t *x, int32_t *y, int64_t m, int64_t k, int64_t nb,
+                         void *stream) {
+    if (bad_dims(m, k, nb)) return set_err(DET_ERR_ARG, "dimension out of range [0, 2^31)");
+    if (m == 0 || nb == 0) return 0;
+    if (!y || ((!w || !x) && k > 0)) return set_err(DET_ERR_ARG, "null device pointer");
+    hipStream_t s = (hipStream_t)stream;
+    if (k == 0) DET_HIP_CHECK(zero_i32(y, (size_t)m * nb, s));
+    else DET_HIP_CHECK(det::launch_gemv_q16(w, x, y, (int)m, (int)k, (int)nb, s));
+    return 0;
+}
+
+int64_t det_gemv_i16_dev(const int16_t *w, const int16_t *x, int32_t *y, int64_t m, int64_t k, void *stream) {
+    if (bad_dims(m, k, 1)) return set_err(DET_ERR_ARG, "dimension out of range [0, 2^31)");
+    if (m == 0) return 0;
+    if (!y || ((!w || !x) && k > 0)) return set_err(DET_ERR_ARG, "null device pointer");
+    hipStream_t s = (hipStream_t)stream;
+    if (k == 0) DET_HIP_CHECK(zero_i32(y, (size_t)m, s));
+    else DET_HIP_CHECK(det::launch_gemv_i16(w, x, y, (int)m, (int)k, s));
+    return 0;
+}
+
+// ---------------------------------------------------------------- runtime
+const char *det_last_error(void) { return g_err.c_str(); }
+const char *det_version(void) { return "mind-det-mi355x 0.1 (gfx950)"; }
+
+int64_t det_device_count(void) {
+    int n = 0;
+    DET_HIP_CHECK(hipGetDeviceCount(&n));
+    return n;
+}
+int64_t det_set_device(int64_t d) {
+    DET_HIP_CHECK(hipSetDevice((int)d));
+    return 0;
+}
+// info: [0]=CU count [1]=max engine clock kHz [2]=global memory bytes
+// [3]=LDS bytes per workgroup [4]=memory clock kHz [5]=memory bus width bits
+int64_t det_device_info(int64_t *info, char *name, int64_t name_len) {
+    int d = 0;
+    DET_HIP_CHECK(hipGetDevice(&d));
+    hipDeviceProp_t p;
+    DET_HIP_CHECK(hipGetDeviceProperties(&p, d));
+    if (info) {
+        info[0] = p.multiProcessorCount;
+        info[1] = p.clockRate;
+        info[2] = (int64_t)p.totalGlobalMem;
+        info[3] = (int64_t)p.sharedMemPerBlock;
+        info[4] = p.memoryClockRate;
+        info[5] = p.memoryBusWidth;
+    }
+    if (name && name_len > 0) {
+        std::string s = std::string(p.name) + " " + p.gcnArchName;
+        size_t l = s.size() < (size_t)name_len - 1 ? s.size() : (size_t)name_len - 1;
+        memcpy(name, s.data(), l);
+        name[l] = 0;
+    }
+    return 0;
+}
+int64_t det_malloc(void **p, int64_t bytes) {
+    if (!p || bytes < 0) return set_err(DET_ERR_ARG, "bad det_malloc arguments");
+    *p = nullptr;
+    if (bytes == 0) return 0;
+    DET_HIP_CHECK(hipMalloc(p, (size_t)bytes));
+    return 0;
+}
+int64_t det_free(void *p) {
+    if (p) DET_HIP_CHECK(hipFree(p));
+    return 0;
+}
+int64_t det_memcpy_htod(void *dst, const void *src, int64_t bytes) {
+    if (bytes > 0) DET_HIP_CHECK(hipMemcpy(dst, src, (size_t)bytes, hipMemcpyHostToDevice));
+    return 0;
+}
+int64_t det_memcpy_dtoh(void *dst, const void *src, int64_t bytes) {
+    if (bytes > 0) DET_HIP_CHECK(hipMemcpy(dst, src, (size_t)bytes, hipMemcpyDeviceToHost));
+    return 0;
+}
+int64_t det_memset_dev(void *dst, int64_t byte, int64_t bytes) {
+    if (bytes > 0) DET_HIP_CHECK(hipMemset(dst, (int)byte, (size_t)bytes));
+    return 0;
+}
+int64_t det_device_sync(void) {
+    DET_HIP_CHECK(hipDeviceSynchronize());
+    return 0;
+}
+int64_t det_stream_create(void **s) {
+    DET_HIP_CHECK(hipStreamCreateWithFlags((hipStream_t *)s, hipStreamNonBlocking));
+    return 0;
+}
+int64_t det_stream_destroy(void *s) {
+    if (s) DET_HIP_CHECK(hipStreamDestroy((hipStream_t)s));
+    return 0;
+}
+int64_t det_stream_sync(void *s) {
+    DET_HIP_CHECK(hipStreamSynchronize((hipStream_t)s));
+    return 0;
+}
+int64_t det_event_create(void **e) {
+    DET_HIP_CHECK(hipEventCreate((hipEvent_t *)e));
+    return 0;
+}
+int64_t det_event_destroy(void *e) {
+    if (e) DET_HIP_CHECK(hipEventDestroy((hipEvent_t)e));
+    return 0;
+}
+int64_t det_event_record(void *e, void *s) {
+    DET_HIP_CHECK(hipEventRecord((hipEvent_t)e, (hipStream_t)s));
+    return 0;
+}
+int64_t det_event_elapsed_ms(void *start, void *stop, float *ms) {
+    DET_HIP_CHECK(hipEventSynchronize((hipEvent_t)stop));
+    DET_HIP_CHECK(hipEventElapsedTime(ms, (hipEvent_t)start, (hipEvent_t)stop));
+    return 0;
+}
+
+}  // extern "C"

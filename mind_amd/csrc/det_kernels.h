@@ -1,0 +1,33 @@
+// det_kernels.h -- kernel launchers shared between the kernel files and the
+// C-ABI layer.  All pointers are device pointers; every launcher is
+// asynchronous on `s` and returns the launch status.  Shapes must already be
+// validated (0 < M, N; 0 <= K; all below 2^31).
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stddef.h>
+#include <stdint.h>
+
+namespace det {
+
+// C[M,N] (i32) = A[M,K] (i8) * B[K,N] (i8)
+hipError_t launch_gemm_i8(const int8_t *A, const int8_t *B, int32_t *C, int M, int N, int K, hipStream_t s);
+
+// Workspace (device bytes) the limb GEMMs need: operand limb planes, low-16
+// halves (Q16) and exact row / column sums.
+size_t limb_workspace_bytes(int M, int N, int K, int np, bool q16);
+inline size_t q16_workspace_bytes(int M, int N, int K) { return limb_workspace_bytes(M, N, K, 4, true); }
+inline size_t i16_workspace_bytes(int M, int N, int K) { return limb_workspace_bytes(M, N, K, 2, false); }
+
+// Q16.16: B is [K][N], or [N][K] when b_is_t.
+hipError_t launch_gemm_q16(const int32_t *A, const int32_t *B, int32_t *C, int M, int N, int K, bool b_is_t,
+                           void *ws, hipStream_t s);
+hipError_t launch_gemm_i16(const int16_t *A, const int16_t *B, int32_t *C, int M, int N, int K, void *ws,
+                           hipStream_t s);
+
+// Y[nb][M] = Q16 GEMV of W[M][K] with each X[b][K].
+hipError_t launch_gemv_q16(const int32_t *W, const int32_t *X, int32_t *Y, int M, int K, int nb, hipStream_t s);
+// y[M] = int16 GEMV.
+hipError_t launch_gemv_i16(const int16_t *W, const int16_t *x, int32_t *y, int M, int K, hipStream_t s);
+
+}  // namespace det

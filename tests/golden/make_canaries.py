@@ -1,0 +1,58 @@
+"""Write tests/golden/canaries.json from the reference's committed golden data.
+
+Run in the build container only (it reads /root/reference, which the GPU box
+does not have).  It copies DATA, not code: for each hot-path workload the
+generator/seed/shape fields of tests/cross_substrate_identity/<id>/manifest.toml
+and the avx2 / neon SHA-256 lines of reference_hashes.toml, plus the four
+expected digest words embedded in bench/matmul_det_bench.mind:98-101.
+"""
+import json
+import os
+import re
+import sys
+
+REF = os.environ.get("MIND_REF", "/root/reference")
+IDS = [
+    "gemm-i8-64x64x64", "gemm-i8-mt-64x64x64", "gemm-i8-vnni-64x64x64",
+    "gemm-q16-64x64x64", "gemm-q16-fused-64x64x64",
+    "gemv-q16-256x256", "gemv-i16-256x256",
+    "dot-i16-4096", "dot-l2-q16",
+]
+
+
+def kv(text):
+    out = {}
+    for line in text.splitlines():
+        line = line.split("#", 1)[0].strip()
+        m = re.match(r"^([A-Za-z_0-9]+)\s*=\s*(.+)$", line)
+        if m:
+            v = m.group(2).strip()
+            out[m.group(1)] = v.strip('"') if v.startswith('"') else int(v) if v.isdigit() else v
+    return out
+
+
+def main():
+    base = os.path.join(REF, "tests", "cross_substrate_identity")
+    res = {"source": "star-ga/mind v0.10.2 tests/cross_substrate_identity/*/{manifest,reference_hashes}.toml",
+           "workloads": {}}
+    for wid in IDS:
+        man = kv(open(os.path.join(base, wid, "manifest.toml")).read())
+        hashes = kv(open(os.path.join(base, wid, "reference_hashes.toml")).read())
+        keep = {k: man[k] for k in ("seed", "m", "k", "n", "rows", "cols", "length", "dtype", "symbol",
+                                    "output_encoding") if k in man}
+        keep["avx2"] = hashes["avx2"]
+        keep["neon"] = hashes["neon"]
+        res["workloads"][wid] = keep
+    src = open(os.path.join(REF, "bench", "matmul_det_bench.mind")).read()
+    words = [int(x) for x in re.findall(r"let e[0-3]: i64 = (-?\d+);", src)]
+    assert len(words) == 4, words
+    res["matmul_det_bench_256"] = {"source": "bench/matmul_det_bench.mind:98-101",
+                                   "fill_a": "((i+1)%7)-3", "fill_b": "((i+2)%7)-3", "n": 256,
+                                   "digest_words_le_i64": words}
+    out = os.path.join(os.path.dirname(os.path.abspath(__file__)), "canaries.json")
+    json.dump(res, open(out, "w"), indent=1)
+    print("wrote", out)
+
+
+if __name__ == "__main__":
+    sys.exit(main())

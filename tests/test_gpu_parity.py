@@ -1,0 +1,352 @@
+"""GPU tier: the HIP kernels, called through the C ABI, are bit-identical to
+the oracle (and to the reference's committed golden hashes).
+
+Sizes: small and ragged shapes against the full oracle; BASELINE-size
+configs against oracle rows sampled across the output (plus repeat
+stability), so the oracle work stays within seconds.
+"""
+import ctypes
+import json
+import os
+import sys
+
+import numpy as np
+import pytest
+
+import mind_amd as M
+import oracle as O
+
+pytestmark = pytest.mark.gpu
+
+GOLD = os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden")
+
+
+def note(msg):
+    print(f"[gpu-case] {msg}", file=sys.stderr, flush=True)
+
+
+def h32(v):
+    return O.sha256_i32_le(v)
+
+
+def addr(a):
+    return a.ctypes.data
+
+
+def call6(name, a, b, c, m, k, n):
+    note(f"{name} m={m} k={k} n={n}")
+    rc = getattr(M.lib(), name)(addr(a), addr(b), addr(c), m, k, n)
+    assert rc == 0, (rc, M.last_error())
+
+
+def call5(name, w, x, y, r, c):
+    note(f"{name} rows={r} cols={c}")
+    rc = getattr(M.lib(), name)(addr(w), addr(x), addr(y), r, c)
+    assert rc == 0, (rc, M.last_error())
+
+
+# ------------------------------------------------------------------ golden canaries through the ABI
+
+@pytest.mark.parametrize("sym", ["gemmi8", "gemmi8mt", "__mind_blas_matmul_mm_i8_v", "__mind_blas_matmul_mm_i8_mt_v"])
+def test_canary_gemm_i8(canaries, sym):
+    w = canaries["workloads"]["gemm-i8-64x64x64"]
+    a, b = O.gen_i8(w["seed"], 64 * 64, 64 * 64)
+    c = np.full(64 * 64, 0x5A5A5A5A, np.int32)
+    call6(sym, a, b, c, 64, 64, 64)
+    assert h32(c) == w["avx2"]
+
+
+@pytest.mark.parametrize("sym", ["gemmqmm", "__mind_blas_matmul_mm_q16_v", "__mind_blas_matmul_mm_q16_mt_v", "gemmq"])
+def test_canary_gemm_q16(canaries, sym):
+    w = canaries["workloads"]["gemm-q16-fused-64x64x64"]
+    a, b = O.gen_q16(w["seed"], 64 * 64, 64 * 64)
+    if sym == "gemmq":   # the gemv-composed form takes B^T [N][K]
+        b = np.ascontiguousarray(b.reshape(64, 64).T).ravel()
+    c = np.zeros(64 * 64, np.int32)
+    call6(sym, a, b, c, 64, 64, 64)
+    assert h32(c) == w["avx2"]
+
+
+@pytest.mark.parametrize("sym", ["mmq", "__mind_blas_matmul_rmajor_q16_v", "gemvq", "__mind_blas_gemv_q16_mt"])
+def test_canary_gemv_q16(canaries, sym):
+    w = canaries["workloads"]["gemv-q16-256x256"]
+    W, x = O.gen_q16(w["seed"], 256 * 256, 256)
+    y = np.zeros(256, np.int32)
+    call5(sym, W, x, y, 256, 256)
+    assert h32(y) == w["avx2"]
+
+
+@pytest.mark.parametrize("sym", ["mmi16", "__mind_blas_matmul_rmajor_i16_v"])
+def test_canary_gemv_i16(canaries, sym):
+    w = canaries["workloads"]["gemv-i16-256x256"]
+    W, x = O.gen_i16(w["seed"], 256 * 256, 256)
+    y = np.zeros(256, np.int32)
+    call5(sym, W, x, y, 256, 256)
+    assert h32(y) == w["avx2"]
+
+
+def test_canary_dot_l2_q16(canaries):
+    w = canaries["workloads"]["dot-l2-q16"]
+    a, b = O.gen_q16(w["seed"], w["length"], w["length"])
+    note("dotq len=65536")
+    assert O.sha256_i64_le(M.lib().dotq(addr(a), addr(b), len(a))) == w["avx2"]
+
+
+def test_canary_matmul_det_bench(canaries):
+    g = canaries["matmul_det_bench_256"]
+    idx = np.arange(256 * 256)
+    A = (((idx + 1) % 7) - 3).astype(np.int8)
+    B = (((idx + 2) % 7) - 3).astype(np.int8)
+    C = np.zeros(256 * 256, np.int32)
+    call6("gemmi8", A, B, C, 256, 256, 256)
+    import hashlib
+    d = hashlib.sha256(C.astype("<i4").tobytes()).digest()
+    assert [int.from_bytes(d[i:i + 8], "little", signed=True) for i in range(0, 32, 8)] == g["digest_words_le_i64"]
+
+
+def test_dot_q16_reference_vectors():
+    d = json.load(open(os.path.join(GOLD, "dot_q16_ref.json")))
+    ext = np.array([2147483647, -2147483647, -2147483648, 65535, -65536, 1, -1, 0], np.int32)
+    for c in d["cases"]:
+        if c["family"] == "extreme":
+            ia, ib = O.gen_q16(c["seed"], c["len"], c["len"], shift=29)
+            a, b = ext[ia & 7], ext[ib & 7]
+        else:
+            a, b = O.gen_q16(c["seed"], c["len"], c["len"], shift={"ref12": 12, "q4": 13, "full": 0}[c["family"]])
+        note(f"dot_q16 family={c['family']} len={c['len']}")
+        assert M.dot_q16(a, b) == c["scalar"], c
+
+
+# ------------------------------------------------------------------ int8 shapes
+
+I8_SHAPES = [(1, 1, 1), (1, 64, 1), (3, 5, 7), (16, 16, 16), (17, 33, 65), (64, 64, 64), (255, 257, 129),
+             (256, 256, 256), (300, 1000, 77), (513, 96, 260), (100, 4096, 8), (8, 4096, 300), (1000, 17, 999)]
+
+
+@pytest.mark.parametrize("m,k,n", I8_SHAPES, ids=[f"{m}x{k}x{n}" for m, k, n in I8_SHAPES])
+def test_gemm_i8_shapes(m, k, n):
+    a, b = O.gen_i8(0xDEADBEEF00000000 ^ (m * 1000003 + k * 1009 + n), m * k, k * n)
+    note(f"det_matmul_i8 {m}x{k}x{n}")
+    got = M.det_matmul_i8(a.reshape(m, k), b.reshape(k, n))
+    np.testing.assert_array_equal(got, O.gemm_i8(a, b, m, k, n))
+
+
+def test_gemm_i8_k_zero_and_empty():
+    note("det_matmul_i8 k=0")
+    np.testing.assert_array_equal(M.det_matmul_i8(np.zeros((5, 0), np.int8), np.zeros((0, 7), np.int8)),
+                                  np.zeros((5, 7), np.int32))
+    c = np.full(4, 7, np.int32)
+    assert M.lib().gemmi8(0, 0, addr(c), 0, 4, 4) == 0 and (c == 7).all()
+
+
+def test_gemm_i8_wraps_mod_2_32():
+    k = 131136                                   # k * 128 * 128 > 2^31
+    a = np.full((16, k), -128, np.int8)
+    b = np.full((k, 16), -128, np.int8)
+    a[1, :] = 127
+    note(f"det_matmul_i8 wrap 16x{k}x16")
+    got = M.det_matmul_i8(a, b)
+    np.testing.assert_array_equal(got, O.gemm_i8(a.ravel(), b.ravel(), 16, k, 16))
+    assert got[0, 0] == np.int32(np.uint32((k * 16384) % (1 << 32)).astype(np.int32))
+
+
+# ------------------------------------------------------------------ Q16 / i16 shapes
+
+Q_SHAPES = [(1, 1, 1), (3, 5, 7), (64, 64, 64), (65, 63, 66), (128, 300, 96), (200, 129, 33), (7, 1000, 130)]
+
+
+@pytest.mark.parametrize("shift", [12, 13, 0])
+@pytest.mark.parametrize("m,k,n", Q_SHAPES, ids=[f"{m}x{k}x{n}" for m, k, n in Q_SHAPES])
+def test_gemm_q16_shapes(m, k, n, shift):
+    a, b = O.gen_q16(0xDEADBEEF00000000 ^ (m * 7919 + k * 31 + n) ^ shift, m * k, k * n, shift=shift)
+    note(f"det_matmul_q16 {m}x{k}x{n} shift={shift}")
+    got = M.det_matmul_q16(a.reshape(m, k), b.reshape(k, n))
+    np.testing.assert_array_equal(got, O.gemm_q16(a, b, m, k, n))
+
+
+def test_gemm_q16_saturating_config_and_bt():
+    m, k, n = 96, 257, 80
+    a, b = O.gen_q16_sat(0x9A7, m * k, k * n, shift=13)
+    want = O.gemm_q16(a, b, m, k, n)
+    note("det_matmul_q16 sat 96x257x80")
+    np.testing.assert_array_equal(M.det_matmul_q16(a.reshape(m, k), b.reshape(k, n)), want)
+    bt = np.ascontiguousarray(b.reshape(k, n).T)
+    c = np.zeros(m * n, np.int32)
+    call6("gemmq", a, bt, c, m, k, n)
+    np.testing.assert_array_equal(c.reshape(m, n), want)
+
+
+def test_gemm_q16_long_k_flush():
+    # K > 16384 crosses the exact int64 flush of the low limb sets
+    m, k, n = 16, 40000, 24
+    a, b = O.gen_q16(0xF1A5, m * k, k * n, shift=0)
+    note(f"det_matmul_q16 long-k {m}x{k}x{n}")
+    np.testing.assert_array_equal(M.det_matmul_q16(a.reshape(m, k), b.reshape(k, n)), O.gemm_q16(a, b, m, k, n))
+
+
+I16_SHAPES = [(1, 1, 1), (3, 5, 7), (64, 64, 64), (65, 127, 66), (200, 300, 100), (33, 2048, 17)]
+
+
+@pytest.mark.parametrize("m,k,n", I16_SHAPES, ids=[f"{m}x{k}x{n}" for m, k, n in I16_SHAPES])
+def test_gemm_i16_shapes(m, k, n):
+    a, b = O.gen_i16(0xDEADBEEF00000000 ^ (m * 131 + k * 17 + n), m * k, k * n)
+    note(f"det_matmul_i16 {m}x{k}x{n}")
+    np.testing.assert_array_equal(M.det_matmul_i16(a.reshape(m, k), b.reshape(k, n)), O.gemm_i16(a, b, m, k, n))
+
+
+def test_gemm_i16_extremes():
+    m, k, n = 8, 70000, 8
+    a = np.full((m, k), -32768, np.int16)
+    b = np.full((k, n), -32768, np.int16)
+    a[1] = 32767
+    b[:, 2] = 32767
+    note("det_matmul_i16 extremes 8x70000x8")
+    np.testing.assert_array_equal(M.det_matmul_i16(a, b), O.gemm_i16(a.ravel(), b.ravel(), m, k, n))
+
+
+# ------------------------------------------------------------------ GEMV
+
+GEMV_SHAPES = [(1, 1), (5, 3), (64, 64), (512, 130), (128, 96), (256, 1027), (1000, 4096), (11922, 384)]
+
+
+@pytest.mark.parametrize("nb", [1, 2, 3, 8, 9])
+@pytest.mark.parametrize("m,k", GEMV_SHAPES, ids=[f"{m}x{k}" for m, k in GEMV_SHAPES])
+def test_gemv_q16_shapes(m, k, nb):
+    W, X = O.gen_q16(0xDEADBEEF00000000 ^ ((m << 20) ^ k) ^ nb, m * k, nb * k)
+    note(f"det_gemv_q16_batched {m}x{k} nb={nb}")
+    got = M.det_gemv_q16(W.reshape(m, k), X.reshape(nb, k))
+    np.testing.assert_array_equal(got, O.gemv_q16_batched(W, X, m, k, nb))
+
+
+@pytest.mark.parametrize("m,k", [(1, 1), (7, 9), (256, 256), (300, 1001), (4096, 4096)])
+def test_gemv_i16_shapes(m, k):
+    W, x = O.gen_i16(0xDEADBEEF ^ (m * 3 + k), m * k, k)
+    note(f"det_gemv_i16 {m}x{k}")
+    np.testing.assert_array_equal(M.det_gemv_i16(W.reshape(m, k), x), O.gemv_i16(W, x, m, k))
+
+
+# ------------------------------------------------------------------ device-pointer API
+
+def test_dev_api_poisoned_outputs_and_run_to_run():
+    m, k, n = 320, 448, 192
+    a, b = O.gen_i8(0xD0D0, m * k, k * n)
+    want = O.gemm_i8(a, b, m, k, n)
+    da, db = M.DeviceBuffer.from_array(a), M.DeviceBuffer.from_array(b)
+    dc = M.DeviceBuffer(m * n * 4)
+    s = M.Stream()
+    for rep in range(16):
+        dc.fill(0xA5)
+        note(f"det_matmul_i8_dev rep={rep}")
+        M.check(M.lib().det_matmul_i8_dev(da.ptr, db.ptr, dc.ptr, m, k, n, s.ptr))
+        s.sync()
+        np.testing.assert_array_equal(dc.to_array(np.int32, (m, n)), want)
+    aq, bq = O.gen_q16_sat(0xD0D1, m * k, k * n)
+    wq = O.gemm_q16(aq, bq, m, k, n)
+    daq, dbq = M.DeviceBuffer.from_array(aq), M.DeviceBuffer.from_array(bq)
+    ws_bytes = M.lib().det_workspace_bytes(M.DET_OP_Q16, m, k, n)
+    ws = M.DeviceBuffer(ws_bytes)
+    for rep in range(4):
+        dc.fill(0xA5)
+        note(f"det_matmul_q16_dev rep={rep}")
+        M.check(M.lib().det_matmul_q16_dev(daq.ptr, dbq.ptr, dc.ptr, m, k, n, s.ptr))
+        s.sync()
+        np.testing.assert_array_equal(dc.to_array(np.int32, (m, n)), wq)
+        dc.fill(0xA5)
+        note(f"det_matmul_ws_dev q16 rep={rep}")
+        M.check(M.lib().det_matmul_ws_dev(M.DET_OP_Q16, daq.ptr, dbq.ptr, dc.ptr, m, k, n, ws.ptr, ws_bytes, s.ptr))
+        s.sync()
+        np.testing.assert_array_equal(dc.to_array(np.int32, (m, n)), wq)
+    # a too-small workspace is rejected before any launch
+    assert M.lib().det_matmul_ws_dev(M.DET_OP_Q16, daq.ptr, dbq.ptr, dc.ptr, m, k, n, ws.ptr, 16, s.ptr) < 0
+    assert "workspace" in M.last_error()
+    s.destroy()
+
+
+def test_invalid_shapes_are_rejected_before_launch():
+    c = np.zeros(4, np.int32)
+    a = np.zeros(4, np.int8)
+    note("invalid shapes")
+    assert M.lib().gemmi8(addr(a), addr(a), addr(c), -1, 2, 2) < 0
+    assert "dimension" in M.last_error()
+    assert M.lib().det_matmul_i8(addr(a), addr(a), addr(c), 1 << 40, 1, 1) < 0
+
+
+# ------------------------------------------------------------------ BASELINE-size configs
+
+def _sample_rows(m, count=6):
+    rng = np.random.default_rng(m)
+    rows = sorted(set([0, m - 1] + list(rng.integers(0, m, count))))
+    return np.array(rows, np.int64)
+
+
+def _dev_run(fn, inputs, out_shape, reps=2):
+    """Run on device buffers; poison the output each time; all reps must agree."""
+    bufs = [M.DeviceBuffer.from_array(x) for x in inputs]
+    out = M.DeviceBuffer(int(np.prod(out_shape)) * 4)
+    s = M.Stream()
+    res = None
+    for rep in range(reps):
+        out.fill(0xA5)
+        M.check(fn(*[b.ptr for b in bufs], out.ptr, s.ptr))
+        s.sync()
+        got = out.to_array(np.int32, out_shape)
+        if res is None:
+            res = got
+        else:
+            np.testing.assert_array_equal(got, res)
+    s.destroy()
+    for b in bufs + [out]:
+        b.free()
+    return res
+
+
+def test_config_int8_4096_cubed():
+    m = k = n = 4096
+    a, b = M.gen_i8(0xDEADBEEF ^ 0x4096, m * k, k * n)
+    note("det_matmul_i8_dev 4096^3")
+    C = _dev_run(lambda pa, pb, pc, s: M.lib().det_matmul_i8_dev(pa, pb, pc, m, k, n, s), [a, b], (m, n))
+    rows = _sample_rows(m)
+    np.testing.assert_array_equal(C[rows], O.gemm_i8_rows(a, b, m, k, n, rows))
+    cols = _sample_rows(n)
+    Bc = np.ascontiguousarray(b.reshape(k, n)[:, cols]).ravel()
+    np.testing.assert_array_equal(C[:, cols], O.gemm_i8(a, Bc, m, k, len(cols)))
+
+
+def test_config_int8_mlp_4096x4096x11008():
+    m, k, n = 4096, 4096, 11008
+    x = M.gen_i8_gauss(0xDEADBEEF ^ 0x3117, m * k)
+    w = M.gen_i8_sym127(0xDEADBEEF ^ 0x3118, k * n)
+    note("det_matmul_i8_dev mlp 4096x4096x11008")
+    C = _dev_run(lambda pa, pb, pc, s: M.lib().det_matmul_i8_dev(pa, pb, pc, m, k, n, s), [x, w], (m, n))
+    rows = _sample_rows(m, 4)
+    np.testing.assert_array_equal(C[rows], O.gemm_i8_rows(x, w, m, k, n, rows))
+
+
+def test_config_q16_1024_cubed():
+    m = k = n = 1024
+    a, b = M.gen_q16_sat(0xDEADBEEF ^ 0x1016, m * k, k * n, 13)
+    note("det_matmul_q16_dev 1024^3 (saturating config)")
+    C = _dev_run(lambda pa, pb, pc, s: M.lib().det_matmul_q16_dev(pa, pb, pc, m, k, n, s), [a, b], (m, n))
+    np.testing.assert_array_equal(C, O.gemm_q16(a, b, m, k, n))
+
+
+def test_config_i16_2048_cubed():
+    m = k = n = 2048
+    a, b = M.gen_i16(0xDEADBEEF ^ 0x2016, m * k, k * n)
+    note("det_matmul_i16_dev 2048^3")
+    C = _dev_run(lambda pa, pb, pc, s: M.lib().det_matmul_i16_dev(pa, pb, pc, m, k, n, s), [a, b], (m, n))
+    rows = _sample_rows(m)
+    np.testing.assert_array_equal(C[rows], O.gemm_i16_rows(a, b, m, k, n, rows))
+
+
+@pytest.mark.parametrize("nb", [1, 8])
+def test_config_gemv_q16_16384(nb):
+    m = k = 16384
+    W, X = M.gen_q16(0xDEADBEEF ^ 0x6E3F ^ nb, m * k, nb * k, 15)
+    note(f"det_gemv_q16_dev 16384^2 nb={nb}")
+    Y = _dev_run(lambda pw, px, py, s: M.lib().det_gemv_q16_dev(pw, px, py, m, k, nb, s), [W, X], (nb, m))
+    if nb == 1:
+        np.testing.assert_array_equal(Y, O.gemv_q16_batched(W, X, m, k, nb))
+    else:
+        rows = _sample_rows(m, 64)
+        np.testing.assert_array_equal(Y[:, rows], O.gemv_q16_rows(W, X, m, k, nb, rows))
