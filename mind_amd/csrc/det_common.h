@@ -59,6 +59,22 @@ __device__ __forceinline__ void transpose8x8(const uint32_t (&lo)[8], const uint
     transpose4x4(hi[4], hi[5], hi[6], hi[7], chi[4], chi[5], chi[6], chi[7]);
 }
 
+// ---------------------------------------------------------------- buffers
+// Raw buffer resource over [base, base + bytes): a buffer load whose offset
+// lies outside returns zero without touching memory, so tile edges need no
+// branches (an invalid lane passes OOB_OFFSET).  Requires bytes < 2^31.
+constexpr uint32_t OOB_OFFSET = 0x80000000u;
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void *base, uint32_t bytes) {
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void *>(base), (short)0, (int)bytes, 0x00020000);
+}
+__device__ __forceinline__ uint4 buf_load16(__amdgpu_buffer_rsrc_t r, uint32_t off) {
+    const v4i32 v = __builtin_bit_cast(v4i32, __builtin_amdgcn_raw_buffer_load_b128(r, (int)off, 0, 0));
+    return make_uint4((uint32_t)v.x, (uint32_t)v.y, (uint32_t)v.z, (uint32_t)v.w);
+}
+__device__ __forceinline__ uint32_t buf_load4(__amdgpu_buffer_rsrc_t r, uint32_t off) {
+    return __builtin_amdgcn_raw_buffer_load_b32(r, (int)off, 0, 0);
+}
+
 // ---------------------------------------------------------------- XCD map
 // Workgroups are dealt round-robin to the 8 XCDs (each with its own L2).
 // Remap the hardware workgroup id so that each XCD receives a contiguous run

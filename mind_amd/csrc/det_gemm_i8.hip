@@ -27,36 +27,48 @@
 namespace det {
 
 namespace i8g {
-constexpr int BM = 256, BN = 256, BK = 64, THREADS = 256;
+constexpr int BM = 256, BN = 256, BK = 64, THREADS = 512;
 constexpr int TILE_BYTES = BM * BK;  // == BN * BK
 constexpr int GROUP_M = 4;
+constexpr int WM = 128, WN = 64;     // wave tile: 8 x 4 MFMA blocks, 128 accumulators
 
-__device__ __forceinline__ int swz(int row, int chunk) {
+// A tile: row-major [256 rows][64 k] with the four 16-byte chunks of each row
+// XOR-swizzled by (row >> 1) & 3.  Writes of 64 consecutive chunks and the
+// MFMA operand reads of 8 consecutive rows are bank-conflict free.
+__device__ __forceinline__ int swz_a(int row, int chunk) {
     return row * 64 + ((chunk ^ ((row >> 1) & 3)) << 4);
 }
+// B^T tile: [4 k-chunks][256 columns][16 k-bytes]; column slot n is stored at
+// n ^ ((n >> 3) & 7), a permutation inside each aligned group of 8, so both
+// the operand reads (16 consecutive columns) and the transposing writes
+// (columns 4q + c for consecutive q) spread over the 16-byte bank groups.
+__device__ __forceinline__ int swz_b(int g, int n) {
+    return g * 4096 + ((n ^ ((n >> 3) & 7)) << 4);
+}
 
+// Per-thread staging of one K step: 2 x 16 bytes of A, and an 8(k) x 4(n)
+// byte block of B (8 dwords, one per k row).
 struct Frag {
-    uint4 a[4];       // 4 x 16 bytes of A (rows, chunk)
-    uint32_t blo[8];  // 8 rows of B, columns 0..3
-    uint32_t bhi[8];  // 8 rows of B, columns 4..7
+    uint4 a[2];
+    uint32_t b[8];
 };
 
-// Global -> registers.  FAST requires K % 16 == 0, N % 8 == 0 and 16-byte
-// aligned A, 8-byte aligned B: every 16-byte A chunk and 8-byte B run is then
-// either fully inside or fully outside the matrix.
+// Global -> registers.  FAST requires K % 16 == 0, N % 4 == 0, A 16-byte and
+// B 4-byte aligned and both operands below 2^31 bytes: every 16-byte A chunk
+// and 4-byte B run is then either fully inside or fully outside the matrix,
+// and the outside ones are buffer loads at OOB_OFFSET (which return zero).
 template <bool FAST>
 __device__ __forceinline__ void load_tile(Frag &f, const int8_t *__restrict__ A, const int8_t *__restrict__ B,
-                                          int M, int N, int K, int m0, int n0, int k0, int tid) {
+                                          __amdgpu_buffer_rsrc_t ra, __amdgpu_buffer_rsrc_t rb, int M, int N, int K,
+                                          int m0, int n0, int k0, int tid) {
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
+    for (int i = 0; i < 2; ++i) {
         const int idx = i * THREADS + tid;
         const int row = m0 + (idx >> 2);
         const int kc = k0 + ((idx & 3) << 4);
         if (FAST) {
-            if (row < M && kc < K)
-                f.a[i] = *(const uint4 *)(A + (size_t)row * K + kc);
-            else
-                f.a[i] = make_uint4(0, 0, 0, 0);
+            const bool ok = row < M && kc < K;
+            f.a[i] = buf_load16(ra, ok ? (uint32_t)row * (uint32_t)K + (uint32_t)kc : OOB_OFFSET);
         } else {
             uint32_t w[4] = {0, 0, 0, 0};
             if (row < M) {
@@ -68,53 +80,47 @@ __device__ __forceinline__ void load_tile(Frag &f, const int8_t *__restrict__ A,
             f.a[i] = make_uint4(w[0], w[1], w[2], w[3]);
         }
     }
-    const int kb = tid >> 5, nb = tid & 31;
-    const int nc = n0 + nb * 8;
+    const int kb = tid >> 6, q = tid & 63;
+    const int nc = n0 + q * 4;
 #pragma unroll
     for (int r = 0; r < 8; ++r) {
         const int kr = k0 + kb * 8 + r;
         if (FAST) {
-            if (kr < K && nc < N) {
-                const uint2 v = *(const uint2 *)(B + (size_t)kr * N + nc);
-                f.blo[r] = v.x;
-                f.bhi[r] = v.y;
-            } else {
-                f.blo[r] = 0;
-                f.bhi[r] = 0;
-            }
+            const bool ok = kr < K && nc < N;
+            f.b[r] = buf_load4(rb, ok ? (uint32_t)kr * (uint32_t)N + (uint32_t)nc : OOB_OFFSET);
         } else {
-            uint32_t lo = 0, hi = 0;
+            uint32_t v = 0;
             if (kr < K) {
                 const int8_t *p = B + (size_t)kr * N;
 #pragma unroll
-                for (int b = 0; b < 8; ++b)
-                    if (nc + b < N) {
-                        const uint32_t v = (uint32_t)(uint8_t)p[nc + b];
-                        if (b < 4) lo |= v << (b * 8); else hi |= v << ((b - 4) * 8);
-                    }
+                for (int b = 0; b < 4; ++b)
+                    if (nc + b < N) v |= (uint32_t)(uint8_t)p[nc + b] << (b * 8);
             }
-            f.blo[r] = lo;
-            f.bhi[r] = hi;
+            f.b[r] = v;
         }
     }
 }
 
 __device__ __forceinline__ void store_tile(const Frag &f, int8_t *sA, int8_t *sB, int tid) {
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
+    for (int i = 0; i < 2; ++i) {
         const int idx = i * THREADS + tid;
-        *(uint4 *)(sA + swz(idx >> 2, idx & 3)) = f.a[i];
+        *(uint4 *)(sA + swz_a(idx >> 2, idx & 3)) = f.a[i];
     }
-    uint32_t clo[8], chi[8];
-    transpose8x8(f.blo, f.bhi, clo, chi);
-    const int kb = tid >> 5, nb = tid & 31;
+    // 8 rows x 4 columns -> 4 columns x 8 k-bytes
+    uint32_t lo[4], hi[4];
+    transpose4x4(f.b[0], f.b[1], f.b[2], f.b[3], lo[0], lo[1], lo[2], lo[3]);
+    transpose4x4(f.b[4], f.b[5], f.b[6], f.b[7], hi[0], hi[1], hi[2], hi[3]);
+    const int kb = tid >> 6, q = tid & 63;
 #pragma unroll
-    for (int c = 0; c < 8; ++c) {
-        const int n = nb * 8 + c;
-        *(uint2 *)(sB + swz(n, kb >> 1) + ((kb & 1) << 3)) = make_uint2(clo[c], chi[c]);
-    }
+    for (int c = 0; c < 4; ++c)
+        *(uint2 *)(sB + swz_b(kb >> 1, q * 4 + c) + ((kb & 1) << 3)) = make_uint2(lo[c], hi[c]);
 }
 
+// 8 waves (2 per SIMD) share a 256x256 C tile; each owns 128x64.  Loads run
+// two K steps ahead of the MFMAs: register set `next` holds step kt+1 while
+// the other set is refilled with step kt+2, and LDS is double buffered, so
+// each global load has two steps of MFMA work to land.
 template <bool FAST>
 __global__ __launch_bounds__(THREADS, 1) void gemm_i8_kernel(const int8_t *__restrict__ A,
                                                              const int8_t *__restrict__ B,
@@ -133,41 +139,53 @@ __global__ __launch_bounds__(THREADS, 1) void gemm_i8_kernel(const int8_t *__res
 
     const int tid = threadIdx.x;
     const int lane = tid & 63, wave = tid >> 6;
-    const int wm = (wave >> 1) * 128, wn = (wave & 1) * 128;
+    const int wm = (wave >> 2) * WM, wn = (wave & 3) * WN;
     const int lr = lane & 15, lg = lane >> 4;
 
-    v4i32 acc[8][8];
+    v4i32 acc[8][4];
 #pragma unroll
     for (int i = 0; i < 8; ++i)
 #pragma unroll
-        for (int j = 0; j < 8; ++j) acc[i][j] = (v4i32){0, 0, 0, 0};
+        for (int j = 0; j < 4; ++j) acc[i][j] = (v4i32){0, 0, 0, 0};
 
     const int nk = (K + BK - 1) / BK;
-    Frag f;
-    load_tile<FAST>(f, A, B, M, N, K, m0, n0, 0, tid);
-    store_tile(f, smem[0][0], smem[0][1], tid);
+    const __amdgpu_buffer_rsrc_t ra = make_rsrc(A, FAST ? (uint32_t)M * (uint32_t)K : 0u);
+    const __amdgpu_buffer_rsrc_t rb = make_rsrc(B, FAST ? (uint32_t)K * (uint32_t)N : 0u);
+    Frag f0, f1;
+    load_tile<FAST>(f0, A, B, ra, rb, M, N, K, m0, n0, 0, tid);
+    if (nk > 1) load_tile<FAST>(f1, A, B, ra, rb, M, N, K, m0, n0, BK, tid);
+    store_tile(f0, smem[0][0], smem[0][1], tid);
     __syncthreads();
+    if (nk > 2) load_tile<FAST>(f0, A, B, ra, rb, M, N, K, m0, n0, 2 * BK, tid);
 
-    for (int kt = 0; kt < nk; ++kt) {
-        const int cur = kt & 1;
-        const bool more = kt + 1 < nk;
-        if (more) load_tile<FAST>(f, A, B, M, N, K, m0, n0, (kt + 1) * BK, tid);
+    // One K step: MFMAs from LDS buffer CUR, then stage step kt+1 (held in
+    // `next`) into the other buffer, barrier, refill `next` with step kt+3.
+    // Unrolled by two so the register set of each half is static.
+#define DET_I8_STEP(CUR, next)                                                                  \
+    do {                                                                                        \
+        const int8_t *sA = smem[CUR][0];                                                        \
+        const int8_t *sB = smem[CUR][1];                                                        \
+        v2i64 bf[4];                                                                            \
+        _Pragma("unroll") for (int j = 0; j < 4; ++j) bf[j] =                                   \
+            *(const v2i64 *)(sB + swz_b(lg, wn + j * 16 + lr));                                 \
+        _Pragma("unroll") for (int i = 0; i < 8; ++i) {                                         \
+            const v2i64 af = *(const v2i64 *)(sA + swz_a(wm + i * 16 + lr, lg));               \
+            _Pragma("unroll") for (int j = 0; j < 4; ++j) acc[i][j] = mfma16x16x64(af, bf[j], acc[i][j]); \
+        }                                                                                       \
+        if (kt + 1 < nk) store_tile(next, smem[CUR ^ 1][0], smem[CUR ^ 1][1], tid);             \
+        __syncthreads();                                                                        \
+        if (kt + 3 < nk) load_tile<FAST>(next, A, B, ra, rb, M, N, K, m0, n0, (kt + 3) * BK, tid); \
+    } while (0)
 
-        const int8_t *sA = smem[cur][0];
-        const int8_t *sB = smem[cur][1];
-        v2i64 bf[8];
-#pragma unroll
-        for (int j = 0; j < 8; ++j) bf[j] = *(const v2i64 *)(sB + swz(wn + j * 16 + lr, lg));
-#pragma unroll
-        for (int i = 0; i < 8; ++i) {
-            const v2i64 af = *(const v2i64 *)(sA + swz(wm + i * 16 + lr, lg));
-#pragma unroll
-            for (int j = 0; j < 8; ++j) acc[i][j] = mfma16x16x64(af, bf[j], acc[i][j]);
-        }
-
-        if (more) store_tile(f, smem[cur ^ 1][0], smem[cur ^ 1][1], tid);
-        __syncthreads();
+    int kt = 0;
+    for (; kt + 1 < nk; kt += 2) {
+        DET_I8_STEP(0, f1);
+        ++kt;
+        DET_I8_STEP(1, f0);
+        --kt;
     }
+    if (kt < nk) DET_I8_STEP(0, f1);
+#undef DET_I8_STEP
 
     // Epilogue: lane holds C[4*lg + r][lr] of each 16x16 block.
 #pragma unroll
@@ -178,7 +196,7 @@ __global__ __launch_bounds__(THREADS, 1) void gemm_i8_kernel(const int8_t *__res
             if (row >= M) continue;
             int32_t *crow = C + (size_t)row * N;
 #pragma unroll
-            for (int j = 0; j < 8; ++j) {
+            for (int j = 0; j < 4; ++j) {
                 const int col = n0 + wn + j * 16 + lr;
                 if (col < N) __builtin_nontemporal_store(acc[i][j][r], crow + col);
             }
@@ -191,7 +209,8 @@ hipError_t launch_gemm_i8(const int8_t *A, const int8_t *B, int32_t *C, int M, i
     using namespace i8g;
     const int tiles_m = (M + BM - 1) / BM, tiles_n = (N + BN - 1) / BN;
     const dim3 grid(tiles_m * tiles_n), block(THREADS);
-    const bool fast = (K % 16 == 0) && (N % 8 == 0) && (((uintptr_t)A & 15) == 0) && (((uintptr_t)B & 7) == 0);
+    const bool fast = (K % 16 == 0) && (N % 4 == 0) && (((uintptr_t)A & 15) == 0) && (((uintptr_t)B & 3) == 0) &&
+                      (size_t)M * K < 0x80000000ull && (size_t)K * N < 0x80000000ull;
     if (fast)
         hipLaunchKernelGGL(gemm_i8_kernel<true>, grid, block, 0, s, A, B, C, M, N, K, tiles_m, tiles_n);
     else
