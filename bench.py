@@ -138,6 +138,43 @@ def gemv_workload(m: int, k: int, nb: int, steps: int, warmup: int, stream, seed
     return {"ms": ev, "wall_ms": wall, "bytes": nbytes, "verify": verify, "checked_rows": len(rows)}
 
 
+def measure_peaks(stream) -> dict:
+    """Roofline denominators measured on this GPU: int8 MFMA issue rate from
+    a register-only MFMA loop, HBM read and copy bandwidth over 1 GiB."""
+    L = M.lib()
+    sp = stream.ptr
+    ops_in = M.DeviceBuffer.from_array(np.arange(128 * 16, dtype=np.uint8))
+    blocks, iters = 2048, 4096
+    out = M.DeviceBuffer(blocks * 256 * 4)
+    mfma_tops = {}
+    for shape, macs, name in ((0, 16384, "16x16x64"), (1, 32768, "32x32x32")):
+        def mfma():
+            M.check(L.det_probe_mfma_i8(ops_in.ptr, out.ptr, blocks, iters, shape, sp))
+
+        ms, _ = time_steps(mfma, 3, 1, stream)
+        mfma_tops[name] = round(blocks * 4 * iters * 8 * macs * 2 / (ms * 1e-3) / 1e12, 1)
+    nbytes = 1 << 30
+    src, dst = M.DeviceBuffer(nbytes), M.DeviceBuffer(nbytes)
+    src.fill(0x5A)
+    red = M.DeviceBuffer(8192 * 4)
+    red.fill(0)
+
+    def rd():
+        M.check(L.det_probe_read(src.ptr, nbytes, red.ptr, 8192, sp))
+
+    ms_r, _ = time_steps(rd, 5, 2, stream)
+
+    def cp():
+        M.check(L.det_copy_dev(dst.ptr, src.ptr, nbytes, sp))
+
+    ms_c, _ = time_steps(cp, 5, 2, stream)
+    for b in (ops_in, out, src, dst, red):
+        b.free()
+    return {"mfma_i8_tops": mfma_tops, "hbm_read_gbs": round(nbytes / (ms_r * 1e-3) / 1e9, 1),
+            "hbm_copy_gbs": round(2 * nbytes / (ms_c * 1e-3) / 1e9, 1),
+            "note": "register-only int8 MFMA loop (inline asm, 8 independent chains, 32 waves/CU); 1 GiB streaming read; 1 GiB copy (read+write)"}
+
+
 def cpu_baseline_int8(A: np.ndarray, B: np.ndarray, C_gpu: np.ndarray, m: int, k: int, n: int) -> dict:
     """The multithreaded CPU restatement of the reference's MT int8 path
     (oracle/det_cpu_mt.c), timed on this host's cores on a bounded row band
@@ -182,6 +219,7 @@ def main() -> int:
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--only", default="", help="comma list of workloads (default: all)")
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--no-peaks", action="store_true", help="skip the roofline probe micro-kernels")
     args = ap.parse_args()
 
     world = int(os.environ.get("WORLD_SIZE", "1"))
@@ -236,6 +274,11 @@ def main() -> int:
                      "event_ms_per_launch": round(head["ms"], 5)},
         "device": info["name"],
     }
+
+    if not args.no_peaks:
+        log("peaks: int8 MFMA probe, HBM read and copy probes")
+        result["measured_peaks"] = measure_peaks(stream)
+        log(f"peaks: {result['measured_peaks']}")
 
     runs = {"i8_4096": head}
     sec = {}

@@ -147,6 +147,18 @@ int64_t det_event_destroy(void *e);
 int64_t det_event_record(void *e, void *s);
 int64_t det_event_elapsed_ms(void *start, void *stop, float *ms);
 
+/* Roofline probes (no reference counterpart: they measure this GPU).
+ * det_probe_mfma_i8: `blocks` x 256 threads issue 8 independent int8 MFMAs
+ * per iteration on register operands (in: 128 x 16 bytes, out: blocks*256
+ * ints); shape 0 = 16x16x64, 1 = 32x32x32;
+ * ops = blocks * 4 * iters * 8 * (16384 or 32768) * 2.  det_probe_read streams
+ * `bytes` once (out: `blocks` zeroed words).  det_copy_dev is the plain copy
+ * kernel of known size that calibrates the profiler's byte counters. */
+int64_t det_probe_mfma_i8(const void *in, int32_t *out, int64_t blocks, int64_t iters, int64_t shape,
+                          void *stream);
+int64_t det_probe_read(const void *src, int64_t bytes, uint32_t *out, int64_t blocks, void *stream);
+int64_t det_copy_dev(void *dst, const void *src, int64_t bytes, void *stream);
+
 /* Seeded input generators of the reference bench harness (LCG
  * benches/det_matmul_q16.rs:196-209; draw A then B). */
 void det_gen_i8(uint64_t seed, int8_t *a, int64_t na, int8_t *b, int64_t nb);

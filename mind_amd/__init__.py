@@ -82,6 +82,9 @@ def _bind(L):
     L.det_event_create.argtypes = [ctypes.POINTER(_p)]; L.det_event_create.restype = _i64
     L.det_event_record.argtypes = [_p, _p]; L.det_event_record.restype = _i64
     L.det_event_elapsed_ms.argtypes = [_p, _p, ctypes.POINTER(ctypes.c_float)]; L.det_event_elapsed_ms.restype = _i64
+    L.det_probe_mfma_i8.argtypes = [_p, _p, _i64, _i64, _i64, _p]; L.det_probe_mfma_i8.restype = _i64
+    L.det_probe_read.argtypes = [_p, _i64, _p, _i64, _p]; L.det_probe_read.restype = _i64
+    L.det_copy_dev.argtypes = [_p, _p, _i64, _p]; L.det_copy_dev.restype = _i64
     for name in ("det_gen_i8", "det_gen_i16"):
         f = getattr(L, name); f.argtypes = [_u64, _p, _i64, _p, _i64]; f.restype = None
     for name in ("det_gen_q16", "det_gen_q16_sat"):
