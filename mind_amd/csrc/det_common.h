@@ -27,6 +27,14 @@ __device__ __forceinline__ v4i32 mfma16x16x64(const v2i64 a, const v2i64 b, v4i3
     return __builtin_amdgcn_mfma_i32_16x16x64_i8(a, b, c, 0, 0, 0);
 }
 
+// v_mfma_i32_32x32x32_i8: D[32x32] += A[32x32] * B[32x32].  Operands: lane l
+// holds 16 bytes of A row (l & 31) / B column (l & 31), K slice l >> 5.
+// Result: lane l, element r holds D[8*(r >> 2) + 4*(l >> 5) + (r & 3)][l & 31].
+typedef int v16i32 __attribute__((ext_vector_type(16)));
+__device__ __forceinline__ v16i32 mfma32x32x32(const v2i64 a, const v2i64 b, v16i32 c) {
+    return __builtin_amdgcn_mfma_i32_32x32x32_i8(a, b, c, 0, 0, 0);
+}
+
 // ---------------------------------------------------------------- bytes
 // perm(hi, lo, sel): byte i of the result is byte sel.byte[i] of the 64-bit
 // value {hi:lo} (0..3 = lo bytes, 4..7 = hi bytes).

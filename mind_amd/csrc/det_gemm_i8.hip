@@ -30,7 +30,7 @@ namespace i8g {
 constexpr int BM = 256, BN = 256, BK = 64, THREADS = 512;
 constexpr int TILE_BYTES = BM * BK;  // == BN * BK
 constexpr int GROUP_M = 4;
-constexpr int WM = 128, WN = 64;     // wave tile: 8 x 4 MFMA blocks, 128 accumulators
+constexpr int WM = 128, WN = 64;     // wave tile: 4 x 2 blocks of 32x32, 128 accumulators
 
 // A tile: row-major [256 rows][64 k] with the four 16-byte chunks of each row
 // XOR-swizzled by (row >> 1) & 3.  Writes of 64 consecutive chunks and the
@@ -140,13 +140,12 @@ __global__ __launch_bounds__(THREADS, 1) void gemm_i8_kernel(const int8_t *__res
     const int tid = threadIdx.x;
     const int lane = tid & 63, wave = tid >> 6;
     const int wm = (wave >> 2) * WM, wn = (wave & 3) * WN;
-    const int lr = lane & 15, lg = lane >> 4;
-
-    v4i32 acc[8][4];
+    v16i32 acc[4][2];
 #pragma unroll
-    for (int i = 0; i < 8; ++i)
+    for (int i = 0; i < 4; ++i)
 #pragma unroll
-        for (int j = 0; j < 4; ++j) acc[i][j] = (v4i32){0, 0, 0, 0};
+        for (int j = 0; j < 2; ++j) acc[i][j] = (v16i32){0};
+    const int l32 = lane & 31, lh = lane >> 5;
 
     const int nk = (K + BK - 1) / BK;
     const __amdgpu_buffer_rsrc_t ra = make_rsrc(A, FAST ? (uint32_t)M * (uint32_t)K : 0u);
@@ -165,12 +164,14 @@ __global__ __launch_bounds__(THREADS, 1) void gemm_i8_kernel(const int8_t *__res
     do {                                                                                        \
         const int8_t *sA = smem[CUR][0];                                                        \
         const int8_t *sB = smem[CUR][1];                                                        \
-        v2i64 bf[4];                                                                            \
-        _Pragma("unroll") for (int j = 0; j < 4; ++j) bf[j] =                                   \
-            *(const v2i64 *)(sB + swz_b(lg, wn + j * 16 + lr));                                 \
-        _Pragma("unroll") for (int i = 0; i < 8; ++i) {                                         \
-            const v2i64 af = *(const v2i64 *)(sA + swz_a(wm + i * 16 + lr, lg));               \
-            _Pragma("unroll") for (int j = 0; j < 4; ++j) acc[i][j] = mfma16x16x64(af, bf[j], acc[i][j]); \
+        _Pragma("unroll") for (int h = 0; h < 2; ++h) {                                         \
+            v2i64 bf[2];                                                                        \
+            _Pragma("unroll") for (int j = 0; j < 2; ++j) bf[j] =                               \
+                *(const v2i64 *)(sB + swz_b(2 * h + lh, wn + j * 32 + l32));                    \
+            _Pragma("unroll") for (int i = 0; i < 4; ++i) {                                     \
+                const v2i64 af = *(const v2i64 *)(sA + swz_a(wm + i * 32 + l32, 2 * h + lh));   \
+                _Pragma("unroll") for (int j = 0; j < 2; ++j) acc[i][j] = mfma32x32x32(af, bf[j], acc[i][j]); \
+            }                                                                                   \
         }                                                                                       \
         if (kt + 1 < nk) store_tile(next, smem[CUR ^ 1][0], smem[CUR ^ 1][1], tid);             \
         __syncthreads();                                                                        \
@@ -187,17 +188,18 @@ __global__ __launch_bounds__(THREADS, 1) void gemm_i8_kernel(const int8_t *__res
     if (kt < nk) DET_I8_STEP(0, f1);
 #undef DET_I8_STEP
 
-    // Epilogue: lane holds C[4*lg + r][lr] of each 16x16 block.
+    // Epilogue: lane holds C[8*(r >> 2) + 4*lh + (r & 3)][l32] of each 32x32
+    // block; a store instruction covers 32 consecutive columns (128 bytes).
 #pragma unroll
-    for (int i = 0; i < 8; ++i) {
+    for (int i = 0; i < 4; ++i) {
 #pragma unroll
-        for (int r = 0; r < 4; ++r) {
-            const int row = m0 + wm + i * 16 + lg * 4 + r;
+        for (int r = 0; r < 16; ++r) {
+            const int row = m0 + wm + i * 32 + 8 * (r >> 2) + 4 * lh + (r & 3);
             if (row >= M) continue;
             int32_t *crow = C + (size_t)row * N;
 #pragma unroll
-            for (int j = 0; j < 4; ++j) {
-                const int col = n0 + wn + j * 16 + lr;
+            for (int j = 0; j < 2; ++j) {
+                const int col = n0 + wn + j * 32 + l32;
                 if (col < N) __builtin_nontemporal_store(acc[i][j][r], crow + col);
             }
         }

@@ -7,8 +7,6 @@
 namespace det {
 namespace probe {
 
-typedef int v16i32 __attribute__((ext_vector_type(16)));
-
 // Every wave issues `iters` rounds of 8 independent int8 MFMAs on register
 // operands (no memory traffic).  The MFMAs are emitted as inline assembly so
 // the loop holds nothing else: the compiler's register allocation cannot add
