@@ -10,17 +10,22 @@
 // wrap-around, i.e. mod 2^32, which is exactly the reference's i64 sum
 // truncated to i32.
 //
-// Tiling: one 256-thread workgroup (4 waves, 2x2) per 256x256 C tile, each
-// wave owns a 128x128 sub-tile = 8x8 MFMA blocks (256 accumulator registers).
-// K advances 64 bytes per step.  A tiles go global -> LDS unchanged (K is
-// contiguous, which is what the MFMA operand wants).  B is row-major (N
-// contiguous) but the MFMA B operand needs K-contiguous bytes per column, so
-// every thread loads an 8(k) x 8(n) byte block and transposes it in registers
-// with v_perm_b32 before writing it to LDS as B^T.  LDS rows are 64 bytes;
-// the four 16-byte chunks of a row are XOR-swizzled by (row >> 1) & 3 so the
-// ds_read_b128 operand fetches of 8 consecutive rows hit distinct banks.
-// Two LDS buffers: the global loads for step t+1 are issued before the MFMAs
-// of step t and written to the other buffer afterwards, one barrier per step.
+// Tiling: one 512-thread workgroup (8 waves, 2 per SIMD) per 256x256 C tile;
+// each wave owns 128x64 = 4x2 blocks of v_mfma_i32_32x32x32_i8.  K advances
+// 64 bytes per step.  Both operands move global -> registers -> LDS as raw
+// 16-byte row chunks (buffer_load_dwordx4 / ds_write_b128, XOR-swizzled so
+// both the writes and the operand reads are bank-conflict free):
+//  * A (K contiguous) is read back with ds_read_b128: lane l gets 16
+//    K-bytes of row l & 31, the MFMA A layout.
+//  * B (N contiguous) needs K-contiguous bytes per column; it is read back
+//    with gfx950's transposing LDS read ds_read_b64_tr_b8.  Within each
+//    16-lane group that instruction returns, to lane t, byte t & 7 of the
+//    8-byte segments addressed by lanes 2j + (t >> 3), j = 0..7; so when
+//    lane i addresses row k0 + (i >> 1), columns n0 + 8 (i & 1), lane t
+//    receives B[k0 .. k0+7][n0 + t] -- one column, 8 consecutive K.  Two such
+//    reads form the 16-byte B operand.
+// Loads run two K steps ahead of the MFMAs (two register sets, two LDS
+// buffers, one barrier per step).
 #include "det_common.h"
 #include "det_kernels.h"
 
@@ -32,31 +37,36 @@ constexpr int TILE_BYTES = BM * BK;  // == BN * BK
 constexpr int GROUP_M = 4;
 constexpr int WM = 128, WN = 64;     // wave tile: 4 x 2 blocks of 32x32, 128 accumulators
 
-// A tile: row-major [256 rows][64 k] with the four 16-byte chunks of each row
-// XOR-swizzled by (row >> 1) & 3.  Writes of 64 consecutive chunks and the
-// MFMA operand reads of 8 consecutive rows are bank-conflict free.
+// A tile: [256 rows][64 k]; the four 16-byte chunks of a row are XOR-swizzled
+// by (row >> 1) & 3.
 __device__ __forceinline__ int swz_a(int row, int chunk) {
     return row * 64 + ((chunk ^ ((row >> 1) & 3)) << 4);
 }
-// B^T tile: [4 k-chunks][256 columns][16 k-bytes]; column slot n is stored at
-// n ^ ((n >> 3) & 7), a permutation inside each aligned group of 8, so both
-// the operand reads (16 consecutive columns) and the transposing writes
-// (columns 4q + c for consecutive q) spread over the 16-byte bank groups.
-__device__ __forceinline__ int swz_b(int g, int n) {
-    return g * 4096 + ((n ^ ((n >> 3) & 7)) << 4);
+// B tile: [64 k rows][256 n]; the sixteen 16-byte chunks of a row are
+// XOR-swizzled by row & 7, so the eight rows a transposing read touches land
+// in eight different bank groups.
+__device__ __forceinline__ int swz_b(int row, int chunk) {
+    return row * 256 + ((chunk ^ (row & 7)) << 4);
 }
 
-// Per-thread staging of one K step: 2 x 16 bytes of A, and an 8(k) x 4(n)
-// byte block of B (8 dwords, one per k row).
+typedef int v2i32 __attribute__((ext_vector_type(2)));
+typedef __attribute__((address_space(3))) v2i32 *lds_v2i32_ptr;
+
+// Transposing read: see the header comment.  `p` is this lane's segment.
+__device__ __forceinline__ v2i32 read_tr8(const int8_t *p) {
+    return __builtin_amdgcn_ds_read_tr8_b64_v2i32((lds_v2i32_ptr)(p));
+}
+
+// Per-thread staging of one K step: 2 x 16 bytes of A and 2 x 16 bytes of B.
 struct Frag {
     uint4 a[2];
-    uint32_t b[8];
+    uint4 b[2];
 };
 
-// Global -> registers.  FAST requires K % 16 == 0, N % 4 == 0, A 16-byte and
-// B 4-byte aligned and both operands below 2^31 bytes: every 16-byte A chunk
-// and 4-byte B run is then either fully inside or fully outside the matrix,
-// and the outside ones are buffer loads at OOB_OFFSET (which return zero).
+// Global -> registers.  FAST requires K % 16 == 0, N % 16 == 0, 16-byte
+// aligned A and B, both below 2^31 bytes: every 16-byte chunk is then either
+// fully inside or fully outside its matrix, and the outside ones are buffer
+// loads at OOB_OFFSET (which return zero).
 template <bool FAST>
 __device__ __forceinline__ void load_tile(Frag &f, const int8_t *__restrict__ A, const int8_t *__restrict__ B,
                                           __amdgpu_buffer_rsrc_t ra, __amdgpu_buffer_rsrc_t rb, int M, int N, int K,
@@ -64,39 +74,31 @@ __device__ __forceinline__ void load_tile(Frag &f, const int8_t *__restrict__ A,
 #pragma unroll
     for (int i = 0; i < 2; ++i) {
         const int idx = i * THREADS + tid;
+        // A: 256 rows x 4 chunks
         const int row = m0 + (idx >> 2);
         const int kc = k0 + ((idx & 3) << 4);
+        // B: 64 rows x 16 chunks
+        const int kr = k0 + (idx >> 4);
+        const int nc = n0 + ((idx & 15) << 4);
         if (FAST) {
-            const bool ok = row < M && kc < K;
-            f.a[i] = buf_load16(ra, ok ? (uint32_t)row * (uint32_t)K + (uint32_t)kc : OOB_OFFSET);
+            f.a[i] = buf_load16(ra, row < M && kc < K ? (uint32_t)row * (uint32_t)K + (uint32_t)kc : OOB_OFFSET);
+            f.b[i] = buf_load16(rb, kr < K && nc < N ? (uint32_t)kr * (uint32_t)N + (uint32_t)nc : OOB_OFFSET);
         } else {
-            uint32_t w[4] = {0, 0, 0, 0};
+            uint32_t w[4] = {0, 0, 0, 0}, v[4] = {0, 0, 0, 0};
             if (row < M) {
                 const int8_t *p = A + (size_t)row * K;
 #pragma unroll
                 for (int b = 0; b < 16; ++b)
                     if (kc + b < K) w[b >> 2] |= (uint32_t)(uint8_t)p[kc + b] << ((b & 3) * 8);
             }
-            f.a[i] = make_uint4(w[0], w[1], w[2], w[3]);
-        }
-    }
-    const int kb = tid >> 6, q = tid & 63;
-    const int nc = n0 + q * 4;
-#pragma unroll
-    for (int r = 0; r < 8; ++r) {
-        const int kr = k0 + kb * 8 + r;
-        if (FAST) {
-            const bool ok = kr < K && nc < N;
-            f.b[r] = buf_load4(rb, ok ? (uint32_t)kr * (uint32_t)N + (uint32_t)nc : OOB_OFFSET);
-        } else {
-            uint32_t v = 0;
             if (kr < K) {
                 const int8_t *p = B + (size_t)kr * N;
 #pragma unroll
-                for (int b = 0; b < 4; ++b)
-                    if (nc + b < N) v |= (uint32_t)(uint8_t)p[nc + b] << (b * 8);
+                for (int b = 0; b < 16; ++b)
+                    if (nc + b < N) v[b >> 2] |= (uint32_t)(uint8_t)p[nc + b] << ((b & 3) * 8);
             }
-            f.b[r] = v;
+            f.a[i] = make_uint4(w[0], w[1], w[2], w[3]);
+            f.b[i] = make_uint4(v[0], v[1], v[2], v[3]);
         }
     }
 }
@@ -106,21 +108,10 @@ __device__ __forceinline__ void store_tile(const Frag &f, int8_t *sA, int8_t *sB
     for (int i = 0; i < 2; ++i) {
         const int idx = i * THREADS + tid;
         *(uint4 *)(sA + swz_a(idx >> 2, idx & 3)) = f.a[i];
+        *(uint4 *)(sB + swz_b(idx >> 4, idx & 15)) = f.b[i];
     }
-    // 8 rows x 4 columns -> 4 columns x 8 k-bytes
-    uint32_t lo[4], hi[4];
-    transpose4x4(f.b[0], f.b[1], f.b[2], f.b[3], lo[0], lo[1], lo[2], lo[3]);
-    transpose4x4(f.b[4], f.b[5], f.b[6], f.b[7], hi[0], hi[1], hi[2], hi[3]);
-    const int kb = tid >> 6, q = tid & 63;
-#pragma unroll
-    for (int c = 0; c < 4; ++c)
-        *(uint2 *)(sB + swz_b(kb >> 1, q * 4 + c) + ((kb & 1) << 3)) = make_uint2(lo[c], hi[c]);
 }
 
-// 8 waves (2 per SIMD) share a 256x256 C tile; each owns 128x64.  Loads run
-// two K steps ahead of the MFMAs: register set `next` holds step kt+1 while
-// the other set is refilled with step kt+2, and LDS is double buffered, so
-// each global load has two steps of MFMA work to land.
 template <bool FAST>
 __global__ __launch_bounds__(THREADS, 1) void gemm_i8_kernel(const int8_t *__restrict__ A,
                                                              const int8_t *__restrict__ B,
@@ -140,12 +131,17 @@ __global__ __launch_bounds__(THREADS, 1) void gemm_i8_kernel(const int8_t *__res
     const int tid = threadIdx.x;
     const int lane = tid & 63, wave = tid >> 6;
     const int wm = (wave >> 2) * WM, wn = (wave & 3) * WN;
+    const int l32 = lane & 31, lh = lane >> 5;
+    // transposing-read addressing of this lane (16-lane group G, index i)
+    const int tg = lane >> 4, ti = lane & 15;
+    const int tr_row = 16 * (tg >> 1) + (ti >> 1);   // + 32 h + 8 q
+    const int tr_col = 16 * (tg & 1) + 8 * (ti & 1); // + wn + 32 j
+
     v16i32 acc[4][2];
 #pragma unroll
     for (int i = 0; i < 4; ++i)
 #pragma unroll
         for (int j = 0; j < 2; ++j) acc[i][j] = (v16i32){0};
-    const int l32 = lane & 31, lh = lane >> 5;
 
     const int nk = (K + BK - 1) / BK;
     const __amdgpu_buffer_rsrc_t ra = make_rsrc(A, FAST ? (uint32_t)M * (uint32_t)K : 0u);
@@ -166,8 +162,13 @@ __global__ __launch_bounds__(THREADS, 1) void gemm_i8_kernel(const int8_t *__res
         const int8_t *sB = smem[CUR][1];                                                        \
         _Pragma("unroll") for (int h = 0; h < 2; ++h) {                                         \
             v2i64 bf[2];                                                                        \
-            _Pragma("unroll") for (int j = 0; j < 2; ++j) bf[j] =                               \
-                *(const v2i64 *)(sB + swz_b(2 * h + lh, wn + j * 32 + l32));                    \
+            _Pragma("unroll") for (int j = 0; j < 2; ++j) {                                     \
+                const int r = 32 * h + tr_row, cb = (wn + 32 * j + tr_col) >> 4;                \
+                const int sub = tr_col & 8;                                                     \
+                const v2i32 lo = read_tr8(sB + swz_b(r, cb) + sub);                             \
+                const v2i32 hi = read_tr8(sB + swz_b(r + 8, cb) + sub);                         \
+                bf[j] = __builtin_bit_cast(v2i64, (v4i32){lo.x, lo.y, hi.x, hi.y});            \
+            }                                                                                   \
             _Pragma("unroll") for (int i = 0; i < 4; ++i) {                                     \
                 const v2i64 af = *(const v2i64 *)(sA + swz_a(wm + i * 32 + l32, 2 * h + lh));   \
                 _Pragma("unroll") for (int j = 0; j < 2; ++j) acc[i][j] = mfma32x32x32(af, bf[j], acc[i][j]); \
@@ -211,7 +212,7 @@ hipError_t launch_gemm_i8(const int8_t *A, const int8_t *B, int32_t *C, int M, i
     using namespace i8g;
     const int tiles_m = (M + BM - 1) / BM, tiles_n = (N + BN - 1) / BN;
     const dim3 grid(tiles_m * tiles_n), block(THREADS);
-    const bool fast = (K % 16 == 0) && (N % 4 == 0) && (((uintptr_t)A & 15) == 0) && (((uintptr_t)B & 3) == 0) &&
+    const bool fast = (K % 16 == 0) && (N % 16 == 0) && (((uintptr_t)A & 15) == 0) && (((uintptr_t)B & 15) == 0) &&
                       (size_t)M * K < 0x80000000ull && (size_t)K * N < 0x80000000ull;
     if (fast)
         hipLaunchKernelGGL(gemm_i8_kernel<true>, grid, block, 0, s, A, B, C, M, N, K, tiles_m, tiles_n);
