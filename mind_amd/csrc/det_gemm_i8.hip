@@ -37,16 +37,21 @@ constexpr int TILE_BYTES = BM * BK;  // == BN * BK
 constexpr int GROUP_M = 4;
 constexpr int WM = 128, WN = 64;     // wave tile: 4 x 2 blocks of 32x32, 128 accumulators
 
+// LDS has 64 four-byte banks (256 bytes per cycle).
 // A tile: [256 rows][64 k]; the four 16-byte chunks of a row are XOR-swizzled
-// by (row >> 1) & 3.
+// by (row >> 2) & 3, so the 16 lanes of a ds_read_b128 (16 consecutive rows,
+// one chunk) and of a ds_write_b128 (4 rows x 4 chunks) hit 16 distinct
+// 16-byte bank groups.
 __device__ __forceinline__ int swz_a(int row, int chunk) {
-    return row * 64 + ((chunk ^ ((row >> 1) & 3)) << 4);
+    return row * 64 + ((chunk ^ ((row >> 2) & 3)) << 4);
 }
 // B tile: [64 k rows][256 n]; the sixteen 16-byte chunks of a row are
-// XOR-swizzled by row & 7, so the eight rows a transposing read touches land
-// in eight different bank groups.
+// XOR-swizzled by 2 * (row & 7).  A transposing read's 16-lane group touches
+// 8 rows x one chunk: 8 distinct slots of one parity; the neighbouring group
+// reads the next (opposite parity) chunk, so each pair of groups covers all
+// 64 banks once.
 __device__ __forceinline__ int swz_b(int row, int chunk) {
-    return row * 256 + ((chunk ^ (row & 7)) << 4);
+    return row * 256 + ((chunk ^ ((row & 7) << 1)) << 4);
 }
 
 typedef int v2i32 __attribute__((ext_vector_type(2)));
@@ -148,35 +153,58 @@ __global__ __launch_bounds__(THREADS, 1) void gemm_i8_kernel(const int8_t *__res
     const __amdgpu_buffer_rsrc_t rb = make_rsrc(B, FAST ? (uint32_t)K * (uint32_t)N : 0u);
     Frag f0, f1;
     load_tile<FAST>(f0, A, B, ra, rb, M, N, K, m0, n0, 0, tid);
-    if (nk > 1) load_tile<FAST>(f1, A, B, ra, rb, M, N, K, m0, n0, BK, tid);
+    load_tile<FAST>(f1, A, B, ra, rb, M, N, K, m0, n0, BK, tid);
     store_tile(f0, smem[0][0], smem[0][1], tid);
     __syncthreads();
-    if (nk > 2) load_tile<FAST>(f0, A, B, ra, rb, M, N, K, m0, n0, 2 * BK, tid);
+    load_tile<FAST>(f0, A, B, ra, rb, M, N, K, m0, n0, 2 * BK, tid);
 
-    // One K step: MFMAs from LDS buffer CUR, then stage step kt+1 (held in
-    // `next`) into the other buffer, barrier, refill `next` with step kt+3.
-    // Unrolled by two so the register set of each half is static.
-#define DET_I8_STEP(CUR, next)                                                                  \
-    do {                                                                                        \
-        const int8_t *sA = smem[CUR][0];                                                        \
-        const int8_t *sB = smem[CUR][1];                                                        \
-        _Pragma("unroll") for (int h = 0; h < 2; ++h) {                                         \
-            v2i64 bf[2];                                                                        \
-            _Pragma("unroll") for (int j = 0; j < 2; ++j) {                                     \
-                const int r = 32 * h + tr_row, cb = (wn + 32 * j + tr_col) >> 4;                \
-                const int sub = tr_col & 8;                                                     \
-                const v2i32 lo = read_tr8(sB + swz_b(r, cb) + sub);                             \
-                const v2i32 hi = read_tr8(sB + swz_b(r + 8, cb) + sub);                         \
-                bf[j] = __builtin_bit_cast(v2i64, (v4i32){lo.x, lo.y, hi.x, hi.y});            \
-            }                                                                                   \
-            _Pragma("unroll") for (int i = 0; i < 4; ++i) {                                     \
-                const v2i64 af = *(const v2i64 *)(sA + swz_a(wm + i * 32 + l32, 2 * h + lh));   \
-                _Pragma("unroll") for (int j = 0; j < 2; ++j) acc[i][j] = mfma32x32x32(af, bf[j], acc[i][j]); \
-            }                                                                                   \
-        }                                                                                       \
-        if (kt + 1 < nk) store_tile(next, smem[CUR ^ 1][0], smem[CUR ^ 1][1], tid);             \
-        __syncthreads();                                                                        \
-        if (kt + 3 < nk) load_tile<FAST>(next, A, B, ra, rb, M, N, K, m0, n0, (kt + 3) * BK, tid); \
+    // Operand fragments of one K sub-step (32 k): 4 A rows-blocks, 2 B columns.
+    struct Ops {
+        v2i64 a[4], b[2];
+    };
+    auto read_ops = [&](Ops &o, const int8_t *sA, const int8_t *sB, int h) {
+#pragma unroll
+        for (int j = 0; j < 2; ++j) {
+            const int r = 32 * h + tr_row, cb = (wn + 32 * j + tr_col) >> 4, sub = tr_col & 8;
+            const v2i32 lo = read_tr8(sB + swz_b(r, cb) + sub);
+            const v2i32 hi = read_tr8(sB + swz_b(r + 8, cb) + sub);
+            o.b[j] = __builtin_bit_cast(v2i64, (v4i32){lo.x, lo.y, hi.x, hi.y});
+        }
+#pragma unroll
+        for (int i = 0; i < 4; ++i) o.a[i] = *(const v2i64 *)(sA + swz_a(wm + i * 32 + l32, 2 * h + lh));
+    };
+    auto mma = [&](const Ops &o) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+#pragma unroll
+            for (int j = 0; j < 2; ++j) acc[i][j] = mfma32x32x32(o.a[i], o.b[j], acc[i][j]);
+    };
+
+    // Software pipeline, per K step kt (LDS buffer CUR holds step kt, `p0`
+    // its first 32-k fragments, already read):
+    //   read second-half fragments -> p1;  MFMAs on p0;
+    //   stage step kt+1 (register set `next`) into the other LDS buffer;
+    //   barrier (the issued MFMAs keep running through it);
+    //   refill `next` with step kt+3 (two steps of lead);
+    //   read the first-half fragments of step kt+1 -> p0;  MFMAs on p1.
+    // Every LDS burst thus overlaps MFMAs already in flight.  The body is
+    // branch-free: past the end of K the loads fall outside the matrix
+    // (zeros, no memory access on the fast path), and the last stores / reads
+    // touch a buffer whose contents are never used.  sched_barrier pins the
+    // phase order against the scheduler.
+    Ops p0, p1;
+    read_ops(p0, smem[0][0], smem[0][1], 0);
+#define DET_I8_STEP(CUR, next)                                                    \
+    do {                                                                          \
+        read_ops(p1, smem[CUR][0], smem[CUR][1], 1);                              \
+        mma(p0);                                                                  \
+        store_tile(next, smem[CUR ^ 1][0], smem[CUR ^ 1][1], tid);                \
+        __syncthreads();                                                          \
+        load_tile<FAST>(next, A, B, ra, rb, M, N, K, m0, n0, (kt + 3) * BK, tid); \
+        __builtin_amdgcn_sched_barrier(0);                                        \
+        read_ops(p0, smem[CUR ^ 1][0], smem[CUR ^ 1][1], 0);                      \
+        mma(p1);                                                                  \
+        __builtin_amdgcn_sched_barrier(0);                                        \
     } while (0)
 
     int kt = 0;
