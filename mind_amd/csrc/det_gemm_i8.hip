@@ -234,6 +234,181 @@ __global__ __launch_bounds__(THREADS, 1) void gemm_i8_kernel(const int8_t *__res
         }
     }
 }
+
+// ---------------------------------------------------------------- DMA path
+// Fast path (aligned shapes): operands go global -> LDS directly with
+// buffer_load_dwordx4 ... lds (no register staging, no ds_write).  One such
+// instruction writes 64 x 16 consecutive LDS bytes, lane i at offset 16 i;
+// the lane -> global chunk assignment is the inverse of swz_a / swz_b, so
+// the LDS tiles have exactly the layouts above.  Out-of-range chunks use
+// OOB_OFFSET and land in LDS as zeros.  NSTAGE LDS stages; each wave issues
+// 2 A blocks + 2 B blocks (4 instructions) per stage.
+//
+// Per iteration kt (fragments p0 = first half of step kt already read):
+//   read p1 (second half of step kt);  MFMAs on p0;
+//   wait until this wave's loads of step kt+1 landed, then s_barrier
+//   (every wave's loads of step kt+1 are in LDS, and every wave finished
+//   iteration kt-1, so buffer (kt-1) % NSTAGE is free);
+//   issue step kt-1+NSTAGE into that buffer;
+//   read p0 of step kt+1;  MFMAs on p1.
+// The wait is explicit (s_waitcnt vmcnt) and the barrier is a bare
+// s_barrier: the loads of later steps stay in flight across it.
+constexpr int NSTAGE = 4;
+constexpr int DMA_PER_STAGE = 4;     // instructions per wave per stage
+
+typedef __attribute__((address_space(3))) int8_t *lds_i8_ptr;
+
+// Raw buffer descriptor as four SGPR words (base, stride 0, num_records,
+// gfx9 data-format word) for the inline-assembly DMA below.
+__device__ __forceinline__ v4i32 rsrc_words(const void *base, uint32_t bytes) {
+    const uint64_t a = (uint64_t)(uintptr_t)base;
+    return (v4i32){(int)(uint32_t)a, (int)(uint32_t)(a >> 32) & 0xffff, (int)bytes, 0x00020000};
+}
+// One buffer_load_dwordx4 ... lds: lane i's 16 bytes at `voff` land at LDS
+// byte lds + 16 i.  Written as inline assembly so the compiler's wait-count
+// pass does not treat every later LDS read as dependent on it (it would
+// drain all loads in flight); the kernel orders these loads itself with
+// explicit s_waitcnt vmcnt and s_barrier.  The kernel issues no other
+// vector-memory loads while these are outstanding.
+__device__ __forceinline__ void dma16(v4i32 rsrc, uint32_t lds, int voff) {
+    asm volatile("s_mov_b32 m0, %0\n\tbuffer_load_dwordx4 %1, %2, 0 offen lds" ::"s"(lds), "v"(voff), "s"(rsrc)
+                 : "memory", "m0");
+}
+__device__ __forceinline__ uint32_t lds_addr(const int8_t *p) {
+    return __builtin_amdgcn_readfirstlane((uint32_t)(uintptr_t)(lds_i8_ptr)(p));
+}
+
+// s_waitcnt with vmcnt <= n (n < 64), expcnt / lgkmcnt left unconstrained.
+#define DET_WAIT_VMCNT(n) __builtin_amdgcn_s_waitcnt(((n) & 15) | (7 << 4) | (15 << 8) | (((n) >> 4) << 14))
+
+__global__ __launch_bounds__(THREADS, 1) void gemm_i8_dma_kernel(const int8_t *__restrict__ A,
+                                                                 const int8_t *__restrict__ B,
+                                                                 int32_t *__restrict__ C, int M, int N, int K,
+                                                                 int tiles_m, int tiles_n) {
+    __shared__ __attribute__((aligned(1024))) int8_t smem[NSTAGE][2][TILE_BYTES];
+
+    const int ntiles = tiles_m * tiles_n;
+    const int pid = xcd_remap(blockIdx.x, ntiles);
+    const int in_group = GROUP_M * tiles_n;
+    const int first_m = (pid / in_group) * GROUP_M;
+    const int gsize = min(tiles_m - first_m, GROUP_M);
+    const int tm = first_m + (pid % in_group) % gsize;
+    const int tn = (pid % in_group) / gsize;
+    const int m0 = tm * BM, n0 = tn * BN;
+
+    const int tid = threadIdx.x;
+    const int lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int wm = (wave >> 2) * WM, wn = (wave & 3) * WN;
+    const int l32 = lane & 31, lh = lane >> 5;
+    const int tg = lane >> 4, ti = lane & 15;
+    const int tr_row = 16 * (tg >> 1) + (ti >> 1);
+    const int tr_col = 16 * (tg & 1) + 8 * (ti & 1);
+
+    const v4i32 ra = rsrc_words(A, (uint32_t)M * (uint32_t)K);
+    const v4i32 rb = rsrc_words(B, (uint32_t)K * (uint32_t)N);
+
+    // this lane's chunk of each of the wave's 2 A blocks and 2 B blocks
+    uint32_t a_off[2], b_off[2];
+    int a_kc[2], b_kr[2];
+    bool a_ok[2], b_ok[2];
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+        const int slot = 64 * (2 * wave + j) + lane;
+        const int ar = slot >> 2, ac = (slot & 3) ^ ((ar >> 2) & 3);
+        a_ok[j] = m0 + ar < M;
+        a_kc[j] = 16 * ac;
+        a_off[j] = (uint32_t)(m0 + ar) * (uint32_t)K + (uint32_t)a_kc[j];
+        const int br = slot >> 4, bc = (slot & 15) ^ ((br & 7) << 1);
+        b_ok[j] = n0 + 16 * bc < N;
+        b_kr[j] = br;
+        b_off[j] = (uint32_t)br * (uint32_t)N + (uint32_t)(n0 + 16 * bc);
+    }
+    auto issue = [&](int stage, int k0) {
+#pragma unroll
+        for (int j = 0; j < 2; ++j) {
+            const int blk = 2 * wave + j;
+            const bool oka = a_ok[j] && k0 + a_kc[j] < K;
+            dma16(ra, lds_addr(smem[stage][0] + blk * 1024), oka ? (int)(a_off[j] + (uint32_t)k0) : (int)OOB_OFFSET);
+            const bool okb = b_ok[j] && k0 + b_kr[j] < K;
+            dma16(rb, lds_addr(smem[stage][1] + blk * 1024),
+                  okb ? (int)(b_off[j] + (uint32_t)k0 * (uint32_t)N) : (int)OOB_OFFSET);
+        }
+    };
+
+    v16i32 acc[4][2];
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int j = 0; j < 2; ++j) acc[i][j] = (v16i32){0};
+
+    struct Ops {
+        v2i64 a[4], b[2];
+    };
+    auto read_ops = [&](Ops &o, int stage, int h) {
+        const int8_t *sA = smem[stage][0];
+        const int8_t *sB = smem[stage][1];
+#pragma unroll
+        for (int j = 0; j < 2; ++j) {
+            const int r = 32 * h + tr_row, cb = (wn + 32 * j + tr_col) >> 4, sub = tr_col & 8;
+            const v2i32 lo = read_tr8(sB + swz_b(r, cb) + sub);
+            const v2i32 hi = read_tr8(sB + swz_b(r + 8, cb) + sub);
+            o.b[j] = __builtin_bit_cast(v2i64, (v4i32){lo.x, lo.y, hi.x, hi.y});
+        }
+#pragma unroll
+        for (int i = 0; i < 4; ++i) o.a[i] = *(const v2i64 *)(sA + swz_a(wm + i * 32 + l32, 2 * h + lh));
+    };
+    auto mma = [&](const Ops &o) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+#pragma unroll
+            for (int j = 0; j < 2; ++j) acc[i][j] = mfma32x32x32(o.a[i], o.b[j], acc[i][j]);
+    };
+
+    const int nk = (K + BK - 1) / BK;
+#pragma unroll
+    for (int st = 0; st < NSTAGE - 1; ++st) issue(st, st * BK);
+    DET_WAIT_VMCNT(DMA_PER_STAGE * (NSTAGE - 2));   // step 0 landed
+    __builtin_amdgcn_s_barrier();
+    Ops p0, p1;
+    read_ops(p0, 0, 0);
+    for (int kt = 0; kt < nk; ++kt) {
+        const int cur = kt % NSTAGE, nxt = (kt + 1) % NSTAGE;
+        read_ops(p1, cur, 1);
+        mma(p0);
+        // loads of steps kt+1 .. kt+NSTAGE-2 are outstanding; the oldest
+        // (kt+1) must have landed
+        DET_WAIT_VMCNT(DMA_PER_STAGE * (NSTAGE - 3));
+        __builtin_amdgcn_s_waitcnt(0xc07f & ~(15 << 8));   // lgkmcnt(0): this wave's reads done
+        __builtin_amdgcn_s_barrier();
+        issue((kt + NSTAGE - 1) % NSTAGE, (kt + NSTAGE - 1) * BK);
+        __builtin_amdgcn_sched_barrier(0);
+        read_ops(p0, nxt, 0);
+        mma(p1);
+        __builtin_amdgcn_sched_barrier(0);
+    }
+    // the loads issued past the end of K are zero fills; none may still be
+    // writing LDS when the workgroup ends
+    DET_WAIT_VMCNT(0);
+
+    // Epilogue: lane holds C[8*(r >> 2) + 4*lh + (r & 3)][l32] of each 32x32
+    // block; a store instruction covers 32 consecutive columns (128 bytes).
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+            const int row = m0 + wm + i * 32 + 8 * (r >> 2) + 4 * lh + (r & 3);
+            if (row >= M) continue;
+            int32_t *crow = C + (size_t)row * N;
+#pragma unroll
+            for (int j = 0; j < 2; ++j) {
+                const int col = n0 + wn + j * 32 + l32;
+                if (col < N) __builtin_nontemporal_store(acc[i][j][r], crow + col);
+            }
+        }
+    }
+}
+#undef DET_WAIT_VMCNT
 }  // namespace i8g
 
 hipError_t launch_gemm_i8(const int8_t *A, const int8_t *B, int32_t *C, int M, int N, int K, hipStream_t s) {
@@ -243,7 +418,7 @@ hipError_t launch_gemm_i8(const int8_t *A, const int8_t *B, int32_t *C, int M, i
     const bool fast = (K % 16 == 0) && (N % 16 == 0) && (((uintptr_t)A & 15) == 0) && (((uintptr_t)B & 15) == 0) &&
                       (size_t)M * K < 0x80000000ull && (size_t)K * N < 0x80000000ull;
     if (fast)
-        hipLaunchKernelGGL(gemm_i8_kernel<true>, grid, block, 0, s, A, B, C, M, N, K, tiles_m, tiles_n);
+        hipLaunchKernelGGL(gemm_i8_dma_kernel, grid, block, 0, s, A, B, C, M, N, K, tiles_m, tiles_n);
     else
         hipLaunchKernelGGL(gemm_i8_kernel<false>, grid, block, 0, s, A, B, C, M, N, K, tiles_m, tiles_n);
     return hipGetLastError();
