@@ -180,6 +180,29 @@ int64_t gemm_host(Op op, int64_t a, int64_t b, int64_t c, int64_t m, int64_t k, 
     return 0;
 }
 
+// Q16 GEMV over nb vectors on device pointers: groups of up to 8 vectors go
+// to the MFMA kernel when the shape allows it (and nb >= 2), the rest to the
+// one-vector VALU kernel.  `ws` must hold gemv8_workspace_bytes(K) when
+// gemv_ws_need() is non-zero.
+size_t gemv_ws_need(const int32_t *W, const int32_t *X, int64_t m, int64_t k, int64_t nb) {
+    if (nb < 2 || k == 0 || !det::gemv8_eligible(W, X, (int)m, (int)k)) return 0;
+    return det::gemv8_workspace_bytes((int)k);
+}
+
+hipError_t gemv_q16_any(const int32_t *W, const int32_t *X, int32_t *Y, int64_t m, int64_t k, int64_t nb, void *ws,
+                        hipStream_t s) {
+    const int M = (int)m, K = (int)k;
+    if (K == 0) return zero_i32(Y, (size_t)m * nb, s);
+    if (!ws || nb < 2) return det::launch_gemv_q16(W, X, Y, M, K, (int)nb, s);
+    for (int64_t b = 0; b < nb; b += 8) {
+        const int g = (int)(nb - b < 8 ? nb - b : 8);
+        hipError_t e = g >= 2 ? det::launch_gemv_q16_mfma(W, X + b * k, Y + b * m, M, K, g, ws, s)
+                              : det::launch_gemv_q16(W, X + b * k, Y + b * m, M, K, g, s);
+        if (e != hipSuccess) return e;
+    }
+    return hipSuccess;
+}
+
 // Host-pointer GEMV family (Q16 batched, int16).
 int64_t gemv_host(bool q16, int64_t w, int64_t x, int64_t y, int64_t m, int64_t k, int64_t nb) {
     if (bad_dims(m, k, nb)) return set_err(DET_ERR_ARG, "dimension out of range [0, 2^31)");
@@ -200,10 +223,12 @@ int64_t gemv_host(bool q16, int64_t w, int64_t x, int64_t y, int64_t m, int64_t 
     if (bytes_w) DET_HIP_CHECK(hipMemcpyAsync(io, (const void *)w, bytes_w, hipMemcpyHostToDevice, s));
     if (bytes_x) DET_HIP_CHECK(hipMemcpyAsync(io + off_x, (const void *)x, bytes_x, hipMemcpyHostToDevice, s));
     if (k == 0) DET_HIP_CHECK(zero_i32((int32_t *)(io + off_y), (size_t)nb * m, s));
-    else if (q16)
-        DET_HIP_CHECK(det::launch_gemv_q16((const int32_t *)io, (const int32_t *)(io + off_x),
-                                           (int32_t *)(io + off_y), (int)m, (int)k, (int)nb, s));
-    else
+    else if (q16) {
+        const int32_t *dW = (const int32_t *)io, *dX = (const int32_t *)(io + off_x);
+        const size_t need = gemv_ws_need(dW, dX, m, k, nb);
+        if ((rc = ensure(&ds.ws, &ds.ws_bytes, need))) return rc;
+        DET_HIP_CHECK(gemv_q16_any(dW, dX, (int32_t *)(io + off_y), m, k, nb, need ? ds.ws : nullptr, s));
+    } else
         DET_HIP_CHECK(det::launch_gemv_i16((const int16_t *)io, (const int16_t *)(io + off_x),
                                            (int32_t *)(io + off_y), (int)m, (int)k, s));
     DET_HIP_CHECK(hipMemcpyAsync((void *)y, io + off_y, bytes_y, hipMemcpyDeviceToHost, s));
@@ -337,8 +362,21 @@ int64_t det_gemv_q16_dev(const int32_t *w, const int32_t *x, int32_t *y, int64_t
     if (m == 0 || nb == 0) return 0;
     if (!y || ((!w || !x) && k > 0)) return set_err(DET_ERR_ARG, "null device pointer");
     hipStream_t s = (hipStream_t)stream;
-    if (k == 0) DET_HIP_CHECK(zero_i32(y, (size_t)m * nb, s));
-    else DET_HIP_CHECK(det::launch_gemv_q16(w, x, y, (int)m, (int)k, (int)nb, s));
+    const size_t need = gemv_ws_need(w, x, m, k, nb);
+    if (need == 0) {
+        DET_HIP_CHECK(gemv_q16_any(w, x, y, m, k, nb, nullptr, s));
+        return 0;
+    }
+    int64_t rc = 0;
+    const int d = cur_device(&rc);
+    if (d < 0) return rc;
+    DevState &ds = g_dev[d];
+    std::lock_guard<std::mutex> lock(ds.mu);
+    if ((rc = ensure_stream(ds))) return rc;
+    if ((rc = ensure(&ds.ws, &ds.ws_bytes, need))) return rc;
+    DET_HIP_CHECK(hipStreamWaitEvent(s, ds.ws_free, 0));
+    DET_HIP_CHECK(gemv_q16_any(w, x, y, m, k, nb, ds.ws, s));
+    DET_HIP_CHECK(hipEventRecord(ds.ws_free, s));
     return 0;
 }
 

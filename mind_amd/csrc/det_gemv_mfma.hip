@@ -1,0 +1,292 @@
+// det_gemv_mfma.hip -- exact Q16.16 GEMV for several query vectors at once:
+// S on the int8 MFMA, the per-term residue on the VALU.
+//
+//   y[b][i] = (int32) sum_k ( (int64)W[i,k] * (int64)x[b][k]  >>arith 16 ),  b < nb <= 8
+// (the batched form of __mind_blas_gemv_q16_mt: reference src/mlir/lowering.rs:
+// 9822-9997; oracle benches/det_gemv_q16_mt.rs:186-197).
+//
+// Why: the one-vector kernel (det_gemv.hip) spends ~8 VALU slots per term on
+// the 64-bit product; with 8 vectors that is ~4x the VALU budget HBM speed
+// allows.  Here, per W element, the VALU only splits W into limbs (3 ops) and
+// computes the residue for each vector (1 op per term):
+//   * S = sum_k W x exactly (mod 2^48) from int8 limb-pair MFMAs with the
+//     bias identity (see det_gemm_limb.hip): W and x are written as signed
+//     int8 limbs t_p (low bytes biased by -128 = u ^ 0x80), c = 0x808080,
+//     sum W x = sum T(W)T(x) + c sum W + c sum x - K c^2, and
+//     sum T(W)T(x) = sum_{p+q<=5} 2^{8(p+q)} sum_k t_p(W) t_q(x).
+//     v_mfma_i32_16x16x64_i8 with 16 W rows as A and the query vectors as the
+//     16 B columns (nb used, column 8 = a ones vector in limb 0, which yields
+//     sum_k t_p(W) -- the row sums -- for free).
+//   * R = sum_k ((W x) mod 2^16) = sum_k ((lo16 W * lo16 x) mod 2^16) with
+//     v_pk_mul_lo_u16 + v_dot2_u32_u16 (two terms per pair of ops).
+//   * y = (int32)(((S - R) mod 2^48) >> 16).
+// Exactness bounds: K <= 32768 keeps the exact shift-0 / shift-1 MFMA sets
+// below 2^31 (|t_p t_q| <= 2^14) and R below 2^32; sets with shift >= 2 only
+// need their value mod 2^32 (i32 wrap-around).
+//
+// Layout: a prep kernel rewrites the (small) query vectors into MFMA B
+// operands (xp) and packed low halves (xl) in exactly the per-lane K order
+// the main kernel uses; W is streamed once, straight from HBM into registers
+// (buffer loads four K steps ahead), and split into limb planes with v_perm.
+// Lane l of a wave handles W row (l & 15) and, within each 64-wide K step,
+// the K indices {16 j + 4 (l >> 4) + e : j, e < 4}; any consistent K order
+// of the A and B operands gives the exact dot product.
+#include "det_common.h"
+#include "det_kernels.h"
+
+namespace det {
+namespace gemv8 {
+
+constexpr int THREADS = 256, DEPTH = 4;
+constexpr uint32_t BIAS = 0x00808080u;
+
+// One 256-thread block per 64-wide K step s.
+__global__ __launch_bounds__(256) void prep_kernel(const int32_t *__restrict__ X, int nb, int K,
+                                                   uint4 *__restrict__ xp, uint4 *__restrict__ xl,
+                                                   unsigned long long *__restrict__ colsum) {
+    const int s = blockIdx.x, t = threadIdx.x;
+    {   // xp[s][plane q][lane l]: 16 limb bytes of column b = l & 15, group g = l >> 4
+        const int q = t >> 6, l = t & 63, b = l & 15, g = l >> 4;
+        uint32_t w[4];
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            uint32_t v = 0;
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                const int k = 64 * s + 16 * j + 4 * g + e;
+                uint32_t byte;
+                if (b < nb) byte = (((uint32_t)X[(size_t)b * K + k] ^ BIAS) >> (8 * q)) & 0xffu;
+                else byte = (b == 8 && q == 0) ? 1u : 0u;
+                v |= byte << (8 * e);
+            }
+            w[j] = v;
+        }
+        xp[((size_t)s * 4 + q) * 64 + l] = make_uint4(w[0], w[1], w[2], w[3]);
+    }
+    if (t < 64) {   // xl[s][j][bp][g]: low halves of vectors 2bp, 2bp+1 at K 16j+4g+{0,1},{2,3}
+                    // (g fastest: the four K groups read adjacent 16-byte slots, no bank conflict)
+        const int g = t >> 4, j = (t >> 2) & 3, bp = t & 3;
+        uint32_t d[4];
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+            const int b = 2 * bp + h;
+#pragma unroll
+            for (int pr = 0; pr < 2; ++pr) {
+                const int k0 = 64 * s + 16 * j + 4 * g + 2 * pr;
+                const uint32_t lo = b < nb ? ((uint32_t)X[(size_t)b * K + k0] & 0xffffu) : 0u;
+                const uint32_t hi = b < nb ? ((uint32_t)X[(size_t)b * K + k0 + 1] & 0xffffu) : 0u;
+                d[2 * h + pr] = lo | (hi << 16);
+            }
+        }
+        xl[(((size_t)s * 4 + j) * 4 + bp) * 4 + g] = make_uint4(d[0], d[1], d[2], d[3]);
+    }
+    if (t < 8 && t < nb) {   // exact column sums, one integer atomic per vector per step
+        long long sum = 0;
+        for (int k = 64 * s; k < 64 * s + 64; ++k) sum += X[(size_t)t * K + k];
+        atomicAdd(colsum + t, (unsigned long long)sum);
+    }
+}
+
+__global__ void zero8(unsigned long long *p) {
+    if (threadIdx.x < 8) p[threadIdx.x] = 0;
+}
+
+__device__ __forceinline__ uint32_t residue2(uint32_t w2, uint32_t x2, uint32_t acc) {
+    // two 16-bit residues (lo16 w * lo16 x mod 2^16) added into acc
+    const v2u16 one = {1, 1};
+    return __builtin_amdgcn_udot2(__builtin_bit_cast(v2u16, w2) * __builtin_bit_cast(v2u16, x2), one, acc, false);
+}
+
+// One block = 8 waves (2 per SIMD, so one wave's LDS / MFMA latency hides
+// behind the other's VALU work) on 64 W rows: wave w takes rows
+// 16 (w & 3) .. +16 and K half (w >> 2).  The query operands of a chunk of CH
+// K steps of both halves (xp: 4 KiB per step, xl: 1 KiB per step) are staged
+// in LDS, double buffered, by all threads through registers: LDS reads wait
+// on lgkmcnt, so the only vector-memory loads a step waits for are its own W
+// rows, kept DEPTH steps ahead in a register ring (vmcnt retires in order,
+// so mixing other loads into that stream would drain the ring).  The staging
+// loads of chunk c+1 are issued at the start of chunk c and written to LDS
+// at its end.  The two K halves are combined exactly at the end (int64 for
+// the exact shift-0/1 sets).
+// Requires K % 512 == 0, K <= 32768, W < 2^31 bytes, nb <= 8.
+constexpr int CH = 4;                                   // K steps per LDS chunk (per half)
+constexpr int XP_CH = CH * 4 * 64, XL_CH = CH * 64;     // uint4 per chunk per half
+constexpr int X_HALF = XP_CH + XL_CH;                   // 1280 uint4 = 20 KiB
+constexpr int WAVES = 8, THREADS8 = WAVES * 64;
+constexpr int STAGE_PER_THREAD = 2 * X_HALF / THREADS8; // 5
+struct Tail {                                           // post-loop reduction (aliases the staging)
+    int32_t acc[WAVES][6][16][17];
+    uint32_t r[WAVES][16][8];
+};
+constexpr int SMEM_BYTES = sizeof(Tail) > 2 * 2 * X_HALF * 16 ? sizeof(Tail) : 2 * 2 * X_HALF * 16;
+
+__global__ __launch_bounds__(THREADS8, 1) void gemv8_kernel(const int32_t *__restrict__ W,
+                                                            const uint4 *__restrict__ xp,
+                                                            const uint4 *__restrict__ xl,
+                                                            const unsigned long long *__restrict__ colsum,
+                                                            int32_t *__restrict__ Y, int M, int K, int nb) {
+    __shared__ __attribute__((aligned(16))) char smem[SMEM_BYTES];
+    uint4 *s_x = (uint4 *)smem;                       // [2 buffers][2 halves][X_HALF]
+    Tail &tail = *(Tail *)smem;
+
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int r = lane & 15, g = lane >> 4;
+    const int rg = wave & 3, kh = wave >> 2;
+    const int row0 = blockIdx.x * 64 + rg * 16;
+    const int myrow = min(row0 + r, M - 1);
+    const __amdgpu_buffer_rsrc_t rw = make_rsrc(W, (uint32_t)M * (uint32_t)K * 4u);
+    const int nsteps = K / 64, half = nsteps / 2, nch = half / CH;
+    const int sbeg = kh * half;
+    const uint32_t wbase = ((uint32_t)myrow * (uint32_t)K + 4u * g) * 4u;   // bytes
+
+    // staging of chunk c (both halves): element e -> half e / X_HALF, then xp or xl
+    uint4 stg[STAGE_PER_THREAD];
+    auto stage_load = [&](int c) {
+#pragma unroll
+        for (int i = 0; i < STAGE_PER_THREAD; ++i) {
+            const int e = i * THREADS8 + tid;
+            const int h = e >= X_HALF ? 1 : 0, f = e - h * X_HALF;
+            const int cstep = h * half / CH + c;   // chunk index in the global step order
+            stg[i] = f < XP_CH ? xp[(size_t)cstep * XP_CH + f] : xl[(size_t)cstep * XL_CH + (f - XP_CH)];
+        }
+    };
+    auto stage_store = [&](int buf) {
+#pragma unroll
+        for (int i = 0; i < STAGE_PER_THREAD; ++i) s_x[buf * 2 * X_HALF + i * THREADS8 + tid] = stg[i];
+    };
+
+    v4i32 acc[6];
+#pragma unroll
+    for (int i = 0; i < 6; ++i) acc[i] = (v4i32){0, 0, 0, 0};
+    uint32_t racc[8];
+#pragma unroll
+    for (int b = 0; b < 8; ++b) racc[b] = 0;
+
+    stage_load(0);
+    stage_store(0);
+    // W ring: DEPTH steps in flight; loads past the end read out of range
+    uint4 wb[DEPTH][4];
+#pragma unroll
+    for (int d = 0; d < DEPTH; ++d)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) wb[d][j] = buf_load16(rw, wbase + (uint32_t)(64 * (sbeg + d) + 16 * j) * 4u);
+    __syncthreads();
+
+    for (int c = 0; c < nch; ++c) {
+        const int buf = c & 1;
+        stage_load(c + 1 < nch ? c + 1 : c);   // branch-free; the last reload is unused
+        __builtin_amdgcn_sched_barrier(0);      // keep its LDS stores at the end of the chunk
+        const uint4 *sxp = s_x + (buf * 2 + kh) * X_HALF;
+        const uint4 *sxl = sxp + XP_CH;
+#pragma unroll
+        for (int d8 = 0; d8 < CH; ++d8) {
+            const int d = d8 % DEPTH;
+            const int ls = c * CH + d8;         // step within this wave's half
+            const int st = sbeg + ls;
+            uint4 w[4];
+#pragma unroll
+            for (int j = 0; j < 4; ++j) w[j] = wb[d][j];
+#pragma unroll
+            for (int j = 0; j < 4; ++j)
+                wb[d][j] = buf_load16(rw, ls + DEPTH < half ? wbase + (uint32_t)(64 * (st + DEPTH) + 16 * j) * 4u
+                                                            : OOB_OFFSET);
+            v2i64 B[4];
+#pragma unroll
+            for (int q = 0; q < 4; ++q) B[q] = __builtin_bit_cast(v2i64, sxp[(d8 * 4 + q) * 64 + lane]);
+            // A operands: W limb planes (byte p of W ^ BIAS for 16 K)
+            uint32_t T[4][4];
+#pragma unroll
+            for (int j = 0; j < 4; ++j)
+                transpose4x4(w[j].x ^ BIAS, w[j].y ^ BIAS, w[j].z ^ BIAS, w[j].w ^ BIAS, T[j][0], T[j][1], T[j][2],
+                             T[j][3]);
+#pragma unroll
+            for (int p = 0; p < 4; ++p) {
+                const v2i64 A = __builtin_bit_cast(v2i64, (v4i32){(int)T[0][p], (int)T[1][p], (int)T[2][p], (int)T[3][p]});
+#pragma unroll
+                for (int q = 0; q < 4; ++q)
+                    if (p + q <= 5) acc[p + q] = mfma16x16x64(A, B[q], acc[p + q]);
+            }
+            // residues for every query vector
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                const uint32_t L0 = perm(w[j].y, w[j].x, 0x05040100u);   // lo16 of K e=0,1
+                const uint32_t L1 = perm(w[j].w, w[j].z, 0x05040100u);   // lo16 of K e=2,3
+#pragma unroll
+                for (int bp = 0; bp < 4; ++bp) {
+                    const uint4 xv = sxl[((d8 * 4 + j) * 4 + bp) * 4 + g];
+                    racc[2 * bp] = residue2(L1, xv.y, residue2(L0, xv.x, racc[2 * bp]));
+                    racc[2 * bp + 1] = residue2(L1, xv.w, residue2(L0, xv.z, racc[2 * bp + 1]));
+                }
+            }
+        }
+        __builtin_amdgcn_sched_barrier(0);
+        stage_store(buf ^ 1);   // buffer buf ^ 1 was last read in chunk c - 1
+        __syncthreads();
+    }
+
+    // residue: sum the four K groups of each row (lanes r, r+16, r+32, r+48)
+#pragma unroll
+    for (int b = 0; b < 8; ++b) {
+        racc[b] += __shfl_xor(racc[b], 16);
+        racc[b] += __shfl_xor(racc[b], 32);
+    }
+    // (the loop ended with a barrier: the staging area is free for the tail)
+#pragma unroll
+    for (int sft = 0; sft < 6; ++sft)
+#pragma unroll
+        for (int e = 0; e < 4; ++e) tail.acc[wave][sft][4 * g + e][r] = acc[sft][e];
+    if (g == 0)
+#pragma unroll
+        for (int b = 0; b < 8; ++b) tail.r[wave][r][b] = racc[b];
+    __syncthreads();
+    // 64 rows x 8 vectors = 512 outputs, one per thread, summing both K halves
+    const int rgo = tid >> 7, row = (tid >> 3) & 15, b = tid & 7;
+    const int grow = blockIdx.x * 64 + rgo * 16 + row;
+    if (b >= nb || grow >= M) return;
+    const unsigned long long cb = 0x808080ull;
+    const unsigned long long kc = (unsigned long long)(unsigned)K * cb;
+    long long tw = 0, s0x = 0, s1x = 0;
+    uint32_t hi[4] = {0, 0, 0, 0}, rsum = 0;
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+        const int wv = h * 4 + rgo;
+#pragma unroll
+        for (int sft = 0; sft < 4; ++sft) tw += (long long)tail.acc[wv][sft][row][8] * (1ll << (8 * sft));
+        s0x += tail.acc[wv][0][row][b];
+        s1x += tail.acc[wv][1][row][b];
+#pragma unroll
+        for (int sft = 2; sft < 6; ++sft) hi[sft - 2] += (uint32_t)tail.acc[wv][sft][row][b];
+        rsum += tail.r[wv][row][b];
+    }
+    const unsigned long long rowsum = (unsigned long long)tw + kc;   // sum_k W[row, k]
+    unsigned long long S = cb * (rowsum + colsum[b]) - kc * cb;
+    S += (unsigned long long)s0x + ((unsigned long long)s1x << 8);
+#pragma unroll
+    for (int sft = 2; sft < 6; ++sft) S += (unsigned long long)hi[sft - 2] << (8 * sft);
+    S -= (unsigned long long)rsum;
+    Y[(size_t)b * M + grow] = (int32_t)(uint32_t)(S >> 16);
+}
+
+}  // namespace gemv8
+
+size_t gemv8_workspace_bytes(int K) { return (size_t)K * 64 + (size_t)K * 16 + 64; }
+
+bool gemv8_eligible(const int32_t *W, const int32_t *X, int M, int K) {
+    return M >= 16 && K % 512 == 0 && K <= 32768 && (size_t)M * K * 4 < 0x80000000ull &&
+           ((uintptr_t)W & 15) == 0 && ((uintptr_t)X & 3) == 0;
+}
+
+// X: [nb][K] with nb <= 8, Y: [nb][M].  Requires gemv8_eligible.
+hipError_t launch_gemv_q16_mfma(const int32_t *W, const int32_t *X, int32_t *Y, int M, int K, int nb, void *ws,
+                                hipStream_t s) {
+    using namespace gemv8;
+    uint4 *xp = (uint4 *)ws;
+    uint4 *xl = xp + (size_t)K / 64 * 4 * 64;
+    unsigned long long *colsum = (unsigned long long *)(xl + (size_t)K / 64 * 64);
+    hipLaunchKernelGGL(zero8, dim3(1), dim3(64), 0, s, colsum);
+    hipLaunchKernelGGL(prep_kernel, dim3(K / 64), dim3(256), 0, s, X, nb, K, xp, xl, colsum);
+    hipLaunchKernelGGL(gemv8_kernel, dim3((M + 63) / 64), dim3(THREADS8), 0, s, W, xp, xl, colsum, Y, M, K, nb);
+    return hipGetLastError();
+}
+
+}  // namespace det
