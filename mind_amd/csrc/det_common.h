@@ -97,7 +97,36 @@ __device__ __forceinline__ int xcd_remap(int wg, int nwg) {
     return x * (per + 1) + per;          // x < rem here
 }
 
+// ---------------------------------------------------------------- LDS DMA
+typedef __attribute__((address_space(3))) int8_t *lds_i8_ptr;
+
+// Raw buffer descriptor as four SGPR words (base, stride 0, num_records,
+// gfx9 data-format word) for the inline-assembly DMA below.  bytes < 2^31.
+__device__ __forceinline__ v4i32 rsrc_words(const void *base, uint32_t bytes) {
+    const uint64_t a = (uint64_t)(uintptr_t)base;
+    return (v4i32){(int)(uint32_t)a, (int)(uint32_t)(a >> 32) & 0xffff, (int)bytes, 0x00020000};
+}
+// One buffer_load_dwordx4 ... lds: lane i's 16 bytes at `voff` land at LDS
+// byte lds + 16 i (an offset past num_records lands zeros).  Written as
+// inline assembly so the compiler's wait-count pass does not treat every
+// later LDS read as dependent on it (it would drain all loads in flight); a
+// kernel using it orders these loads itself with explicit s_waitcnt vmcnt
+// and s_barrier, and issues no other vector-memory loads while they are
+// outstanding.
+__device__ __forceinline__ void dma16(v4i32 rsrc, uint32_t lds, int voff) {
+    asm volatile("s_mov_b32 m0, %0\n\tbuffer_load_dwordx4 %1, %2, 0 offen lds" ::"s"(lds), "v"(voff), "s"(rsrc)
+                 : "memory", "m0");
+}
+__device__ __forceinline__ uint32_t lds_addr(const void *p) {
+    return __builtin_amdgcn_readfirstlane((uint32_t)(uintptr_t)(lds_i8_ptr)(const int8_t *)(p));
+}
+
 }  // namespace det
+
+// s_waitcnt with vmcnt <= n (n < 64), expcnt / lgkmcnt left unconstrained.
+#define DET_WAIT_VMCNT(n) __builtin_amdgcn_s_waitcnt(((n) & 15) | (7 << 4) | (15 << 8) | (((n) >> 4) << 14))
+// s_waitcnt lgkmcnt(0) only.
+#define DET_WAIT_LGKM0() __builtin_amdgcn_s_waitcnt(0xc07f & ~(15 << 8))
 
 // Host-side launch check shared by the entry points.
 #define DET_HIP_CHECK(expr)                                      \

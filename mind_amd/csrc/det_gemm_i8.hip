@@ -256,30 +256,6 @@ __global__ __launch_bounds__(THREADS, 1) void gemm_i8_kernel(const int8_t *__res
 constexpr int NSTAGE = 4;
 constexpr int DMA_PER_STAGE = 4;     // instructions per wave per stage
 
-typedef __attribute__((address_space(3))) int8_t *lds_i8_ptr;
-
-// Raw buffer descriptor as four SGPR words (base, stride 0, num_records,
-// gfx9 data-format word) for the inline-assembly DMA below.
-__device__ __forceinline__ v4i32 rsrc_words(const void *base, uint32_t bytes) {
-    const uint64_t a = (uint64_t)(uintptr_t)base;
-    return (v4i32){(int)(uint32_t)a, (int)(uint32_t)(a >> 32) & 0xffff, (int)bytes, 0x00020000};
-}
-// One buffer_load_dwordx4 ... lds: lane i's 16 bytes at `voff` land at LDS
-// byte lds + 16 i.  Written as inline assembly so the compiler's wait-count
-// pass does not treat every later LDS read as dependent on it (it would
-// drain all loads in flight); the kernel orders these loads itself with
-// explicit s_waitcnt vmcnt and s_barrier.  The kernel issues no other
-// vector-memory loads while these are outstanding.
-__device__ __forceinline__ void dma16(v4i32 rsrc, uint32_t lds, int voff) {
-    asm volatile("s_mov_b32 m0, %0\n\tbuffer_load_dwordx4 %1, %2, 0 offen lds" ::"s"(lds), "v"(voff), "s"(rsrc)
-                 : "memory", "m0");
-}
-__device__ __forceinline__ uint32_t lds_addr(const int8_t *p) {
-    return __builtin_amdgcn_readfirstlane((uint32_t)(uintptr_t)(lds_i8_ptr)(p));
-}
-
-// s_waitcnt with vmcnt <= n (n < 64), expcnt / lgkmcnt left unconstrained.
-#define DET_WAIT_VMCNT(n) __builtin_amdgcn_s_waitcnt(((n) & 15) | (7 << 4) | (15 << 8) | (((n) >> 4) << 14))
 
 __global__ __launch_bounds__(THREADS, 1) void gemm_i8_dma_kernel(const int8_t *__restrict__ A,
                                                                  const int8_t *__restrict__ B,
@@ -408,7 +384,6 @@ __global__ __launch_bounds__(THREADS, 1) void gemm_i8_dma_kernel(const int8_t *_
         }
     }
 }
-#undef DET_WAIT_VMCNT
 }  // namespace i8g
 
 hipError_t launch_gemm_i8(const int8_t *A, const int8_t *B, int32_t *C, int M, int N, int K, hipStream_t s) {

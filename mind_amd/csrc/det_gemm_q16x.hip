@@ -1,0 +1,430 @@
+// det_gemm_q16x.hip -- Q16.16 GEMM for K < 65536: limb-plane int8 MFMA for
+// the bilinear part, VALU residue for the per-term floor, 8 waves per tile.
+//
+// Semantics (reference src/mlir/lowering.rs:9300-9410, 7074-7676, oracle
+// benches/det_matmul_q16.rs:227-240):
+//     C[i,j] = (int32) sum_k ( (int64)A[i,k] * (int64)B[k,j]  >>arith 16 )
+// computed as C = (int32)(((S - R) mod 2^48) >> 16) with S = sum_k a b
+// (from 15 limb-pair int8 MFMAs plus the bias identity) and
+// R = sum_k ((lo16(a) lo16(b)) mod 2^16) (v_pk_mul_lo_u16 + v_dot2_u32_u16).
+// The derivation and the limb / bias algebra are the same as the first
+// generation kernel in det_gemm_limb.hip; this file changes the schedule:
+//
+//  * Prep: one wave per source row (A, or B^T) with no atomics, and a
+//    transposing 64x64 tile kernel for row-major B.  Both write the limb
+//    planes [p][rows][Kp] (K-contiguous, biased bytes), the low-16 halves
+//    [rows][Kp] and the exact int64 row / column sums.
+//  * Main kernel: 64x64 output tile per 512-thread workgroup, 48 KiB LDS
+//    stages (limb planes + low halves of A and B for 64 k) filled by
+//    direct global->LDS DMA two steps ahead (3 stages).  The waves are
+//    specialised: on each SIMD one "limb wave" runs the 15 limb-pair
+//    v_mfma_i32_32x32x32_i8 of a 32x32 quadrant (six shift-set
+//    accumulators) and issues the DMA, and one "residue wave" computes R for
+//    the whole tile over a quarter of each K step with an 8x8 output
+//    micro-tile per lane (0.5 LDS bytes per residue term).  On gfx950 an
+//    MFMA and a VALU operation of another wave on the same SIMD do not
+//    execute concurrently (measured), so the kernel is bounded by MFMA time
+//    plus residue VALU time per SIMD; the specialisation keeps each wave's
+//    instruction stream dense and the residue LDS traffic low.
+//  * Exactness: the limb waves cover the whole K, so the shift-0 set is
+//    bounded by K 2^14 and the shift-1 set by K 2^15 (exact in int32 for
+//    K < 2^16); each residue wave's partial is below (K/4) 2^16 and the sum
+//    of the four below K 2^16 < 2^32.  Sets with shift >= 2 only need their
+//    value mod 2^32.  The epilogue combines S, R and the bias terms in
+//    uint64 and keeps bits 16..47.
+#include "det_common.h"
+#include "det_kernels.h"
+
+namespace det {
+namespace q16x {
+
+constexpr int KP_ALIGN = 64;
+constexpr int BM = 64, BN = 64, BK = 64, THREADS = 512;
+constexpr int PT = BM * BK;             // bytes per limb-plane tile
+constexpr int LT = BM * BK * 2;         // bytes per low-16 tile
+constexpr int STAGE = 8 * PT + 2 * LT;  // A and B: 4 planes + low halves
+constexpr uint32_t BIAS4 = 0x80808080u;
+
+// Byte mask of the valid elements of dword d of a 16-element run with nv
+// valid elements (nv in [0, 16]).
+__device__ __forceinline__ uint32_t valid_mask(int nv, int d) {
+    const int r = nv - 4 * d;
+    return r >= 4 ? 0xffffffffu : (r <= 0 ? 0u : (1u << (8 * r)) - 1u);
+}
+
+// 16 consecutive Q16 values (zero where invalid) -> 4 limb-plane chunks of
+// 16 bytes (t_p = byte_p ^ 0x80 for p < 3, the signed top byte for p = 3,
+// 0 for invalid k) and 8 dwords of packed low-16 halves.
+__device__ __forceinline__ void split16(const uint32_t (&w)[16], int nv, uint4 (&pl)[4], uint4 (&lo)[2]) {
+    uint32_t e[4][4];
+#pragma unroll
+    for (int d = 0; d < 4; ++d) {
+        uint32_t e0, e1, e2, e3;
+        transpose4x4(w[4 * d], w[4 * d + 1], w[4 * d + 2], w[4 * d + 3], e0, e1, e2, e3);
+        const uint32_t x = BIAS4 & valid_mask(nv, d);
+        e[0][d] = e0 ^ x;
+        e[1][d] = e1 ^ x;
+        e[2][d] = e2 ^ x;
+        e[3][d] = e3;
+    }
+#pragma unroll
+    for (int p = 0; p < 4; ++p) pl[p] = make_uint4(e[p][0], e[p][1], e[p][2], e[p][3]);
+    uint32_t l[8];
+#pragma unroll
+    for (int h = 0; h < 8; ++h) l[h] = perm(w[2 * h + 1], w[2 * h], 0x05040100u);
+    lo[0] = make_uint4(l[0], l[1], l[2], l[3]);
+    lo[1] = make_uint4(l[4], l[5], l[6], l[7]);
+}
+
+// ------------------------------------------------------------------ prep
+// Rows of src[R][K] (operand A, or B given as B^T): one wave per row, lane
+// chunks of 16 k.  Also zeroes `zero[0..nzero)` (the other operand's sum
+// buffer, accumulated atomically by a later launch on the same stream).
+__global__ __launch_bounds__(256) void prep_rows_kernel(const int32_t *__restrict__ src, int R, int K, int Kp,
+                                                        uint8_t *__restrict__ planes, size_t plane_stride,
+                                                        uint16_t *__restrict__ lo16,
+                                                        unsigned long long *__restrict__ sums,
+                                                        unsigned long long *__restrict__ zero, int nzero) {
+    const int tid = threadIdx.x, lane = tid & 63;
+    for (int i = blockIdx.x * 256 + tid; i < nzero; i += gridDim.x * 256) zero[i] = 0;
+    const int row = blockIdx.x * 4 + (tid >> 6);
+    if (row >= R) return;
+    const int32_t *s = src + (size_t)row * K;
+    const bool vec = ((K & 3) == 0) && ((((uintptr_t)src) & 15) == 0);
+    long long sum = 0;
+    for (int k0 = lane * 16; k0 < Kp; k0 += 1024) {
+        const int nv = min(max(K - k0, 0), 16);
+        uint32_t w[16];
+        if (vec && nv == 16) {
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+                const uint4 v = *(const uint4 *)(s + k0 + 4 * q);
+                w[4 * q] = v.x, w[4 * q + 1] = v.y, w[4 * q + 2] = v.z, w[4 * q + 3] = v.w;
+            }
+        } else {
+#pragma unroll
+            for (int e = 0; e < 16; ++e) w[e] = e < nv ? (uint32_t)s[k0 + e] : 0u;
+        }
+#pragma unroll
+        for (int e = 0; e < 16; ++e) sum += (int32_t)w[e];
+        uint4 pl[4], lo[2];
+        split16(w, nv, pl, lo);
+        const size_t o = (size_t)row * Kp + k0;
+#pragma unroll
+        for (int p = 0; p < 4; ++p) *(uint4 *)(planes + p * plane_stride + o) = pl[p];
+        *(uint4 *)(lo16 + o) = lo[0];
+        *(uint4 *)(lo16 + o + 8) = lo[1];
+    }
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) sum += __shfl_xor(sum, off);
+    if (lane == 0) sums[row] = (unsigned long long)sum;
+}
+
+// Row-major B[K][N] -> B^T planes [p][N][Kp], low halves [N][Kp], column
+// sums (atomic; zeroed by prep_rows_kernel).  One 64 (k) x 64 (n) tile per
+// 256-thread workgroup; lane = 4 * column + k-quarter so that each column's
+// 64 plane bytes are written by four neighbouring lanes.
+__global__ __launch_bounds__(256) void prep_cols_kernel(const int32_t *__restrict__ src, int K, int N, int Kp,
+                                                        uint8_t *__restrict__ planes, size_t plane_stride,
+                                                        uint16_t *__restrict__ lo16,
+                                                        unsigned long long *__restrict__ sums) {
+    __shared__ int32_t tile[64][65];
+    const int n0 = blockIdx.x * 64, k0 = blockIdx.y * 64;
+    const int tid = threadIdx.x;
+    const bool vec = ((N & 3) == 0) && ((((uintptr_t)src) & 15) == 0);
+#pragma unroll
+    for (int pass = 0; pass < 4; ++pass) {
+        const int kr = (tid >> 4) + 16 * pass, c = (tid & 15) * 4;
+        const int k = k0 + kr, n = n0 + c;
+        uint32_t v[4] = {0, 0, 0, 0};
+        if (k < K) {
+            const int32_t *p = src + (size_t)k * N + n;
+            if (vec && n + 4 <= N) {
+                const uint4 q = *(const uint4 *)p;
+                v[0] = q.x, v[1] = q.y, v[2] = q.z, v[3] = q.w;
+            } else {
+#pragma unroll
+                for (int e = 0; e < 4; ++e) v[e] = n + e < N ? (uint32_t)p[e] : 0u;
+            }
+        }
+#pragma unroll
+        for (int e = 0; e < 4; ++e) tile[kr][c + e] = (int32_t)v[e];
+    }
+    __syncthreads();
+    const int lane = tid & 63, wave = tid >> 6;
+    const int nl = wave * 16 + (lane >> 2), kq = lane & 3;
+    const int n = n0 + nl, kb = k0 + kq * 16;
+    uint32_t w[16];
+    long long sum = 0;
+#pragma unroll
+    for (int e = 0; e < 16; ++e) {
+        w[e] = (uint32_t)tile[kq * 16 + e][nl];
+        sum += (int32_t)w[e];
+    }
+    const int nv = min(max(K - kb, 0), 16);
+    uint4 pl[4], lo[2];
+    split16(w, nv, pl, lo);
+    if (n < N) {
+        const size_t o = (size_t)n * Kp + kb;
+#pragma unroll
+        for (int p = 0; p < 4; ++p) *(uint4 *)(planes + p * plane_stride + o) = pl[p];
+        *(uint4 *)(lo16 + o) = lo[0];
+        *(uint4 *)(lo16 + o + 8) = lo[1];
+    }
+    sum += __shfl_xor(sum, 1);
+    sum += __shfl_xor(sum, 2);
+    if (kq == 0 && n < N) atomicAdd(sums + n, (unsigned long long)sum);
+}
+
+// ------------------------------------------------------------------ main
+// Limb-plane tile [64 rows][64 k]: 16-byte chunk ch of a row is stored at
+// chunk ch ^ ((row >> 2) & 3), so the 16 rows of an MFMA operand read hit 16
+// distinct 16-byte bank groups.
+__device__ __forceinline__ int swz_pl(int row, int ch) { return row * 64 + ((ch ^ ((row >> 2) & 3)) << 4); }
+// Low-16 tile [64 rows][64 k as u16]: chunk ch (8 k) at ch ^ ((row >> 3) & 7),
+// so the 8 rows 8*ly + i (ly = 0..7) read by one residue load are distinct.
+__device__ __forceinline__ int swz_lo(int row, int ch) { return row * 128 + ((ch ^ ((row >> 3) & 7)) << 4); }
+
+constexpr int NST = 3;   // LDS stages: the DMA runs two K steps ahead
+
+// Workspace offsets (bytes) of the four operand regions, all inside one
+// buffer descriptor: A planes, B^T planes, A low halves, B low halves.
+struct Q16xWs {
+    uint32_t a_plane, b_plane;   // bytes per limb plane (M*Kp, N*Kp)
+    uint32_t bp, alo, blo;       // region offsets from the workspace base
+    uint32_t bytes;              // total bytes of the four regions
+};
+
+// Residue partials in the epilogue: [4 K quarters][64 lanes][RP_STRIDE] u32
+// (a lane's 8x8 block at i*8 + j; the stride makes both the dump and the
+// MFMA-layout gather conflict-light).
+constexpr int RP_STRIDE = 72;
+
+// Wave roles (one of each per SIMD; waves w and w+4 share SIMD w):
+//  * waves 0..3 ("limb waves"): 32x32 quadrant w of the tile over the whole
+//    K: the 15 limb-pair MFMAs (shift sets s = p+q in six accumulators) and
+//    all of the DMA (12 loads per stage each).
+//  * waves 4..7 ("residue waves"): the whole 64x64 tile over K quarter w-4
+//    of every step: an 8x8 micro-tile per lane (rows 8*ly+i, columns
+//    8*lx+j), 16 LDS reads of 8 bytes per 256 VALU operations.
+// The residue is VALU work that no MFMA can do; giving it whole waves lets
+// the SIMD issue it back to back while the limb wave's MFMAs and LDS
+// traffic proceed beside it.
+__global__ __launch_bounds__(THREADS, 1) void q16x_kernel(
+    const uint8_t *__restrict__ ws, Q16xWs L,
+    const unsigned long long *__restrict__ rowsum, const unsigned long long *__restrict__ colsum,
+    int32_t *__restrict__ C, int M, int N, int Kp, int tiles_m, int tiles_n, unsigned long long kc2) {
+    __shared__ __attribute__((aligned(1024))) uint8_t smem[NST * STAGE];
+
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    // tile order: XCD-contiguous ids, then groups of 8 row tiles
+    const int ntiles = tiles_m * tiles_n;
+    const int pid = xcd_remap(blockIdx.x, ntiles);
+    constexpr int GM = 8;
+    const int group = pid / (GM * tiles_n), first = group * GM;
+    const int gsz = min(tiles_m - first, GM);
+    const int inner = pid - group * GM * tiles_n;
+    const int tm = first + inner % gsz, tn = inner / gsz;
+    const int m0 = tm * BM, n0 = tn * BN;
+    const int nk = Kp / BK;
+    uint32_t *sR = (uint32_t *)smem;   // epilogue residue partials
+
+    if (wave < 4) {
+        // ------------------------------------------------ limb waves
+        const int qm = wave >> 1, qn = wave & 1;
+        // DMA: a stage is 48 blocks of 1 KiB (A planes 0..15, B planes
+        // 16..31, A low halves 32..39, B low halves 40..47); limb wave w
+        // issues blocks 12w .. 12w+11.  Lane i of a block fills LDS slot i,
+        // so it loads the global chunk that the swizzle places there.
+        const v4i32 rw = rsrc_words(ws, L.bytes);
+        uint32_t doff[12];
+#pragma unroll
+        for (int j = 0; j < 12; ++j) {
+            const int b = 12 * wave + j;
+            if (b < 32) {
+                const int p = (b >> 2) & 3, sl = (b & 3) * 64 + lane;
+                const int row = sl >> 2, ch = (sl & 3) ^ ((row >> 2) & 3);
+                doff[j] = (b < 16 ? p * L.a_plane + (uint32_t)(m0 + row) * Kp
+                                  : L.bp + p * L.b_plane + (uint32_t)(n0 + row) * Kp) + ch * 16;
+            } else {
+                const int bb = b - 32, sl = (bb & 7) * 64 + lane;
+                const int row = sl >> 3, ch = (sl & 7) ^ ((row >> 3) & 7);
+                doff[j] = (bb < 8 ? L.alo + 2 * (uint32_t)(m0 + row) * Kp : L.blo + 2 * (uint32_t)(n0 + row) * Kp) +
+                          ch * 16;
+            }
+        }
+        auto issue = [&](int buf, int kt) {
+#pragma unroll
+            for (int j = 0; j < 12; ++j) {
+                const int b = 12 * wave + j;
+                const uint32_t step = b < 32 ? BK : 2 * BK;
+                dma16(rw, lds_addr(smem + buf * STAGE + b * 1024), (int)(doff[j] + (uint32_t)kt * step));
+            }
+        };
+        const int fr = lane & 31, fh = lane >> 5;
+        v16i32 acc[6];
+#pragma unroll
+        for (int s = 0; s < 6; ++s)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) acc[s][r] = 0;
+
+        issue(0, 0);
+        issue(1, nk > 1 ? 1 : 0);
+        DET_WAIT_VMCNT(12);   // step 0 landed
+        __builtin_amdgcn_s_barrier();
+        for (int kt = 0; kt < nk; ++kt) {
+            issue((kt + 2) % NST, kt + 2 < nk ? kt + 2 : nk - 1);
+            __builtin_amdgcn_sched_barrier(0);
+            const uint8_t *stg = smem + (kt % NST) * STAGE;
+#pragma unroll
+            for (int h = 0; h < 2; ++h) {   // two 32-wide K slices
+                v2i64 af[4], bf[4];
+#pragma unroll
+                for (int p = 0; p < 4; ++p) {
+                    af[p] = *(const v2i64 *)(stg + p * PT + swz_pl(qm * 32 + fr, 2 * h + fh));
+                    bf[p] = *(const v2i64 *)(stg + 4 * PT + p * PT + swz_pl(qn * 32 + fr, 2 * h + fh));
+                }
+#pragma unroll
+                for (int q = 0; q < 4; ++q)
+#pragma unroll
+                    for (int p = 0; p < 4; ++p)
+                        if (p + q <= 5) acc[p + q] = mfma32x32x32(af[p], bf[q], acc[p + q]);
+            }
+            __builtin_amdgcn_sched_barrier(0);
+            DET_WAIT_VMCNT(12);   // step kt+1 (issued one iteration ago) landed
+            DET_WAIT_LGKM0();
+            __builtin_amdgcn_s_barrier();
+        }
+        DET_WAIT_VMCNT(0);     // no load past the end may still write LDS
+        __syncthreads();       // stages free
+        __syncthreads();       // residue partials written
+        // combine in the MFMA layout: lane l, element r -> row 8(r>>2) +
+        // 4(l>>5) + (r&3), column l&31 of the quadrant
+        const int col_l = qn * 32 + (lane & 31);
+        const int col = n0 + col_l;
+        const unsigned long long c = 0x808080ull;
+        const unsigned long long cb = col < N ? colsum[col] : 0ull;
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+            const int row_l = qm * 32 + 8 * (r >> 2) + 4 * fh + (r & 3);
+            const int row = m0 + row_l;
+            const int ri = ((row_l >> 3) * 8 + (col_l >> 3)) * RP_STRIDE + (row_l & 7) * 8 + (col_l & 7);
+            const uint32_t R = sR[ri] + sR[64 * RP_STRIDE + ri] + sR[128 * RP_STRIDE + ri] + sR[192 * RP_STRIDE + ri];
+            if (row >= M || col >= N) continue;
+            const long long x = (long long)acc[0][r] + ((long long)acc[1][r] << 8) - (long long)R;
+            const uint32_t y = (uint32_t)acc[2][r] + ((uint32_t)acc[3][r] << 8) + ((uint32_t)acc[4][r] << 16) +
+                               ((uint32_t)acc[5][r] << 24);
+            const unsigned long long v =
+                (unsigned long long)x + ((unsigned long long)y << 16) + c * (rowsum[row] + cb) - kc2;
+            C[(size_t)row * N + col] = (int32_t)(uint32_t)(v >> 16);
+        }
+    } else {
+        // ------------------------------------------------ residue waves
+        const int kq = wave - 4;
+        const int ly = lane >> 3, lx = lane & 7;
+        uint32_t racc[8][8];
+#pragma unroll
+        for (int i = 0; i < 8; ++i)
+#pragma unroll
+            for (int j = 0; j < 8; ++j) racc[i][j] = 0;
+        const v2u16 one = {1, 1};
+        __builtin_amdgcn_s_barrier();   // step 0 landed
+        for (int kt = 0; kt < nk; ++kt) {
+            const uint8_t *sal = smem + (kt % NST) * STAGE + 8 * PT, *sbl = sal + LT;
+            // sub-chunk sc (4 k) of this wave's quarter: chunk 2*kq + (sc>>1),
+            // 8-byte half (sc & 1); reads run one sub-chunk ahead
+            uint2 av[2][8], bv[2][8];
+            auto rload = [&](int sc, uint2 (&a)[8], uint2 (&b)[8]) {
+                const int ch = 2 * kq + (sc >> 1), half = (sc & 1) * 8;
+#pragma unroll
+                for (int i = 0; i < 8; ++i) {
+                    a[i] = *(const uint2 *)(sal + swz_lo(8 * ly + i, ch) + half);
+                    b[i] = *(const uint2 *)(sbl + swz_lo(8 * lx + i, ch) + half);
+                }
+            };
+            rload(0, av[0], bv[0]);
+#pragma unroll
+            for (int sc = 0; sc < 4; ++sc) {
+                if (sc < 3) rload(sc + 1, av[(sc + 1) & 1], bv[(sc + 1) & 1]);
+                const uint2(&a)[8] = av[sc & 1];
+                const uint2(&b)[8] = bv[sc & 1];
+#pragma unroll
+                for (int w = 0; w < 2; ++w)
+#pragma unroll
+                    for (int i = 0; i < 8; ++i) {
+                        const uint32_t x = w ? a[i].y : a[i].x;
+                        uint32_t prod[8];
+#pragma unroll
+                        for (int j = 0; j < 8; ++j) {
+                            const uint32_t y = w ? b[j].y : b[j].x;
+                            prod[j] = __builtin_bit_cast(uint32_t,
+                                                         __builtin_bit_cast(v2u16, x) * __builtin_bit_cast(v2u16, y));
+                        }
+#pragma unroll
+                        for (int j = 0; j < 8; ++j)
+                            racc[i][j] = __builtin_amdgcn_udot2(__builtin_bit_cast(v2u16, prod[j]), one, racc[i][j], false);
+                    }
+            }
+            DET_WAIT_LGKM0();
+            __builtin_amdgcn_s_barrier();
+        }
+        __syncthreads();       // stages free (matches the limb waves)
+        uint32_t *dst = sR + (kq * 64 + lane) * RP_STRIDE;
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            *(uint4 *)(dst + i * 8) = make_uint4(racc[i][0], racc[i][1], racc[i][2], racc[i][3]);
+            *(uint4 *)(dst + i * 8 + 4) = make_uint4(racc[i][4], racc[i][5], racc[i][6], racc[i][7]);
+        }
+        __syncthreads();       // residue partials written
+    }
+}
+
+}  // namespace q16x
+
+bool q16x_eligible(int M, int N, int K) {
+    const long long Kp = ((long long)K + q16x::KP_ALIGN - 1) / q16x::KP_ALIGN * q16x::KP_ALIGN;
+    return K >= 1 && K < 65536 && 6LL * ((long long)M + N) * Kp < (1LL << 31);
+}
+
+// Workspace layout (same size as limb_workspace_bytes(M, N, K, 4, true)):
+// A planes [4][M][Kp], B^T planes [4][N][Kp], A low halves [M][Kp] u16,
+// B low halves [N][Kp] u16, row sums [M] u64, column sums [N] u64.
+hipError_t launch_gemm_q16x(const int32_t *A, const int32_t *B, int32_t *C, int M, int N, int K, bool b_is_t,
+                            void *ws, hipStream_t s) {
+    using namespace q16x;
+    const int Kp = (K + KP_ALIGN - 1) / KP_ALIGN * KP_ALIGN;
+    const size_t a_plane = (size_t)M * Kp, b_plane = (size_t)N * Kp;
+    uint8_t *Ap = (uint8_t *)ws;
+    uint8_t *Bp = Ap + 4 * a_plane;
+    uint16_t *Alo = (uint16_t *)(Bp + 4 * b_plane);
+    uint16_t *Blo = Alo + a_plane;
+    unsigned long long *rowsum = (unsigned long long *)(Blo + b_plane);
+    unsigned long long *colsum = rowsum + M;
+
+    if (b_is_t) {
+        hipLaunchKernelGGL(prep_rows_kernel, dim3((M + 3) / 4), dim3(256), 0, s, A, M, K, Kp, Ap, a_plane, Alo,
+                           rowsum, colsum, 0);
+        hipLaunchKernelGGL(prep_rows_kernel, dim3((N + 3) / 4), dim3(256), 0, s, B, N, K, Kp, Bp, b_plane, Blo,
+                           colsum, rowsum, 0);
+    } else {
+        hipLaunchKernelGGL(prep_rows_kernel, dim3((M + 3) / 4), dim3(256), 0, s, A, M, K, Kp, Ap, a_plane, Alo,
+                           rowsum, colsum, N);
+        hipLaunchKernelGGL(prep_cols_kernel, dim3((N + 63) / 64, Kp / 64), dim3(256), 0, s, B, K, N, Kp, Bp,
+                           b_plane, Blo, colsum);
+    }
+    const int tiles_m = (M + BM - 1) / BM, tiles_n = (N + BN - 1) / BN;
+    const unsigned long long kc2 = (unsigned long long)K * 0x808080ull * 0x808080ull;
+    Q16xWs L;
+    L.a_plane = (uint32_t)a_plane;
+    L.b_plane = (uint32_t)b_plane;
+    L.bp = (uint32_t)(Bp - Ap);
+    L.alo = (uint32_t)((uint8_t *)Alo - Ap);
+    L.blo = (uint32_t)((uint8_t *)Blo - Ap);
+    L.bytes = (uint32_t)((uint8_t *)(Blo + b_plane) - Ap);
+    hipLaunchKernelGGL(q16x_kernel, dim3(tiles_m * tiles_n), dim3(THREADS), 0, s, Ap, L, rowsum, colsum, C, M, N,
+                       Kp, tiles_m, tiles_n, kc2);
+    return hipGetLastError();
+}
+
+}  // namespace det

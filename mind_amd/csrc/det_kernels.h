@@ -22,6 +22,11 @@ inline size_t i16_workspace_bytes(int M, int N, int K) { return limb_workspace_b
 // Q16.16: B is [K][N], or [N][K] when b_is_t.
 hipError_t launch_gemm_q16(const int32_t *A, const int32_t *B, int32_t *C, int M, int N, int K, bool b_is_t,
                            void *ws, hipStream_t s);
+// Second-generation Q16 kernel (8 waves per tile, no flush): K <= 65536 and
+// 4 * max(M, N) * Kp < 2^31.  Same workspace as q16_workspace_bytes.
+bool q16x_eligible(int M, int N, int K);
+hipError_t launch_gemm_q16x(const int32_t *A, const int32_t *B, int32_t *C, int M, int N, int K, bool b_is_t,
+                            void *ws, hipStream_t s);
 hipError_t launch_gemm_i16(const int16_t *A, const int16_t *B, int32_t *C, int M, int N, int K, void *ws,
                            hipStream_t s);
 

@@ -176,12 +176,38 @@ def test_gemm_q16_saturating_config_and_bt():
     np.testing.assert_array_equal(c.reshape(m, n), want)
 
 
-def test_gemm_q16_long_k_flush():
-    # K > 16384 crosses the exact int64 flush of the low limb sets
+def test_gemm_q16_long_k_split_halves():
+    # K = 40000: each K half of the 8-wave kernel holds 20000 terms, close to
+    # the 32-bit bounds of its shift-0 / shift-1 sets and residue
     m, k, n = 16, 40000, 24
     a, b = O.gen_q16(0xF1A5, m * k, k * n, shift=0)
     note(f"det_matmul_q16 long-k {m}x{k}x{n}")
     np.testing.assert_array_equal(M.det_matmul_q16(a.reshape(m, k), b.reshape(k, n)), O.gemm_q16(a, b, m, k, n))
+
+
+def test_gemm_q16_long_k_flush():
+    # K > 65536 takes the flushing kernel (exact int64 totals every 16384 K)
+    m, k, n = 4, 70000, 5
+    a, b = O.gen_q16(0xF1A6, m * k, k * n, shift=0)
+    note(f"det_matmul_q16 flush {m}x{k}x{n}")
+    np.testing.assert_array_equal(M.det_matmul_q16(a.reshape(m, k), b.reshape(k, n)), O.gemm_q16(a, b, m, k, n))
+
+
+@pytest.mark.parametrize("gen", ["full", "sat"])
+def test_gemm_q16_multi_tile(gen):
+    # several 64x64 tiles, ragged in M and N, K not a multiple of 64
+    m, k, n = 200, 1000, 136
+    if gen == "full":
+        a, b = O.gen_q16(0x51DE, m * k, k * n, shift=0)
+    else:
+        a, b = O.gen_q16_sat(0x51DF, m * k, k * n, shift=13)
+    note(f"det_matmul_q16 {gen} {m}x{k}x{n}")
+    want = O.gemm_q16(a, b, m, k, n)
+    np.testing.assert_array_equal(M.det_matmul_q16(a.reshape(m, k), b.reshape(k, n)), want)
+    bt = np.ascontiguousarray(b.reshape(k, n).T)
+    c = np.zeros(m * n, np.int32)
+    call6("gemmq", a, bt, c, m, k, n)
+    np.testing.assert_array_equal(c.reshape(m, n), want)
 
 
 I16_SHAPES = [(1, 1, 1), (3, 5, 7), (64, 64, 64), (65, 127, 66), (200, 300, 100), (33, 2048, 17)]
