@@ -1,0 +1,165 @@
+// det_gemm_i16x.hip -- int16 GEMM as one int8 MFMA GEMM on interleaved limbs.
+//
+// Semantics (build-defined GEMM whose every element is the reference int16
+// dot, benches/det_matmul_i16.rs:218-224):
+//     C[i,j] = (int32) sum_k (int64)A[i,k] * (int64)B[k,j]   (mod 2^32)
+//
+// With the bias identity of det_gemm_limb.hip (a = T(a) + c, c = 0x80,
+// T(a) = t0 + 2^8 t1, t0 = low byte ^ 0x80 as int8, t1 = signed high byte):
+//     sum_k a b = sum_{x,y} 2^(8(x+y)) sum_k t_x(a) t_y(b)
+//                 + c sum_k a + c sum_k b - K c^2            (mod 2^32)
+// The four limb-pair sums are the 2x2 blocks of ONE int8 GEMM
+//     A2 [2M][Kp] (row 2i = t0(A row i), row 2i+1 = t1(A row i))
+//   x B2 [Kp][N2] (column 2j = t0(B column j), column 2j+1 = t1(B column j))
+// and B2 is simply B's bytes with each low byte XORed with 0x80.  The int8
+// DMA kernel (det_gemm_i8.hip) runs that GEMM and its EPI_I16 epilogue folds
+// each 2x2 block, with the bias terms, into one int32 output.  Every step is
+// mod 2^32, which is the i64 sum truncated to 32 bits: no flush, any K.
+//
+// Prep: prep_i16_a (one wave per A row: limb split, exact row sum, zeroes
+// the column-sum buffer) and prep_i16_b (64 x 128 tiles of B: the XOR, zero
+// padding, column sums by one atomic per column per tile).
+#include "det_common.h"
+#include "det_kernels.h"
+
+namespace det {
+
+hipError_t launch_gemm_i8_i16epi(const int8_t *A2, const int8_t *B2, int M2, int N2, int Kp, const uint32_t *rowsum,
+                                 const uint32_t *colsum, int32_t *C, int M16, int N16, int K16, hipStream_t s);
+
+namespace i16x {
+
+// Byte mask of the valid elements of dword d of a 16-element run with nv
+// valid elements (nv in [0, 16]).
+__device__ __forceinline__ uint32_t valid_mask(int nv, int d) {
+    const int r = nv - 4 * d;
+    return r >= 4 ? 0xffffffffu : (r <= 0 ? 0u : (1u << (8 * r)) - 1u);
+}
+
+// A [M][K] int16 -> A2 [2M][Kp] int8 limb rows, rowsum [M] (mod 2^32).
+__global__ __launch_bounds__(256) void prep_i16_a(const int16_t *__restrict__ src, int M, int K, int Kp,
+                                                  int8_t *__restrict__ A2, uint32_t *__restrict__ rowsum,
+                                                  uint32_t *__restrict__ zero, int nzero) {
+    const int tid = threadIdx.x, lane = tid & 63;
+    for (int i = blockIdx.x * 256 + tid; i < nzero; i += gridDim.x * 256) zero[i] = 0;
+    const int row = blockIdx.x * 4 + (tid >> 6);
+    if (row >= M) return;
+    const int16_t *s = src + (size_t)row * K;
+    const bool vec = ((K & 7) == 0) && ((((uintptr_t)src) & 15) == 0);
+    uint32_t sum = 0;
+    for (int k0 = lane * 16; k0 < Kp; k0 += 1024) {
+        const int nv = min(max(K - k0, 0), 16);
+        uint32_t d[8];   // 16 int16, two per dword
+        if (vec && nv == 16) {
+            const uint4 v0 = *(const uint4 *)(s + k0), v1 = *(const uint4 *)(s + k0 + 8);
+            d[0] = v0.x, d[1] = v0.y, d[2] = v0.z, d[3] = v0.w, d[4] = v1.x, d[5] = v1.y, d[6] = v1.z, d[7] = v1.w;
+        } else {
+#pragma unroll
+            for (int h = 0; h < 8; ++h) {
+                const uint32_t lo = 2 * h < nv ? (uint16_t)s[k0 + 2 * h] : 0u;
+                const uint32_t hi = 2 * h + 1 < nv ? (uint16_t)s[k0 + 2 * h + 1] : 0u;
+                d[h] = lo | (hi << 16);
+            }
+        }
+#pragma unroll
+        for (int h = 0; h < 8; ++h) sum += (uint32_t)(int32_t)(int16_t)(d[h] & 0xffff) + (uint32_t)((int32_t)d[h] >> 16);
+        uint32_t lo[4], hi[4];
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+            lo[q] = perm(d[2 * q + 1], d[2 * q], 0x06040200u) ^ (0x80808080u & valid_mask(nv, q));
+            hi[q] = perm(d[2 * q + 1], d[2 * q], 0x07050301u);
+        }
+        *(uint4 *)(A2 + (size_t)(2 * row) * Kp + k0) = make_uint4(lo[0], lo[1], lo[2], lo[3]);
+        *(uint4 *)(A2 + (size_t)(2 * row + 1) * Kp + k0) = make_uint4(hi[0], hi[1], hi[2], hi[3]);
+    }
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) sum += (uint32_t)__shfl_xor((int)sum, off);
+    if (lane == 0) rowsum[row] = sum;
+}
+
+// B [K][N] int16 -> B2 [Kp][N2] int8 (N2 = round_up(2N, 16)): the bytes of B
+// with every low byte ^ 0x80, zero in padding rows / columns; colsum [N]
+// (mod 2^32, atomic, zeroed by prep_i16_a).  256 threads per 64 x 128 tile:
+// thread t handles 8 columns (16 bytes) of rows (t >> 4) + 16 q, q = 0..3.
+__global__ __launch_bounds__(256) void prep_i16_b(const int16_t *__restrict__ src, int K, int N, int Kp, int N2,
+                                                  int8_t *__restrict__ B2, uint32_t *__restrict__ colsum) {
+    __shared__ uint32_t part[16][129];
+    const int tid = threadIdx.x, cg = tid & 15, rg = tid >> 4;
+    const int c0 = blockIdx.x * 128 + cg * 8;   // first int16 column of this thread
+    const int k0 = blockIdx.y * 64;
+    const bool vec = ((N & 7) == 0) && ((((uintptr_t)src) & 15) == 0);
+    uint32_t cs[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+    const bool out_col = 2 * c0 < N2;           // this 16-byte chunk exists in B2
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+        const int k = k0 + rg + 16 * q;
+        if (k >= Kp) continue;
+        uint32_t d[4] = {0, 0, 0, 0};
+        if (k < K) {
+            const int16_t *p = src + (size_t)k * N + c0;
+            if (vec && c0 + 8 <= N) {
+                const uint4 v = *(const uint4 *)p;
+                d[0] = v.x, d[1] = v.y, d[2] = v.z, d[3] = v.w;
+            } else {
+#pragma unroll
+                for (int h = 0; h < 4; ++h) {
+                    const uint32_t lo = c0 + 2 * h < N ? (uint16_t)p[2 * h] : 0u;
+                    const uint32_t hi = c0 + 2 * h + 1 < N ? (uint16_t)p[2 * h + 1] : 0u;
+                    d[h] = lo | (hi << 16);
+                }
+            }
+        }
+        uint32_t o[4];
+#pragma unroll
+        for (int h = 0; h < 4; ++h) {
+            cs[2 * h] += (uint32_t)(int32_t)(int16_t)(d[h] & 0xffff);
+            cs[2 * h + 1] += (uint32_t)((int32_t)d[h] >> 16);
+            // low byte ^ 0x80 for the valid columns only
+            const uint32_t m = (k < K ? (c0 + 2 * h < N ? 0x80u : 0u) | (c0 + 2 * h + 1 < N ? 0x800000u : 0u) : 0u);
+            o[h] = d[h] ^ m;
+        }
+        if (out_col) *(uint4 *)(B2 + (size_t)k * N2 + 2 * c0) = make_uint4(o[0], o[1], o[2], o[3]);
+    }
+#pragma unroll
+    for (int e = 0; e < 8; ++e) part[rg][cg * 8 + e] = cs[e];
+    __syncthreads();
+    if (tid < 128) {
+        uint32_t t = 0;
+#pragma unroll
+        for (int r = 0; r < 16; ++r) t += part[r][tid];
+        const int col = blockIdx.x * 128 + tid;
+        if (col < N) atomicAdd(colsum + col, t);
+    }
+}
+
+}  // namespace i16x
+
+static size_t align256(size_t x) { return (x + 255) & ~(size_t)255; }
+
+bool i16x_eligible(int M, int N, int K) {
+    const long long Kp = ((long long)K + 15) / 16 * 16, N2 = (2LL * N + 15) / 16 * 16;
+    return K >= 1 && 2LL * M * Kp < (1LL << 31) && Kp * N2 < (1LL << 31);
+}
+
+size_t i16x_workspace_bytes(int M, int N, int K) {
+    const size_t Kp = ((size_t)K + 15) / 16 * 16, N2 = (2 * (size_t)N + 15) / 16 * 16;
+    return align256(2 * (size_t)M * Kp) + align256(Kp * N2) + align256(4 * (size_t)M) + align256(4 * (size_t)N);
+}
+
+hipError_t launch_gemm_i16x(const int16_t *A, const int16_t *B, int32_t *C, int M, int N, int K, void *ws,
+                            hipStream_t s) {
+    using namespace i16x;
+    const int Kp = (K + 15) / 16 * 16, N2 = (2 * N + 15) / 16 * 16;
+    int8_t *A2 = (int8_t *)ws;
+    int8_t *B2 = A2 + align256(2 * (size_t)M * Kp);
+    uint32_t *rowsum = (uint32_t *)(B2 + align256((size_t)Kp * N2));
+    uint32_t *colsum = (uint32_t *)((int8_t *)rowsum + align256(4 * (size_t)M));
+    hipLaunchKernelGGL(prep_i16_a, dim3((M + 3) / 4), dim3(256), 0, s, A, M, K, Kp, A2, rowsum, colsum, N);
+    hipLaunchKernelGGL(prep_i16_b, dim3((N + 127) / 128, (Kp + 63) / 64), dim3(256), 0, s, B, K, N, Kp, N2, B2,
+                       colsum);
+    const hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return e;
+    return launch_gemm_i8_i16epi(A2, B2, 2 * M, N2, Kp, rowsum, colsum, C, M, N, K, s);
+}
+
+}  // namespace det

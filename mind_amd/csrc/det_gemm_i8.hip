@@ -257,10 +257,25 @@ constexpr int NSTAGE = 4;
 constexpr int DMA_PER_STAGE = 4;     // instructions per wave per stage
 
 
+// Epilogues of the DMA kernel.  EPI_I8: store C.  EPI_I16: the operands are
+// the int16 limb interleave built by the int16 prep (A'' row 2i / 2i+1 = low
+// / high limb of A row i, B'' column 2j / 2j+1 = low / high limb of B column
+// j), so each 2x2 block of the int8 product holds the four limb-pair sums of
+// one int16 output; the epilogue combines them (weights 1, 2^8, 2^8, 2^16)
+// and adds the bias terms, all mod 2^32.
+enum { EPI_I8 = 0, EPI_I16 = 1 };
+struct I16Epi {
+    const uint32_t *rowsum, *colsum;   // exact sums mod 2^32 of A rows / B columns
+    int32_t *C;                        // [M16][N16] int32
+    int M16, N16;
+    uint32_t bias_c, kc2;              // c = 0x80, K c^2 mod 2^32
+};
+
+template <int EPI>
 __global__ __launch_bounds__(THREADS, 1) void gemm_i8_dma_kernel(const int8_t *__restrict__ A,
                                                                  const int8_t *__restrict__ B,
                                                                  int32_t *__restrict__ C, int M, int N, int K,
-                                                                 int tiles_m, int tiles_n) {
+                                                                 int tiles_m, int tiles_n, I16Epi e16) {
     __shared__ __attribute__((aligned(1024))) int8_t smem[NSTAGE][2][TILE_BYTES];
 
     const int ntiles = tiles_m * tiles_n;
@@ -367,19 +382,78 @@ __global__ __launch_bounds__(THREADS, 1) void gemm_i8_dma_kernel(const int8_t *_
     // writing LDS when the workgroup ends
     DET_WAIT_VMCNT(0);
 
-    // Epilogue: lane holds C[8*(r >> 2) + 4*lh + (r & 3)][l32] of each 32x32
-    // block; a store instruction covers 32 consecutive columns (128 bytes).
+    if (EPI == EPI_I8) {
+        // lane holds C[8*(r >> 2) + 4*lh + (r & 3)][l32] of each 32x32 block;
+        // a store instruction covers 32 consecutive columns (128 bytes).
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
+        for (int i = 0; i < 4; ++i) {
 #pragma unroll
-        for (int r = 0; r < 16; ++r) {
-            const int row = m0 + wm + i * 32 + 8 * (r >> 2) + 4 * lh + (r & 3);
-            if (row >= M) continue;
-            int32_t *crow = C + (size_t)row * N;
+            for (int r = 0; r < 16; ++r) {
+                const int row = m0 + wm + i * 32 + 8 * (r >> 2) + 4 * lh + (r & 3);
+                if (row >= M) continue;
+                int32_t *crow = C + (size_t)row * N;
+#pragma unroll
+                for (int j = 0; j < 2; ++j) {
+                    const int col = n0 + wn + j * 32 + l32;
+                    if (col < N) __builtin_nontemporal_store(acc[i][j][r], crow + col);
+                }
+            }
+        }
+    } else {
+        // Elements 2p, 2p+1 of a lane are rows 2i', 2i'+1 (low / high A limb)
+        // of one column; lanes l, l^1 hold columns 2j', 2j'+1 (low / high B
+        // limb).  The even lane forms c00 + 2^8 c10, the odd lane
+        // 2^8 c01 + 2^16 c11; one exchange completes pairs 0..3 on the even
+        // lane and pairs 4..7 on the odd lane.  The 128x128 int16-output tile
+        // is staged in LDS (the stages are free) and written back with the
+        // bias terms as coalesced 16-byte rows.
+        constexpr int OS = 132;   // u32 row stride of the staged tile
+        uint32_t *sO = (uint32_t *)&smem[0][0][0];
+        __syncthreads();          // every wave is done with the stages
+        const bool odd = l32 & 1;
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
 #pragma unroll
             for (int j = 0; j < 2; ++j) {
-                const int col = n0 + wn + j * 32 + l32;
-                if (col < N) __builtin_nontemporal_store(acc[i][j][r], crow + col);
+                uint32_t part[8];
+#pragma unroll
+                for (int p = 0; p < 8; ++p) {
+                    const uint32_t lo = (uint32_t)acc[i][j][2 * p], hi = (uint32_t)acc[i][j][2 * p + 1];
+                    part[p] = odd ? (lo << 8) + (hi << 16) : lo + (hi << 8);
+                }
+                const int lc = (wn + j * 32 + l32) >> 1;
+#pragma unroll
+                for (int k = 0; k < 4; ++k) {
+                    const uint32_t recv = (uint32_t)__shfl_xor((int)(odd ? part[k] : part[4 + k]), 1);
+                    const int p = odd ? 4 + k : k;
+                    const int lr = (wm + i * 32 + 8 * (p >> 1) + 4 * lh + 2 * (p & 1)) >> 1;
+                    sO[lr * OS + lc] = (odd ? part[4 + k] : part[k]) + recv;
+                }
+            }
+        __syncthreads();
+        const int r0 = m0 >> 1, c0 = n0 >> 1;
+        const int cq = (tid & 31) * 4;             // 4 consecutive columns
+        const int col = c0 + cq;
+        uint32_t cs[4];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) cs[e] = col + e < e16.N16 ? e16.colsum[col + e] : 0u;
+        const bool vec = (e16.N16 & 3) == 0 && col + 4 <= e16.N16;
+#pragma unroll
+        for (int q = 0; q < 8; ++q) {
+            const int lr = (tid >> 5) + 16 * q, row = r0 + lr;
+            if (row >= e16.M16 || col >= e16.N16) continue;
+            const uint32_t rs = e16.rowsum[row];
+            const uint4 v = *(const uint4 *)(sO + lr * OS + cq);
+            uint32_t o[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+            for (int e = 0; e < 4; ++e) o[e] += e16.bias_c * (rs + cs[e]) - e16.kc2;
+            int32_t *dst = e16.C + (size_t)row * e16.N16 + col;
+            if (vec) {
+                __builtin_nontemporal_store(__builtin_bit_cast(v4i32, make_uint4(o[0], o[1], o[2], o[3])), (v4i32 *)dst);
+            } else {
+#pragma unroll
+                for (int e = 0; e < 4; ++e)
+                    if (col + e < e16.N16) dst[e] = (int32_t)o[e];
             }
         }
     }
@@ -393,9 +467,23 @@ hipError_t launch_gemm_i8(const int8_t *A, const int8_t *B, int32_t *C, int M, i
     const bool fast = (K % 16 == 0) && (N % 16 == 0) && (((uintptr_t)A & 15) == 0) && (((uintptr_t)B & 15) == 0) &&
                       (size_t)M * K < 0x80000000ull && (size_t)K * N < 0x80000000ull;
     if (fast)
-        hipLaunchKernelGGL(gemm_i8_dma_kernel, grid, block, 0, s, A, B, C, M, N, K, tiles_m, tiles_n);
+        hipLaunchKernelGGL(gemm_i8_dma_kernel<EPI_I8>, grid, block, 0, s, A, B, C, M, N, K, tiles_m, tiles_n,
+                           I16Epi{});
     else
         hipLaunchKernelGGL(gemm_i8_kernel<false>, grid, block, 0, s, A, B, C, M, N, K, tiles_m, tiles_n);
+    return hipGetLastError();
+}
+
+// int16 GEMM through the int8 DMA kernel on the limb interleave (see
+// det_gemm_i16x.hip): A2 [2*M16][Kp], B2 [Kp][N2] with Kp % 16 == 0,
+// N2 % 16 == 0, both 16-byte aligned, 2*M16*Kp and Kp*N2 below 2^31.
+hipError_t launch_gemm_i8_i16epi(const int8_t *A2, const int8_t *B2, int M2, int N2, int Kp, const uint32_t *rowsum,
+                                 const uint32_t *colsum, int32_t *C, int M16, int N16, int K16, hipStream_t s) {
+    using namespace i8g;
+    const int tiles_m = (M2 + BM - 1) / BM, tiles_n = (N2 + BN - 1) / BN;
+    I16Epi e{rowsum, colsum, C, M16, N16, 0x80u, (uint32_t)((uint64_t)(uint32_t)K16 * 0x4000u)};
+    hipLaunchKernelGGL(gemm_i8_dma_kernel<EPI_I16>, dim3(tiles_m * tiles_n), dim3(THREADS), 0, s, A2, B2,
+                       (int32_t *)nullptr, M2, N2, Kp, tiles_m, tiles_n, e);
     return hipGetLastError();
 }
 

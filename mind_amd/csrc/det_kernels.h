@@ -17,7 +17,7 @@ hipError_t launch_gemm_i8(const int8_t *A, const int8_t *B, int32_t *C, int M, i
 // halves (Q16) and exact row / column sums.
 size_t limb_workspace_bytes(int M, int N, int K, int np, bool q16);
 inline size_t q16_workspace_bytes(int M, int N, int K) { return limb_workspace_bytes(M, N, K, 4, true); }
-inline size_t i16_workspace_bytes(int M, int N, int K) { return limb_workspace_bytes(M, N, K, 2, false); }
+size_t i16_workspace_bytes(int M, int N, int K);   // covers both int16 paths below
 
 // Q16.16: B is [K][N], or [N][K] when b_is_t.
 hipError_t launch_gemm_q16(const int32_t *A, const int32_t *B, int32_t *C, int M, int N, int K, bool b_is_t,
@@ -29,6 +29,13 @@ hipError_t launch_gemm_q16x(const int32_t *A, const int32_t *B, int32_t *C, int 
                             void *ws, hipStream_t s);
 hipError_t launch_gemm_i16(const int16_t *A, const int16_t *B, int32_t *C, int M, int N, int K, void *ws,
                            hipStream_t s);
+// int16 as one int8 MFMA GEMM on interleaved limbs (det_gemm_i16x.hip):
+// eligible when 2*M*Kp and Kp*round_up(2N, 16) are below 2^31 (Kp = K
+// rounded up to 16).
+bool i16x_eligible(int M, int N, int K);
+size_t i16x_workspace_bytes(int M, int N, int K);
+hipError_t launch_gemm_i16x(const int16_t *A, const int16_t *B, int32_t *C, int M, int N, int K, void *ws,
+                            hipStream_t s);
 
 // Y[nb][M] = Q16 GEMV of W[M][K] with each X[b][K].
 hipError_t launch_gemv_q16(const int32_t *W, const int32_t *X, int32_t *Y, int M, int K, int nb, hipStream_t s);

@@ -210,7 +210,8 @@ def test_gemm_q16_multi_tile(gen):
     np.testing.assert_array_equal(c.reshape(m, n), want)
 
 
-I16_SHAPES = [(1, 1, 1), (3, 5, 7), (64, 64, 64), (65, 127, 66), (200, 300, 100), (33, 2048, 17)]
+I16_SHAPES = [(1, 1, 1), (3, 5, 7), (64, 64, 64), (65, 127, 66), (200, 300, 100), (33, 2048, 17),
+              (300, 1000, 270), (129, 16, 128)]
 
 
 @pytest.mark.parametrize("m,k,n", I16_SHAPES, ids=[f"{m}x{k}x{n}" for m, k, n in I16_SHAPES])
