@@ -139,20 +139,33 @@ __global__ __launch_bounds__(THREADS8, 1) void gemv8_kernel(const int32_t *__res
     const int sbeg = kh * half;
     const uint32_t wbase = ((uint32_t)myrow * (uint32_t)K + 4u * g) * 4u;   // bytes
 
-    // staging of chunk c (both halves): element e -> half e / X_HALF, then xp or xl
+    // staging of chunk c (both halves), one fixed source per slot: slots 0..1
+    // xp of half 0, slots 2..3 xp of half 1, slot 4 xl (half tid >> 8).
+    // Buffer loads with 32-bit offsets and no per-thread source select keep
+    // the address registers apart from the data, so the loads stay in flight
+    // (the wait is at the LDS store at the end of the chunk).
+    static_assert(STAGE_PER_THREAD == 5 && XP_CH == 2 * THREADS8 && XL_CH == THREADS8 / 2, "staging slots");
+    const __amdgpu_buffer_rsrc_t rxp = make_rsrc(xp, (uint32_t)K * 64u);
+    const __amdgpu_buffer_rsrc_t rxl = make_rsrc(xl, (uint32_t)K * 16u);
+    const int xl_h = tid >> 8, xl_f = tid & 255;
     uint4 stg[STAGE_PER_THREAD];
     auto stage_load = [&](int c) {
+        const uint32_t c0 = (uint32_t)c, c1 = (uint32_t)(half / CH + c);
 #pragma unroll
-        for (int i = 0; i < STAGE_PER_THREAD; ++i) {
-            const int e = i * THREADS8 + tid;
-            const int h = e >= X_HALF ? 1 : 0, f = e - h * X_HALF;
-            const int cstep = h * half / CH + c;   // chunk index in the global step order
-            stg[i] = f < XP_CH ? xp[(size_t)cstep * XP_CH + f] : xl[(size_t)cstep * XL_CH + (f - XP_CH)];
+        for (int i = 0; i < 2; ++i) {
+            stg[i] = buf_load16(rxp, ((c0 * XP_CH) + i * THREADS8 + tid) * 16u);
+            stg[2 + i] = buf_load16(rxp, ((c1 * XP_CH) + i * THREADS8 + tid) * 16u);
         }
+        stg[4] = buf_load16(rxl, (((xl_h ? c1 : c0) * XL_CH) + xl_f) * 16u);
     };
     auto stage_store = [&](int buf) {
+        uint4 *d = s_x + buf * 2 * X_HALF;
 #pragma unroll
-        for (int i = 0; i < STAGE_PER_THREAD; ++i) s_x[buf * 2 * X_HALF + i * THREADS8 + tid] = stg[i];
+        for (int i = 0; i < 2; ++i) {
+            d[i * THREADS8 + tid] = stg[i];
+            d[X_HALF + i * THREADS8 + tid] = stg[2 + i];
+        }
+        d[xl_h * X_HALF + XP_CH + xl_f] = stg[4];
     };
 
     v4i32 acc[6];
@@ -183,9 +196,17 @@ __global__ __launch_bounds__(THREADS8, 1) void gemv8_kernel(const int32_t *__res
             const int d = d8 % DEPTH;
             const int ls = c * CH + d8;         // step within this wave's half
             const int st = sbeg + ls;
-            uint4 w[4];
+            // consume the ring slot (limb transpose, low halves) before
+            // reloading it: the reload then reuses the same registers, so no
+            // register copy has to wait for a load still in flight
+            uint32_t T[4][4], L[4][2];
 #pragma unroll
-            for (int j = 0; j < 4; ++j) w[j] = wb[d][j];
+            for (int j = 0; j < 4; ++j) {
+                const uint4 w = wb[d][j];
+                transpose4x4(w.x ^ BIAS, w.y ^ BIAS, w.z ^ BIAS, w.w ^ BIAS, T[j][0], T[j][1], T[j][2], T[j][3]);
+                L[j][0] = perm(w.y, w.x, 0x05040100u);   // lo16 of K e=0,1
+                L[j][1] = perm(w.w, w.z, 0x05040100u);   // lo16 of K e=2,3
+            }
 #pragma unroll
             for (int j = 0; j < 4; ++j)
                 wb[d][j] = buf_load16(rw, ls + DEPTH < half ? wbase + (uint32_t)(64 * (st + DEPTH) + 16 * j) * 4u
@@ -194,11 +215,6 @@ __global__ __launch_bounds__(THREADS8, 1) void gemv8_kernel(const int32_t *__res
 #pragma unroll
             for (int q = 0; q < 4; ++q) B[q] = __builtin_bit_cast(v2i64, sxp[(d8 * 4 + q) * 64 + lane]);
             // A operands: W limb planes (byte p of W ^ BIAS for 16 K)
-            uint32_t T[4][4];
-#pragma unroll
-            for (int j = 0; j < 4; ++j)
-                transpose4x4(w[j].x ^ BIAS, w[j].y ^ BIAS, w[j].z ^ BIAS, w[j].w ^ BIAS, T[j][0], T[j][1], T[j][2],
-                             T[j][3]);
 #pragma unroll
             for (int p = 0; p < 4; ++p) {
                 const v2i64 A = __builtin_bit_cast(v2i64, (v4i32){(int)T[0][p], (int)T[1][p], (int)T[2][p], (int)T[3][p]});
@@ -209,8 +225,7 @@ __global__ __launch_bounds__(THREADS8, 1) void gemv8_kernel(const int32_t *__res
             // residues for every query vector
 #pragma unroll
             for (int j = 0; j < 4; ++j) {
-                const uint32_t L0 = perm(w[j].y, w[j].x, 0x05040100u);   // lo16 of K e=0,1
-                const uint32_t L1 = perm(w[j].w, w[j].z, 0x05040100u);   // lo16 of K e=2,3
+                const uint32_t L0 = L[j][0], L1 = L[j][1];
 #pragma unroll
                 for (int bp = 0; bp < 4; ++bp) {
                     const uint4 xv = sxl[((d8 * 4 + j) * 4 + bp) * 4 + g];
