@@ -40,11 +40,21 @@ namespace gemv8 {
 constexpr int THREADS = 256, DEPTH = 4;
 constexpr uint32_t BIAS = 0x00808080u;
 
-// One 256-thread block per 64-wide K step s.
+// One 256-thread block per 64-wide K step s: the step's slice of the query
+// vectors is staged in LDS (coalesced loads), then turned into the limb
+// planes xp, the low halves xl and the exact per-step column sums part[s][b]
+// (summed by the main kernel: no atomics, nothing to zero beforehand).
 __global__ __launch_bounds__(256) void prep_kernel(const int32_t *__restrict__ X, int nb, int K,
                                                    uint4 *__restrict__ xp, uint4 *__restrict__ xl,
-                                                   unsigned long long *__restrict__ colsum) {
+                                                   long long *__restrict__ part) {
+    __shared__ uint32_t xs[8][65];
     const int s = blockIdx.x, t = threadIdx.x;
+#pragma unroll
+    for (int e = t; e < 512; e += 256) {
+        const int b = e >> 6, k = e & 63;
+        xs[b][k] = b < nb ? (uint32_t)X[(size_t)b * K + 64 * s + k] : 0u;
+    }
+    __syncthreads();
     {   // xp[s][plane q][lane l]: 16 limb bytes of column b = l & 15, group g = l >> 4
         const int q = t >> 6, l = t & 63, b = l & 15, g = l >> 4;
         uint32_t w[4];
@@ -53,9 +63,9 @@ __global__ __launch_bounds__(256) void prep_kernel(const int32_t *__restrict__ X
             uint32_t v = 0;
 #pragma unroll
             for (int e = 0; e < 4; ++e) {
-                const int k = 64 * s + 16 * j + 4 * g + e;
+                const int k = 16 * j + 4 * g + e;
                 uint32_t byte;
-                if (b < nb) byte = (((uint32_t)X[(size_t)b * K + k] ^ BIAS) >> (8 * q)) & 0xffu;
+                if (b < nb) byte = ((xs[b][k] ^ BIAS) >> (8 * q)) & 0xffu;
                 else byte = (b == 8 && q == 0) ? 1u : 0u;
                 v |= byte << (8 * e);
             }
@@ -72,23 +82,17 @@ __global__ __launch_bounds__(256) void prep_kernel(const int32_t *__restrict__ X
             const int b = 2 * bp + h;
 #pragma unroll
             for (int pr = 0; pr < 2; ++pr) {
-                const int k0 = 64 * s + 16 * j + 4 * g + 2 * pr;
-                const uint32_t lo = b < nb ? ((uint32_t)X[(size_t)b * K + k0] & 0xffffu) : 0u;
-                const uint32_t hi = b < nb ? ((uint32_t)X[(size_t)b * K + k0 + 1] & 0xffffu) : 0u;
-                d[2 * h + pr] = lo | (hi << 16);
+                const int k0 = 16 * j + 4 * g + 2 * pr;
+                d[2 * h + pr] = (xs[b][k0] & 0xffffu) | (xs[b][k0 + 1] << 16);
             }
         }
         xl[(((size_t)s * 4 + j) * 4 + bp) * 4 + g] = make_uint4(d[0], d[1], d[2], d[3]);
-    }
-    if (t < 8 && t < nb) {   // exact column sums, one integer atomic per vector per step
+    } else if (t >= 64 && t < 72) {   // exact column sums of this step
         long long sum = 0;
-        for (int k = 64 * s; k < 64 * s + 64; ++k) sum += X[(size_t)t * K + k];
-        atomicAdd(colsum + t, (unsigned long long)sum);
+#pragma unroll 8
+        for (int k = 0; k < 64; ++k) sum += (int32_t)xs[t - 64][k];
+        part[(size_t)s * 8 + (t - 64)] = sum;
     }
-}
-
-__global__ void zero8(unsigned long long *p) {
-    if (threadIdx.x < 8) p[threadIdx.x] = 0;
 }
 
 __device__ __forceinline__ uint32_t residue2(uint32_t w2, uint32_t x2, uint32_t acc) {
@@ -123,7 +127,7 @@ constexpr int SMEM_BYTES = sizeof(Tail) > 2 * 2 * X_HALF * 16 ? sizeof(Tail) : 2
 __global__ __launch_bounds__(THREADS8, 1) void gemv8_kernel(const int32_t *__restrict__ W,
                                                             const uint4 *__restrict__ xp,
                                                             const uint4 *__restrict__ xl,
-                                                            const unsigned long long *__restrict__ colsum,
+                                                            const long long *__restrict__ part,
                                                             int32_t *__restrict__ Y, int M, int K, int nb) {
     __shared__ __attribute__((aligned(16))) char smem[SMEM_BYTES];
     uint4 *s_x = (uint4 *)smem;                       // [2 buffers][2 halves][X_HALF]
@@ -175,14 +179,26 @@ __global__ __launch_bounds__(THREADS8, 1) void gemv8_kernel(const int32_t *__res
 #pragma unroll
     for (int b = 0; b < 8; ++b) racc[b] = 0;
 
-    stage_load(0);
-    stage_store(0);
-    // W ring: DEPTH steps in flight; loads past the end read out of range
-    uint4 wb[DEPTH][4];
+    // prologue: W ring, chunk-0 staging and the column-sum partials all in
+    // flight together (one memory round trip)
+    uint4 wb[DEPTH][4];   // W ring: DEPTH steps in flight; loads past the end read out of range
 #pragma unroll
     for (int d = 0; d < DEPTH; ++d)
 #pragma unroll
         for (int j = 0; j < 4; ++j) wb[d][j] = buf_load16(rw, wbase + (uint32_t)(64 * (sbeg + d) + 16 * j) * 4u);
+    stage_load(0);
+    // column sums of the query vectors: thread t adds the per-step partials
+    // i = t/8 + 64 u (u < 8, K <= 32768) of vector t % 8 (finished in the tail)
+    long long pv[8];
+#pragma unroll
+    for (int u = 0; u < 8; ++u) {
+        const int i = (tid >> 3) + 64 * u;
+        pv[u] = i < 2 * half ? part[(size_t)i * 8 + (tid & 7)] : 0;
+    }
+    long long cpart = 0;
+#pragma unroll
+    for (int u = 0; u < 8; ++u) cpart += pv[u];
+    stage_store(0);
     __syncthreads();
 
     for (int c = 0; c < nch; ++c) {
@@ -253,6 +269,13 @@ __global__ __launch_bounds__(THREADS8, 1) void gemv8_kernel(const int32_t *__res
     if (g == 0)
 #pragma unroll
         for (int b = 0; b < 8; ++b) tail.r[wave][r][b] = racc[b];
+    // finish the column sums: lanes with equal (lane & 7) within the wave,
+    // then the eight waves
+    cpart += __shfl_xor(cpart, 8);
+    cpart += __shfl_xor(cpart, 16);
+    cpart += __shfl_xor(cpart, 32);
+    __shared__ long long s_cs[WAVES][8];
+    if (lane < 8) s_cs[wave][lane] = cpart;
     __syncthreads();
     // 64 rows x 8 vectors = 512 outputs, one per thread, summing both K halves
     const int rgo = tid >> 7, row = (tid >> 3) & 15, b = tid & 7;
@@ -274,7 +297,10 @@ __global__ __launch_bounds__(THREADS8, 1) void gemv8_kernel(const int32_t *__res
         rsum += tail.r[wv][row][b];
     }
     const unsigned long long rowsum = (unsigned long long)tw + kc;   // sum_k W[row, k]
-    unsigned long long S = cb * (rowsum + colsum[b]) - kc * cb;
+    long long colsum_b = 0;
+#pragma unroll
+    for (int w = 0; w < WAVES; ++w) colsum_b += s_cs[w][b];
+    unsigned long long S = cb * (rowsum + (unsigned long long)colsum_b) - kc * cb;
     S += (unsigned long long)s0x + ((unsigned long long)s1x << 8);
 #pragma unroll
     for (int sft = 2; sft < 6; ++sft) S += (unsigned long long)hi[sft - 2] << (8 * sft);
@@ -284,7 +310,7 @@ __global__ __launch_bounds__(THREADS8, 1) void gemv8_kernel(const int32_t *__res
 
 }  // namespace gemv8
 
-size_t gemv8_workspace_bytes(int K) { return (size_t)K * 64 + (size_t)K * 16 + 64; }
+size_t gemv8_workspace_bytes(int K) { return (size_t)K * 64 + (size_t)K * 16 + (size_t)K / 64 * 8 * 8; }
 
 bool gemv8_eligible(const int32_t *W, const int32_t *X, int M, int K) {
     return M >= 16 && K % 512 == 0 && K <= 32768 && (size_t)M * K * 4 < 0x80000000ull &&
@@ -297,10 +323,9 @@ hipError_t launch_gemv_q16_mfma(const int32_t *W, const int32_t *X, int32_t *Y, 
     using namespace gemv8;
     uint4 *xp = (uint4 *)ws;
     uint4 *xl = xp + (size_t)K / 64 * 4 * 64;
-    unsigned long long *colsum = (unsigned long long *)(xl + (size_t)K / 64 * 64);
-    hipLaunchKernelGGL(zero8, dim3(1), dim3(64), 0, s, colsum);
-    hipLaunchKernelGGL(prep_kernel, dim3(K / 64), dim3(256), 0, s, X, nb, K, xp, xl, colsum);
-    hipLaunchKernelGGL(gemv8_kernel, dim3((M + 63) / 64), dim3(THREADS8), 0, s, W, xp, xl, colsum, Y, M, K, nb);
+    long long *part = (long long *)(xl + (size_t)K / 64 * 64);
+    hipLaunchKernelGGL(prep_kernel, dim3(K / 64), dim3(256), 0, s, X, nb, K, xp, xl, part);
+    hipLaunchKernelGGL(gemv8_kernel, dim3((M + 63) / 64), dim3(THREADS8), 0, s, W, xp, xl, part, Y, M, K, nb);
     return hipGetLastError();
 }
 
