@@ -5,9 +5,10 @@ Headline (the ``value`` of the JSON line): det_matmul_i8 at 4096^3, int8 in,
 exact int32 out, in TOP/s (2*M*N*K / time).  A "step" is one call of the
 kernel over device-resident synthetic inputs (the reference bench LCG,
 benches/det_matmul_i8.rs:221-226).  The secondary configs of the same
-metric (Q16.16 GEMM 1024^3, int16 GEMM 2048^3, Q16 GEMV 16384^2 at batch 1
-and 8, the int8 MLP layer 4096x4096x11008 and the 8192^3 probe) are timed the
-same way and reported under "secondary".
+metric (Q16.16 GEMM 1024^3 and 4096^3, int16 GEMM 2048^3, Q16 GEMV 16384^2
+at batch 1 and 8, the int8 MLP layer 4096x4096x11008 and the 8192^3 probe)
+are timed the same way and reported under "secondary".  --vendor-ref adds,
+for context only, the vendor int8 GEMM (torch._int_mm) on the headline shape.
 
 Timing: HIP events recorded on the stream the kernels are launched on,
 around exactly K steps after W warm-up steps, with a device synchronisation
@@ -15,7 +16,7 @@ on both sides; ms_per_step is the host wall clock over the same region.
 Every timed output is checked bit-exact against the CPU oracle (sampled rows
 at these sizes) before its number is reported.
 
-Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--only i8_4096]
+Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--only q16_1024,...] [--vendor-ref]
 """
 from __future__ import annotations
 
@@ -138,6 +139,49 @@ def gemv_workload(m: int, k: int, nb: int, steps: int, warmup: int, stream, seed
     return {"ms": ev, "wall_ms": wall, "bytes": nbytes, "verify": verify, "checked_rows": len(rows)}
 
 
+def vendor_int8_child(steps: int) -> None:
+    """Child-process body of --vendor-ref: time the vendor int8 GEMM
+    (torch._int_mm, which dispatches to hipBLASLt on ROCm) on the headline
+    shape with torch's own events and print one JSON line.  B is passed
+    row-major (the reference ABI's layout) and, for comparison, column-major.
+    Context only, never part of the product path; it runs in its own process
+    because torch bundles its own HIP runtime."""
+    import torch
+    out = {"impl": "torch._int_mm (hipBLASLt)", "torch": torch.__version__}
+    m = k = n = 4096
+    a = torch.randint(-128, 128, (m, k), dtype=torch.int8, device="cuda")
+    b = torch.randint(-128, 128, (k, n), dtype=torch.int8, device="cuda")
+    for name, bb in (("b_row_major", b), ("b_col_major", b.t().contiguous().t())):
+        for _ in range(5):
+            torch._int_mm(a, bb)
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        for _ in range(steps):
+            torch._int_mm(a, bb)
+        e1.record()
+        torch.cuda.synchronize()
+        us = e0.elapsed_time(e1) / steps * 1e3
+        out[name] = {"us": round(us, 2), "tops": round(2.0 * m * n * k / us / 1e6, 1)}
+    print(json.dumps(out), flush=True)
+
+
+def vendor_int8_reference(steps: int) -> dict:
+    """Run vendor_int8_child in a child process.  Called before this process
+    makes any HIP call, so the child starts from a process that has not
+    touched the GPU."""
+    import subprocess
+    p = subprocess.run([sys.executable, os.path.abspath(__file__), "--vendor-child", "--steps", str(steps)],
+                       capture_output=True, text=True, timeout=600)
+    lines = [x for x in p.stdout.splitlines() if x.startswith("{")]
+    if p.returncode != 0 or not lines:
+        return {"error": f"vendor child exited {p.returncode}", "stderr_tail": p.stderr[-400:]}
+    res = json.loads(lines[-1])
+    for name in ("b_row_major", "b_col_major"):
+        log(f"vendor {name}: {res[name]['us']:.1f} us  {res[name]['tops']:.1f} TOP/s")
+    return res
+
+
 def measure_peaks(stream) -> dict:
     """Roofline denominators measured on this GPU: int8 MFMA issue rate from
     a register-only MFMA loop, HBM read and copy bandwidth over 1 GiB."""
@@ -220,7 +264,13 @@ def main() -> int:
     ap.add_argument("--only", default="", help="comma list of workloads (default: all)")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-peaks", action="store_true", help="skip the roofline probe micro-kernels")
+    ap.add_argument("--vendor-ref", action="store_true",
+                    help="also time the vendor int8 GEMM (torch._int_mm) on the headline shape, for context")
+    ap.add_argument("--vendor-child", action="store_true", help=argparse.SUPPRESS)
     args = ap.parse_args()
+    if args.vendor_child:
+        vendor_int8_child(args.steps)
+        return 0
 
     world = int(os.environ.get("WORLD_SIZE", "1"))
     if args.gpus != 1 or world != 1:
@@ -228,6 +278,8 @@ def main() -> int:
               "sharding of this path (row bands, no collectives) is described in DESIGN.md, not run.",
               file=sys.stderr)
         return 2
+    # the vendor leg runs first, in a child process, before any HIP call here
+    vendor = vendor_int8_reference(args.steps) if args.vendor_ref else None
 
     L = M.lib()
     M.check(L.det_set_device(0))
@@ -296,6 +348,17 @@ def main() -> int:
                            "limb_mfma_tops": round(15 * t, 2),
                            "frac_of_int8_mfma_peak_limb": round(15 * t / PEAK_INT8_TOPS, 4)}
         log(f"q16_1024: {r['ms'] * 1e3:.1f} us  {t:.2f} TOP/s")
+    if want("q16_4096"):
+        log("q16_4096: det_matmul_q16 4096^3 (saturating config)")
+        r = runs["q16_4096"] = gemm_workload("q16", 4096, 4096, 4096, max(3, K // 4), 1, stream, 0x4016,
+                                             check_rows=2)
+        t = r["ops"] / (r["ms"] * 1e-3) / 1e12
+        sec["q16_4096"] = {"ms": round(r["ms"], 5), "value": round(t, 3), "unit": "Q16 TOP/s (2*MNK/t)",
+                           "limb_mfma_tops": round(15 * t, 2),
+                           "frac_of_int8_mfma_peak_limb": round(15 * t / PEAK_INT8_TOPS, 4),
+                           "residue_valu_note": "the per-term floor needs M*N*K 16-bit residue products on the "
+                                                "VALU (1 op per term); gfx950 does not co-issue them with MFMA"}
+        log(f"q16_4096: {r['ms'] * 1e3:.1f} us  {t:.2f} TOP/s")
     if want("i16_2048"):
         log("i16_2048: det_matmul_i16 2048^3")
         r = runs["i16_2048"] = gemm_workload("i16", 2048, 2048, 2048, K, W, stream, 0x2016)
@@ -331,6 +394,8 @@ def main() -> int:
         log(f"i8_8192: {r['ms'] * 1e3:.1f} us  {t:.1f} TOP/s")
     result["secondary"] = sec
     stream.destroy()
+    if vendor is not None:
+        result["vendor_int8_gemm"] = vendor
 
     # ---- CPU leg: the oracle checks every timed output (sampled rows), then
     # the MT CPU restatement is timed on a row band of the headline workload.
