@@ -36,6 +36,9 @@ extern "C" {
 #define DET_OP_I8 1
 #define DET_OP_I16 2
 #define DET_OP_Q16 3
+#define DET_DOT_Q16 0
+#define DET_DOT_L1_Q16 1
+#define DET_DOT_I16 2
 
 /* ------------------------------------------------------------------------
  * Layer 1: the reference's intrinsic symbols (arity table
@@ -69,6 +72,15 @@ int64_t __mind_blas_dot_q16(int64_t a, int64_t b, int64_t len);
 /* Replaces __mind_blas_dot_q16_v (the vector-dialect twin of the above):
  * src/mlir/lowering.rs:5695-5860. */
 int64_t __mind_blas_dot_q16_v(int64_t a, int64_t b, int64_t len);
+/* Replaces __mind_blas_dot_l1_q16(a, b, len) -> (int64)(int32)sum |a - b|:
+ * runtime-support/mind_intrinsics.c:1551-1562 (scalar), :1598-1608 (export). */
+int64_t __mind_blas_dot_l1_q16(int64_t a, int64_t b, int64_t len);
+/* Replaces __mind_blas_dot_l1_q16_v (vector-dialect twin):
+ * src/type_checker/mod.rs:2260, src/mlir/lowering.rs:2808-2817, :6035-6060. */
+int64_t __mind_blas_dot_l1_q16_v(int64_t a, int64_t b, int64_t len);
+/* Replaces __mind_blas_dot_i16_v(a, b, len) -> (int64)(int32)sum a*b, int16
+ * inputs: src/type_checker/mod.rs:2246, src/mlir/lowering.rs:5861-6030. */
+int64_t __mind_blas_dot_i16_v(int64_t a, int64_t b, int64_t len);
 
 /* ------------------------------------------------------------------------
  * Layer 2: the harness wrappers the reference benches and golden gate
@@ -90,6 +102,10 @@ int64_t mmi16(int64_t w, int64_t x, int64_t y, int64_t rows, int64_t cols);
 int64_t gemvq(int64_t catalog, int64_t query, int64_t scores, int64_t m, int64_t k);
 /* dotq: tests/cross_substrate_identity.rs:70-72 */
 int64_t dotq(int64_t a, int64_t b, int64_t n);
+/* dotl1q: tests/cross_substrate_identity/xnode_driver.c:149, :187 */
+int64_t dotl1q(int64_t a, int64_t b, int64_t n);
+/* doti16: tests/cross_substrate_identity/dot-i16-4096/manifest.toml (symbol) */
+int64_t doti16(int64_t a, int64_t b, int64_t n);
 
 /* ------------------------------------------------------------------------
  * Layer 3: typed entry points of this build.
@@ -105,6 +121,11 @@ int64_t det_gemv_q16(const int32_t *w, const int32_t *x, int32_t *y, int64_t m, 
  * __mind_blas_gemv_q16_mt (the reference takes one query per call). */
 int64_t det_gemv_q16_batched(const int32_t *w, const int32_t *x, int32_t *y, int64_t m, int64_t k, int64_t nb);
 int64_t det_gemv_i16(const int16_t *w, const int16_t *x, int32_t *y, int64_t m, int64_t k);
+/* Vector reductions, returning (int64)(int32)sum like the reference:
+ * Q16 dot (sum of per-term floors), Q16 L1 distance, int16 dot. */
+int64_t det_dot_q16(const int32_t *a, const int32_t *b, int64_t len);
+int64_t det_dot_l1_q16(const int32_t *a, const int32_t *b, int64_t len);
+int64_t det_dot_i16(const int16_t *a, const int16_t *b, int64_t len);
 
 /* Device-pointer, asynchronous on `stream` (a hipStream_t; NULL = default
  * stream).  Inputs must stay valid until the stream reaches the call.  The
@@ -120,6 +141,9 @@ int64_t det_matmul_q16_dev(const int32_t *a, const int32_t *b, int32_t *c, int64
 int64_t det_gemv_q16_dev(const int32_t *w, const int32_t *x, int32_t *y, int64_t m, int64_t k, int64_t nb,
                          void *stream);
 int64_t det_gemv_i16_dev(const int16_t *w, const int16_t *x, int32_t *y, int64_t m, int64_t k, void *stream);
+/* op = DET_DOT_Q16, DET_DOT_L1_Q16 or DET_DOT_I16; *out (device memory)
+ * receives the int32 result (the reference's return value narrowed). */
+int64_t det_dot_dev(int64_t op, const void *a, const void *b, int64_t len, int32_t *out, void *stream);
 /* Workspace bytes op (DET_OP_*) needs at this shape (0 for int8). */
 int64_t det_workspace_bytes(int64_t op, int64_t m, int64_t k, int64_t n);
 int64_t det_matmul_ws_dev(int64_t op, const void *a, const void *b, int32_t *c, int64_t m, int64_t k, int64_t n,

@@ -24,6 +24,8 @@ LIB_PATH = os.path.join(HERE, "lib", "libmind_det_hip.so")
 HEADER = os.path.join(os.path.dirname(HERE), "include", "mind_det.h")
 
 DET_OP_I8, DET_OP_I16, DET_OP_Q16 = 1, 2, 3
+DET_DOT_Q16, DET_DOT_L1_Q16, DET_DOT_I16 = 0, 1, 2
+DET_ERR_ARG, DET_ERR_HIP, DET_ERR_DEVICE = -22, -5, -19
 
 _i64 = ctypes.c_int64
 _u64 = ctypes.c_uint64
@@ -51,8 +53,12 @@ def _bind(L):
     for name in ("__mind_blas_gemv_q16_mt", "__mind_blas_matmul_rmajor_q16_v", "__mind_blas_matmul_rmajor_i16_v",
                  "mmq", "mmi16", "gemvq"):
         f = getattr(L, name); f.argtypes = sig5; f.restype = _i64
-    for name in ("__mind_blas_dot_q16", "__mind_blas_dot_q16_v", "dotq"):
+    for name in ("__mind_blas_dot_q16", "__mind_blas_dot_q16_v", "dotq", "__mind_blas_dot_l1_q16",
+                 "__mind_blas_dot_l1_q16_v", "__mind_blas_dot_i16_v", "dotl1q", "doti16"):
         f = getattr(L, name); f.argtypes = [_i64] * 3; f.restype = _i64
+    for name in ("det_dot_q16", "det_dot_l1_q16", "det_dot_i16"):
+        f = getattr(L, name); f.argtypes = [_p, _p, _i64]; f.restype = _i64
+    L.det_dot_dev.argtypes = [_i64, _p, _p, _i64, _p, _p]; L.det_dot_dev.restype = _i64
     for name in ("det_matmul_i8", "det_matmul_i16", "det_matmul_q16"):
         f = getattr(L, name); f.argtypes = [_p, _p, _p, _i64, _i64, _i64]; f.restype = _i64
     for name in ("det_gemv_q16", "det_gemv_i16"):
@@ -155,6 +161,18 @@ def dot_q16(a, b) -> int:
     """__mind_blas_dot_q16: (int64)(int32) sum (a*b >> 16)."""
     a = _req(a, np.int32); b = _req(b, np.int32)
     return lib().__mind_blas_dot_q16(_addr(a), _addr(b), len(a))
+
+
+def dot_l1_q16(a, b) -> int:
+    """__mind_blas_dot_l1_q16: (int64)(int32) sum |a - b|."""
+    a = _req(a, np.int32); b = _req(b, np.int32)
+    return lib().__mind_blas_dot_l1_q16(_addr(a), _addr(b), len(a))
+
+
+def dot_i16(a, b) -> int:
+    """__mind_blas_dot_i16_v: (int64)(int32) sum a*b over int16 vectors."""
+    a = _req(a, np.int16); b = _req(b, np.int16)
+    return lib().__mind_blas_dot_i16_v(_addr(a), _addr(b), len(a))
 
 
 # ---------------------------------------------------------------- conveniences

@@ -236,6 +236,31 @@ int64_t gemv_host(bool q16, int64_t w, int64_t x, int64_t y, int64_t m, int64_t 
     return 0;
 }
 
+// Host-pointer vector reductions: (int64)(int32)sum; len <= 0 or a NULL
+// pointer returns 0 (the reference's Track A convention).
+int64_t dot_host(int op, int64_t a, int64_t b, int64_t len) {
+    if (len <= 0 || !a || !b) return 0;
+    if (len >= (1LL << 31)) return set_err(DET_ERR_ARG, "dimension out of range [0, 2^31)");
+    int64_t rc = 0;
+    const int d = cur_device(&rc);
+    if (d < 0) return rc;
+    DevState &ds = g_dev[d];
+    std::lock_guard<std::mutex> lock(ds.mu);
+    if ((rc = ensure_stream(ds))) return rc;
+    const size_t eb = op == det::DOT_I16 ? 2 : 4, bytes = (size_t)len * eb;
+    const size_t off_b = align256(bytes), off_o = off_b + align256(bytes);
+    if ((rc = ensure(&ds.io, &ds.io_bytes, off_o + 256))) return rc;
+    char *io = (char *)ds.io;
+    hipStream_t s = ds.stream;
+    DET_HIP_CHECK(hipMemcpyAsync(io, (const void *)a, bytes, hipMemcpyHostToDevice, s));
+    DET_HIP_CHECK(hipMemcpyAsync(io + off_b, (const void *)b, bytes, hipMemcpyHostToDevice, s));
+    DET_HIP_CHECK(det::launch_dot(op, io, io + off_b, len, (uint32_t *)(io + off_o), s));
+    uint32_t out = 0;
+    DET_HIP_CHECK(hipMemcpyAsync(&out, io + off_o, 4, hipMemcpyDeviceToHost, s));
+    DET_HIP_CHECK(hipStreamSynchronize(s));
+    return (int64_t)(int32_t)out;
+}
+
 }  // namespace
 
 extern "C" int64_t det_fail_hip(hipError_t e, const char *what) {
@@ -269,13 +294,11 @@ int64_t __mind_blas_matmul_rmajor_q16_v(int64_t w, int64_t x, int64_t y, int64_t
 int64_t __mind_blas_matmul_rmajor_i16_v(int64_t w, int64_t x, int64_t y, int64_t rows, int64_t cols) {
     return gemv_host(false, w, x, y, rows, cols, 1);
 }
-int64_t __mind_blas_dot_q16(int64_t a, int64_t b, int64_t len) {
-    if (len <= 0 || !a || !b) return 0;
-    int32_t out = 0;
-    if (gemv_host(true, a, b, (int64_t)(intptr_t)&out, 1, len, 1) != 0) return 0;
-    return (int64_t)out;
-}
-int64_t __mind_blas_dot_q16_v(int64_t a, int64_t b, int64_t len) { return __mind_blas_dot_q16(a, b, len); }
+int64_t __mind_blas_dot_q16(int64_t a, int64_t b, int64_t len) { return dot_host(det::DOT_Q16, a, b, len); }
+int64_t __mind_blas_dot_q16_v(int64_t a, int64_t b, int64_t len) { return dot_host(det::DOT_Q16, a, b, len); }
+int64_t __mind_blas_dot_l1_q16(int64_t a, int64_t b, int64_t len) { return dot_host(det::DOT_L1, a, b, len); }
+int64_t __mind_blas_dot_l1_q16_v(int64_t a, int64_t b, int64_t len) { return dot_host(det::DOT_L1, a, b, len); }
+int64_t __mind_blas_dot_i16_v(int64_t a, int64_t b, int64_t len) { return dot_host(det::DOT_I16, a, b, len); }
 
 // ====================================================================== layer 2
 int64_t gemmi8(int64_t a, int64_t b, int64_t c, int64_t m, int64_t k, int64_t n) {
@@ -300,6 +323,8 @@ int64_t gemvq(int64_t catalog, int64_t query, int64_t scores, int64_t m, int64_t
     return __mind_blas_gemv_q16_mt(catalog, query, scores, m, k);
 }
 int64_t dotq(int64_t a, int64_t b, int64_t n) { return __mind_blas_dot_q16_v(a, b, n); }
+int64_t dotl1q(int64_t a, int64_t b, int64_t n) { return __mind_blas_dot_l1_q16_v(a, b, n); }
+int64_t doti16(int64_t a, int64_t b, int64_t n) { return __mind_blas_dot_i16_v(a, b, n); }
 
 // ====================================================================== layer 3
 int64_t det_matmul_i8(const int8_t *a, const int8_t *b, int32_t *c, int64_t m, int64_t k, int64_t n) {
@@ -319,6 +344,15 @@ int64_t det_gemv_q16_batched(const int32_t *w, const int32_t *x, int32_t *y, int
 }
 int64_t det_gemv_i16(const int16_t *w, const int16_t *x, int32_t *y, int64_t m, int64_t k) {
     return gemv_host(false, (int64_t)w, (int64_t)x, (int64_t)y, m, k, 1);
+}
+int64_t det_dot_q16(const int32_t *a, const int32_t *b, int64_t len) {
+    return dot_host(det::DOT_Q16, (int64_t)(intptr_t)a, (int64_t)(intptr_t)b, len);
+}
+int64_t det_dot_l1_q16(const int32_t *a, const int32_t *b, int64_t len) {
+    return dot_host(det::DOT_L1, (int64_t)(intptr_t)a, (int64_t)(intptr_t)b, len);
+}
+int64_t det_dot_i16(const int16_t *a, const int16_t *b, int64_t len) {
+    return dot_host(det::DOT_I16, (int64_t)(intptr_t)a, (int64_t)(intptr_t)b, len);
 }
 
 int64_t det_matmul_i8_dev(const int8_t *a, const int8_t *b, int32_t *c, int64_t m, int64_t k, int64_t n,
@@ -387,6 +421,13 @@ int64_t det_gemv_i16_dev(const int16_t *w, const int16_t *x, int32_t *y, int64_t
     hipStream_t s = (hipStream_t)stream;
     if (k == 0) DET_HIP_CHECK(zero_i32(y, (size_t)m, s));
     else DET_HIP_CHECK(det::launch_gemv_i16(w, x, y, (int)m, (int)k, s));
+    return 0;
+}
+int64_t det_dot_dev(int64_t op, const void *a, const void *b, int64_t len, int32_t *out, void *stream) {
+    if (op < det::DOT_Q16 || op > det::DOT_I16) return set_err(DET_ERR_ARG, "unknown dot op");
+    if (len < 0 || len >= (1LL << 31)) return set_err(DET_ERR_ARG, "dimension out of range [0, 2^31)");
+    if (!out || ((!a || !b) && len > 0)) return set_err(DET_ERR_ARG, "null device pointer");
+    DET_HIP_CHECK(det::launch_dot((int)op, a, b, len, (uint32_t *)out, (hipStream_t)stream));
     return 0;
 }
 

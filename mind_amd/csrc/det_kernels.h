@@ -45,6 +45,11 @@ bool gemv8_eligible(const int32_t *W, const int32_t *X, int M, int K);
 size_t gemv8_workspace_bytes(int K);
 hipError_t launch_gemv_q16_mfma(const int32_t *W, const int32_t *X, int32_t *Y, int M, int K, int nb, void *ws,
                                 hipStream_t s);
+// Vector reductions: sum mod 2^32 of the Q16 per-term floor products
+// (DOT_Q16), of |a - b| (DOT_L1, int32 inputs) or of int16 products
+// (DOT_I16); *out (one device uint32) is overwritten.
+enum { DOT_Q16 = 0, DOT_L1 = 1, DOT_I16 = 2 };
+hipError_t launch_dot(int op, const void *a, const void *b, int64_t n, uint32_t *out, hipStream_t s);
 // y[M] = int16 GEMV.
 hipError_t launch_gemv_i16(const int16_t *W, const int16_t *x, int32_t *y, int M, int K, hipStream_t s);
 

@@ -66,7 +66,7 @@ def lib():
         L.det_or_gemv_q16_rows.restype = None
         L.det_or_gemv_i16.argtypes = [_p, _p, _p, _i64, _i64]
         L.det_or_gemv_i16.restype = None
-        for name in ("det_or_dot_q16", "det_or_dot_i16"):
+        for name in ("det_or_dot_q16", "det_or_dot_i16", "det_or_dot_l1_q16"):
             getattr(L, name).argtypes = [_p, _p, _i64]
             getattr(L, name).restype = _i64
         for name in ("det_cpu_gemm_i8", "det_cpu_gemm_q16", "det_cpu_gemm_i16"):
@@ -87,8 +87,9 @@ def ref_lib():
     global _ref
     if _ref is None and os.path.exists(REF_PATH):
         R = ctypes.CDLL(REF_PATH)
-        R.__mind_blas_dot_q16.argtypes = [_i64, _i64, _i64]
-        R.__mind_blas_dot_q16.restype = _i64
+        for name in ("__mind_blas_dot_q16", "__mind_blas_dot_l1_q16"):
+            getattr(R, name).argtypes = [_i64, _i64, _i64]
+            getattr(R, name).restype = _i64
         R.__mind_blas_set_use_avx2.argtypes = [ctypes.c_int]
         R.__mind_blas_set_use_avx2.restype = ctypes.c_int
         _ref = R
@@ -231,6 +232,11 @@ def dot_q16(a, b):
 def dot_i16(a, b):
     a = _c(a, np.int16); b = _c(b, np.int16)
     return lib().det_or_dot_i16(_ptr(a), _ptr(b), len(a))
+
+
+def dot_l1_q16(a, b):
+    a = _c(a, np.int32); b = _c(b, np.int32)
+    return lib().det_or_dot_l1_q16(_ptr(a), _ptr(b), len(a))
 
 
 # ------------------------------------------------------------------ hashing

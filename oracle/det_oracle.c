@@ -157,6 +157,16 @@ int64_t det_or_dot_i16(const int16_t *a, const int16_t *b, int64_t len) {
     return (int64_t)(int32_t)acc;
 }
 
+int64_t det_or_dot_l1_q16(const int32_t *a, const int32_t *b, int64_t len) {
+    if (len <= 0 || a == NULL || b == NULL) return 0;
+    int64_t acc = 0;
+    for (int64_t i = 0; i < len; ++i) {
+        int64_t d = (int64_t)a[i] - (int64_t)b[i];
+        acc += d < 0 ? -d : d;
+    }
+    return (int64_t)(int32_t)acc;
+}
+
 void det_or_gemv_q16(const int32_t *W, const int32_t *x, int32_t *y, int64_t m, int64_t k) {
     for (int64_t i = 0; i < m; ++i) y[i] = (int32_t)det_or_dot_q16(W + i * k, x, k);
 }

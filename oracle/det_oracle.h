@@ -19,6 +19,9 @@
  *                          golden dot-l2-q16 (1d7f272b...).
  *   det_or_gemv_i16     -> golden sha256 gemv-i16-256x256 (3238e8c7...).
  *   det_or_dot_i16      -> golden dot-i16-4096 (af0fc3cf...).
+ *   det_or_dot_l1_q16   -> golden dot-l1-q16 (ce7e2a80...); the reference's own
+ *                          __mind_blas_dot_l1_q16 (oracle/_ref); exact Python-int
+ *                          brute force incl. the |INT32_MIN - INT32_MAX| extreme.
  *   det_or_gemm_i16     -> composition: every element equals det_or_dot_i16 of
  *                          (row of A, column of B); exact Python-int brute force.
  *   det_or_gen_*        -> the golden hashes above fix the reference draw order
@@ -82,6 +85,9 @@ void det_or_gemv_i16(const int16_t *W, const int16_t *x, int32_t *y, int64_t row
 int64_t det_or_dot_q16(const int32_t *a, const int32_t *b, int64_t len);
 /* (i64)(i32) sum_i (i64)a[i]*b[i]   (benches/det_matmul_i16.rs:218-224) */
 int64_t det_or_dot_i16(const int16_t *a, const int16_t *b, int64_t len);
+/* (int64)(int32) sum |a - b| in int64 (runtime-support/mind_intrinsics.c:
+ * 1551-1562); len <= 0 or NULL -> 0 (:1598-1600). */
+int64_t det_or_dot_l1_q16(const int32_t *a, const int32_t *b, int64_t len);
 
 #ifdef __cplusplus
 }

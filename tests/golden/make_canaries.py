@@ -16,7 +16,7 @@ IDS = [
     "gemm-i8-64x64x64", "gemm-i8-mt-64x64x64", "gemm-i8-vnni-64x64x64",
     "gemm-q16-64x64x64", "gemm-q16-fused-64x64x64",
     "gemv-q16-256x256", "gemv-i16-256x256",
-    "dot-i16-4096", "dot-l2-q16",
+    "dot-i16-4096", "dot-l2-q16", "dot-l1-q16",
 ]
 
 

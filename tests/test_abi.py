@@ -40,7 +40,8 @@ def test_reference_arity_is_kept():
     text = open(mind_amd.HEADER).read()
     for name, arity in (("__mind_blas_matmul_mm_i8_v", 6), ("__mind_blas_matmul_mm_q16_v", 6),
                         ("__mind_blas_gemv_q16_mt", 5), ("__mind_blas_matmul_rmajor_i16_v", 5),
-                        ("__mind_blas_dot_q16", 3)):
+                        ("__mind_blas_dot_q16", 3), ("__mind_blas_dot_q16_v", 3), ("__mind_blas_dot_l1_q16", 3),
+                        ("__mind_blas_dot_l1_q16_v", 3), ("__mind_blas_dot_i16_v", 3), ("dotl1q", 3), ("doti16", 3)):
         m = re.search(r"int64_t " + re.escape(name) + r"\(([^)]*)\)", text)
         args = [a.strip() for a in m.group(1).split(",")]
         assert len(args) == arity and all(a.startswith("int64_t") for a in args), name

@@ -92,6 +92,68 @@ def test_canary_dot_l2_q16(canaries):
     assert O.sha256_i64_le(M.lib().dotq(addr(a), addr(b), len(a))) == w["avx2"]
 
 
+@pytest.mark.parametrize("sym", ["dotl1q", "__mind_blas_dot_l1_q16_v", "__mind_blas_dot_l1_q16"])
+def test_canary_dot_l1_q16(canaries, sym):
+    w = canaries["workloads"]["dot-l1-q16"]
+    a, b = O.gen_q16(w["seed"], w["length"], w["length"])
+    note(f"{sym} len=65536")
+    assert O.sha256_i64_le(getattr(M.lib(), sym)(addr(a), addr(b), len(a))) == w["avx2"]
+
+
+@pytest.mark.parametrize("sym", ["doti16", "__mind_blas_dot_i16_v"])
+def test_canary_dot_i16(canaries, sym):
+    w = canaries["workloads"]["dot-i16-4096"]
+    a, b = O.gen_i16(w["seed"], w["length"], w["length"])
+    note(f"{sym} len=4096")
+    assert O.sha256_i64_le(getattr(M.lib(), sym)(addr(a), addr(b), len(a))) == w["avx2"]
+
+
+DOT_LENS = [0, 1, 3, 4, 5, 7, 8, 9, 17, 4093, 65536, 1 << 20]
+
+
+@pytest.mark.parametrize("n", DOT_LENS)
+@pytest.mark.parametrize("fam", ["q16", "full", "extreme"])
+def test_dots_vs_oracle(n, fam):
+    rng = np.random.default_rng(n * 7 + len(fam))
+    ext = np.array([2147483647, -2147483648, -2147483647, 0, 1, -1, 65535, -65536], np.int32)
+    if fam == "q16":
+        a, b = O.gen_q16(0xD07 ^ n, n, n)
+    elif fam == "full":
+        a, b = O.gen_q16(0xD08 ^ n, n, n, shift=0)
+    else:
+        a, b = ext[rng.integers(0, 8, n)], ext[rng.integers(0, 8, n)]
+    note(f"dots {fam} n={n}")
+    assert M.dot_q16(a, b) == O.dot_q16(a, b)
+    assert M.dot_l1_q16(a, b) == O.dot_l1_q16(a, b)
+    a16, b16 = (a >> 16).astype(np.int16), a.astype(np.int16)
+    assert M.dot_i16(a16, b16) == O.dot_i16(a16, b16)
+    if n >= 2:   # misaligned (element offset 1): the unvectorised path
+        assert M.dot_l1_q16(a[1:], b[1:]) == O.dot_l1_q16(a[1:], b[1:])
+        assert M.dot_q16(a[1:], b[:-1]) == O.dot_q16(a[1:], b[:-1])
+        assert M.dot_i16(a16[1:], b16[1:]) == O.dot_i16(a16[1:], b16[1:])
+
+
+def test_dot_dev_entry_point():
+    n = 100003
+    a, b = O.gen_q16(0xDE7, n, n, shift=0)
+    a16, b16 = O.gen_i16(0xDE8, n, n)
+    s = M.Stream()
+    out = M.DeviceBuffer(4)
+    cases = [(M.DET_DOT_Q16, a, b, O.dot_q16(a, b)), (M.DET_DOT_L1_Q16, a, b, O.dot_l1_q16(a, b)),
+             (M.DET_DOT_I16, a16, b16, O.dot_i16(a16, b16))]
+    for op, x, y, want in cases:
+        dx, dy = M.DeviceBuffer.from_array(x), M.DeviceBuffer.from_array(y)
+        for _ in range(2):   # the output is overwritten, not accumulated
+            out.fill(0x5A)
+            note(f"det_dot_dev op={op} n={n}")
+            M.check(M.lib().det_dot_dev(op, dx.ptr, dy.ptr, n, out.ptr, s.ptr))
+            s.sync()
+            assert int(out.to_array(np.int32, (1,))[0]) == want
+        dx.free(); dy.free()
+    assert M.lib().det_dot_dev(7, out.ptr, out.ptr, 4, out.ptr, s.ptr) == M.DET_ERR_ARG
+    assert M.lib().dotl1q(0, 0, 5) == 0 and M.lib().doti16(addr(a16), addr(b16), 0) == 0
+
+
 def test_canary_matmul_det_bench(canaries):
     g = canaries["matmul_det_bench_256"]
     idx = np.arange(256 * 256)

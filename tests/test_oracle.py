@@ -70,6 +70,54 @@ def test_dot_canaries(canaries):
     w = canaries["workloads"]["dot-l2-q16"]
     a, b = O.gen_q16(w["seed"], w["length"], w["length"])
     assert O.sha256_i64_le(O.dot_q16(a, b)) == w["avx2"]
+    w = canaries["workloads"]["dot-l1-q16"]
+    a, b = O.gen_q16(w["seed"], w["length"], w["length"])
+    assert O.sha256_i64_le(O.dot_l1_q16(a, b)) == w["avx2"]
+
+
+def test_dot_l1_q16_brute_force_and_extremes():
+    # exact Python ints: (int64)(int32) sum |a - b|, including |INT32_MIN - INT32_MAX|
+    # = 2^32 - 1 per term (wraps the int32 result) and the empty / length-1 cases
+    rng = np.random.default_rng(0x11)
+    ext = np.array([2147483647, -2147483648, -2147483647, 0, 1, -1, 65536, -65536], np.int32)
+    cases = [(np.zeros(0, np.int32), np.zeros(0, np.int32)),
+             (np.array([-2147483648], np.int32), np.array([2147483647], np.int32))]
+    for n in (1, 2, 7, 64, 1000):
+        cases.append((rng.integers(-2**31, 2**31, n, dtype=np.int64).astype(np.int32),
+                      rng.integers(-2**31, 2**31, n, dtype=np.int64).astype(np.int32)))
+        cases.append((ext[rng.integers(0, 8, n)], ext[rng.integers(0, 8, n)]))
+    for a, b in cases:
+        want = _to_i32(sum(abs(int(x) - int(y)) for x, y in zip(a, b)))
+        assert O.dot_l1_q16(a, b) == want
+        assert O.dot_l1_q16(b, a) == want                    # symmetric
+        assert O.dot_l1_q16(a, a) == 0
+
+
+@pytest.mark.skipif(O.ref_lib() is None, reason="oracle/_ref not built (reference tree absent)")
+def test_dot_l1_q16_matches_reference_live():
+    """The reference's scalar L1 (mind_intrinsics.c:1551-1562, the contract the
+    vector-dialect emitter lowering.rs:6035-6060 matches byte for byte) on every
+    input family; its AVX2 Track A path (:1566-1596) agrees wherever |a - b| <
+    2^31, but forms a - b in 32 bits (_mm256_sub_epi32 + _mm256_abs_epi32), so on
+    full-range inputs it differs from its own scalar definition.  This build
+    follows the scalar / vector-dialect semantics."""
+    R = O.ref_lib()
+    prev = R.__mind_blas_set_use_avx2(0)
+    try:
+        for fam in ("ref12", "full", "extreme"):
+            for n in (1, 9, 4093, 65536):
+                a, b = _dot_inputs(fam, 0x1D1 ^ n, n)
+                assert O.dot_l1_q16(a, b) == R.__mind_blas_dot_l1_q16(a.ctypes.data, b.ctypes.data, n)
+        R.__mind_blas_set_use_avx2(1)
+        for n in (1, 9, 4093, 65536):            # Q16 range (>> 12): no 32-bit overflow, paths agree
+            a, b = _dot_inputs("ref12", 0x1D2 ^ n, n)
+            assert O.dot_l1_q16(a, b) == R.__mind_blas_dot_l1_q16(a.ctypes.data, b.ctypes.data, n)
+        a = np.array([2147483647] * 8, np.int32)  # |a - b| = 2^32 - 1 per term: AVX2 path wraps
+        b = np.array([-2147483648] * 8, np.int32)
+        assert O.dot_l1_q16(a, b) == _to_i32(8 * (2**32 - 1))
+        assert R.__mind_blas_dot_l1_q16(a.ctypes.data, b.ctypes.data, 8) != O.dot_l1_q16(a, b)
+    finally:
+        R.__mind_blas_set_use_avx2(prev)
 
 
 def test_matmul_det_bench_digest(canaries):
