@@ -6,7 +6,8 @@ exact int32 out, in TOP/s (2*M*N*K / time).  A "step" is one call of the
 kernel over device-resident synthetic inputs (the reference bench LCG,
 benches/det_matmul_i8.rs:221-226).  The secondary configs of the same
 metric (Q16.16 GEMM 1024^3 and 4096^3, int16 GEMM 2048^3, Q16 GEMV 16384^2
-at batch 1 and 8, the int8 MLP layer 4096x4096x11008 and the 8192^3 probe)
+at batch 1 and 8, the strict-FP f32 row matmul 16384^2, the int8 MLP layer
+4096x4096x11008 and the 8192^3 probe)
 are timed the same way and reported under "secondary".  --vendor-ref adds,
 for context only, the vendor int8 GEMM (torch._int_mm) on the headline shape.
 
@@ -137,6 +138,35 @@ def gemv_workload(m: int, k: int, nb: int, steps: int, warmup: int, stream, seed
         buf.free()
     nbytes = 4.0 * m * k + 4.0 * k * nb + 4.0 * m * nb
     return {"ms": ev, "wall_ms": wall, "bytes": nbytes, "verify": verify, "checked_rows": len(rows)}
+
+
+def f32_rows_workload(rows: int, cols: int, steps: int, warmup: int, stream, seed_tag: int):
+    """Strict-FP f32 row-major matmul y = W x (the reference's
+    matmul_rmajor_f32 schedule); W and x from the reference f32 generator."""
+    L = M.lib()
+    W, x = M.gen_f32_unit(SEED ^ seed_tag, rows * cols, cols)
+    dw, dx = M.DeviceBuffer.from_array(W), M.DeviceBuffer.from_array(x)
+    dy = M.DeviceBuffer(rows * 4)
+    dy.fill(0xA5)
+    sp = stream.ptr
+
+    def launch():
+        M.check(L.det_matmul_rmajor_f32_dev(dw.ptr, dx.ptr, dy.ptr, rows, cols, sp))
+
+    ev, wall = time_steps(launch, steps, warmup, stream)
+    y = dy.to_array(np.float32, (rows,))
+    sel = sample_rows(rows, 32)
+    got = y[sel].copy()
+    Wr = np.ascontiguousarray(W.reshape(rows, cols)[sel]).ravel()
+
+    def verify(O):
+        want = O.matmul_rmajor_f32(Wr, x, len(sel), cols)
+        return bool(np.array_equal(got.view(np.uint32), want.view(np.uint32)))
+
+    for buf in (dw, dx, dy):
+        buf.free()
+    nbytes = 4.0 * rows * cols + 4.0 * cols + 4.0 * rows
+    return {"ms": ev, "wall_ms": wall, "bytes": nbytes, "verify": verify, "checked_rows": len(sel)}
 
 
 def vendor_int8_child(steps: int) -> None:
@@ -377,6 +407,15 @@ def main() -> int:
                          "roofline": {"bound": "hbm", "achieved": round(gbs, 1), "peak": PEAK_HBM_GBS,
                                       "frac": round(gbs / PEAK_HBM_GBS, 4)}}
             log(f"{name}: {r['ms'] * 1e3:.1f} us  {gbs:.0f} GB/s")
+    if want("f32_rows_16384"):
+        name = "f32_rows_16384"
+        log(f"{name}: det_matmul_rmajor_f32 16384x16384 (strict-FP f32)")
+        r = runs[name] = f32_rows_workload(16384, 16384, K, W, stream, 0xF32)
+        gbs = r["bytes"] / (r["ms"] * 1e-3) / 1e9
+        sec[name] = {"ms": round(r["ms"], 5), "value": round(gbs, 1), "unit": "GB/s",
+                     "roofline": {"bound": "hbm", "achieved": round(gbs, 1), "peak": PEAK_HBM_GBS,
+                                  "frac": round(gbs / PEAK_HBM_GBS, 4)}}
+        log(f"{name}: {r['ms'] * 1e3:.1f} us  {gbs:.0f} GB/s")
     if want("i8_mlp"):
         log("i8_mlp: det_matmul_i8 4096x4096x11008 (MLP layer)")
         r = runs["i8_mlp_4096x4096x11008"] = gemm_workload("i8_mlp", 4096, 4096, 11008, K, W, stream, 0x3117,

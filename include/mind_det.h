@@ -81,6 +81,22 @@ int64_t __mind_blas_dot_l1_q16_v(int64_t a, int64_t b, int64_t len);
 /* Replaces __mind_blas_dot_i16_v(a, b, len) -> (int64)(int32)sum a*b, int16
  * inputs: src/type_checker/mod.rs:2246, src/mlir/lowering.rs:5861-6030. */
 int64_t __mind_blas_dot_i16_v(int64_t a, int64_t b, int64_t len);
+/* Replaces __mind_blas_dot_f32(a, b, len): strict-FP f32 dot (8 lanes of
+ * unfused multiply-then-add, left-to-right lane fold, sequential tail); the
+ * result's f32 bits are returned in the low 32 bits of the int64 (0 for
+ * len <= 0 or NULL): runtime-support/mind_intrinsics.c:1190-1290. */
+int64_t __mind_blas_dot_f32(int64_t a, int64_t b, int64_t len);
+/* Replaces __mind_blas_dot_f32_v (vector-dialect twin, same schedule):
+ * src/type_checker/mod.rs (dot_f32_v), src/mlir/lowering.rs:5528-5690. */
+int64_t __mind_blas_dot_f32_v(int64_t a, int64_t b, int64_t len);
+/* Replaces __mind_blas_matmul_rmajor_f32(w, x, y, rows, cols): y[r] = the
+ * strict dot of row r with x; -1 on a NULL pointer, 0 (y untouched) when
+ * rows <= 0 or cols <= 0: runtime-support/mind_intrinsics.c:1418-1444. */
+int64_t __mind_blas_matmul_rmajor_f32(int64_t w, int64_t x, int64_t y, int64_t rows, int64_t cols);
+/* Replaces __mind_blas_matmul_rmajor_f32_v (vector-dialect twin):
+ * src/mlir/lowering.rs:6441 (emit_vec_matmul_rmajor_f32).  Same values; a
+ * NULL pointer returns 0 without writing (the emitted kernel has no check). */
+int64_t __mind_blas_matmul_rmajor_f32_v(int64_t w, int64_t x, int64_t y, int64_t rows, int64_t cols);
 
 /* ------------------------------------------------------------------------
  * Layer 2: the harness wrappers the reference benches and golden gate
@@ -106,6 +122,10 @@ int64_t dotq(int64_t a, int64_t b, int64_t n);
 int64_t dotl1q(int64_t a, int64_t b, int64_t n);
 /* doti16: tests/cross_substrate_identity/dot-i16-4096/manifest.toml (symbol) */
 int64_t doti16(int64_t a, int64_t b, int64_t n);
+/* dotf32 / mmf32: tests/cross_substrate_identity/{dot-f32-v-4093,
+ * matmul-f32-v-64x64}/manifest.toml (symbol), cross_substrate_identity.rs:2579-2598 */
+int64_t dotf32(int64_t a, int64_t b, int64_t n);
+int64_t mmf32(int64_t w, int64_t x, int64_t y, int64_t rows, int64_t cols);
 
 /* ------------------------------------------------------------------------
  * Layer 3: typed entry points of this build.
@@ -126,6 +146,10 @@ int64_t det_gemv_i16(const int16_t *w, const int16_t *x, int32_t *y, int64_t m, 
 int64_t det_dot_q16(const int32_t *a, const int32_t *b, int64_t len);
 int64_t det_dot_l1_q16(const int32_t *a, const int32_t *b, int64_t len);
 int64_t det_dot_i16(const int16_t *a, const int16_t *b, int64_t len);
+/* Strict-FP f32 (same schedule as __mind_blas_dot_f32): *out receives the
+ * dot; y[r] receives row r's dot with x.  Return 0 or a negative error. */
+int64_t det_dot_f32(const float *a, const float *b, int64_t len, float *out);
+int64_t det_matmul_rmajor_f32(const float *w, const float *x, float *y, int64_t rows, int64_t cols);
 
 /* Device-pointer, asynchronous on `stream` (a hipStream_t; NULL = default
  * stream).  Inputs must stay valid until the stream reaches the call.  The
@@ -144,6 +168,8 @@ int64_t det_gemv_i16_dev(const int16_t *w, const int16_t *x, int32_t *y, int64_t
 /* op = DET_DOT_Q16, DET_DOT_L1_Q16 or DET_DOT_I16; *out (device memory)
  * receives the int32 result (the reference's return value narrowed). */
 int64_t det_dot_dev(int64_t op, const void *a, const void *b, int64_t len, int32_t *out, void *stream);
+int64_t det_matmul_rmajor_f32_dev(const float *w, const float *x, float *y, int64_t rows, int64_t cols,
+                                  void *stream);
 /* Workspace bytes op (DET_OP_*) needs at this shape (0 for int8). */
 int64_t det_workspace_bytes(int64_t op, int64_t m, int64_t k, int64_t n);
 int64_t det_matmul_ws_dev(int64_t op, const void *a, const void *b, int32_t *c, int64_t m, int64_t k, int64_t n,
@@ -191,6 +217,9 @@ void det_gen_q16(uint64_t seed, int shift, int32_t *a, int64_t na, int32_t *b, i
 void det_gen_q16_sat(uint64_t seed, int shift, int32_t *a, int64_t na, int32_t *b, int64_t nb);
 void det_gen_i8_gauss(uint64_t seed, int8_t *x, int64_t n);
 void det_gen_i8_sym127(uint64_t seed, int8_t *w, int64_t n);
+/* f32 samples ((float)u32 / (float)UINT32_MAX) * 2 - 1, A then B
+ * (tests/cross_substrate_identity.rs make_pair_f32). */
+void det_gen_f32_unit(uint64_t seed, float *a, int64_t na, float *b, int64_t nb);
 
 #ifdef __cplusplus
 }

@@ -59,6 +59,14 @@ def _bind(L):
     for name in ("det_dot_q16", "det_dot_l1_q16", "det_dot_i16"):
         f = getattr(L, name); f.argtypes = [_p, _p, _i64]; f.restype = _i64
     L.det_dot_dev.argtypes = [_i64, _p, _p, _i64, _p, _p]; L.det_dot_dev.restype = _i64
+    for name in ("__mind_blas_dot_f32", "__mind_blas_dot_f32_v", "dotf32"):
+        f = getattr(L, name); f.argtypes = [_i64] * 3; f.restype = _i64
+    for name in ("__mind_blas_matmul_rmajor_f32", "__mind_blas_matmul_rmajor_f32_v", "mmf32"):
+        f = getattr(L, name); f.argtypes = [_i64] * 5; f.restype = _i64
+    L.det_dot_f32.argtypes = [_p, _p, _i64, _p]; L.det_dot_f32.restype = _i64
+    L.det_matmul_rmajor_f32.argtypes = [_p, _p, _p, _i64, _i64]; L.det_matmul_rmajor_f32.restype = _i64
+    L.det_matmul_rmajor_f32_dev.argtypes = [_p, _p, _p, _i64, _i64, _p]
+    L.det_matmul_rmajor_f32_dev.restype = _i64
     for name in ("det_matmul_i8", "det_matmul_i16", "det_matmul_q16"):
         f = getattr(L, name); f.argtypes = [_p, _p, _p, _i64, _i64, _i64]; f.restype = _i64
     for name in ("det_gemv_q16", "det_gemv_i16"):
@@ -91,7 +99,7 @@ def _bind(L):
     L.det_probe_mfma_i8.argtypes = [_p, _p, _i64, _i64, _i64, _p]; L.det_probe_mfma_i8.restype = _i64
     L.det_probe_read.argtypes = [_p, _i64, _p, _i64, _p]; L.det_probe_read.restype = _i64
     L.det_copy_dev.argtypes = [_p, _p, _i64, _p]; L.det_copy_dev.restype = _i64
-    for name in ("det_gen_i8", "det_gen_i16"):
+    for name in ("det_gen_i8", "det_gen_i16", "det_gen_f32_unit"):
         f = getattr(L, name); f.argtypes = [_u64, _p, _i64, _p, _i64]; f.restype = None
     for name in ("det_gen_q16", "det_gen_q16_sat"):
         f = getattr(L, name); f.argtypes = [_u64, ctypes.c_int, _p, _i64, _p, _i64]; f.restype = None
@@ -167,6 +175,21 @@ def dot_l1_q16(a, b) -> int:
     """__mind_blas_dot_l1_q16: (int64)(int32) sum |a - b|."""
     a = _req(a, np.int32); b = _req(b, np.int32)
     return lib().__mind_blas_dot_l1_q16(_addr(a), _addr(b), len(a))
+
+
+def dot_f32_bits(a, b) -> int:
+    """__mind_blas_dot_f32: the strict-FP dot's f32 bits (low 32 bits of the int64)."""
+    a = _req(a, np.float32); b = _req(b, np.float32)
+    return lib().__mind_blas_dot_f32(_addr(a), _addr(b), len(a))
+
+
+def matmul_rmajor_f32(W, x):
+    """__mind_blas_matmul_rmajor_f32: y[rows] (f32) = strict dots of W's rows with x."""
+    W = _req(W, np.float32); x = _req(x, np.float32)
+    rows, cols = W.shape
+    y = np.zeros(rows, np.float32)
+    check(lib().__mind_blas_matmul_rmajor_f32(_addr(W), _addr(x), _addr(y), rows, cols))
+    return y
 
 
 def dot_i16(a, b) -> int:
@@ -320,6 +343,12 @@ def gen_i16(seed, na, nb):
 def gen_q16(seed, na, nb, shift=12):
     a = np.empty(na, np.int32); b = np.empty(nb, np.int32)
     lib().det_gen_q16(seed, shift, _addr(a), na, _addr(b), nb)
+    return a, b
+
+
+def gen_f32_unit(seed, na, nb):
+    a = np.empty(na, np.float32); b = np.empty(nb, np.float32)
+    lib().det_gen_f32_unit(seed, _addr(a), na, _addr(b), nb)
     return a, b
 
 

@@ -261,6 +261,43 @@ int64_t dot_host(int op, int64_t a, int64_t b, int64_t len) {
     return (int64_t)(int32_t)out;
 }
 
+// Host-pointer strict-FP f32 rows: y[r] = dot(W row r, x).  rows, cols > 0.
+int64_t f32_rows_host(const float *w, const float *x, float *y, int64_t rows, int64_t cols) {
+    if (rows >= (1LL << 31) || cols >= (1LL << 31)) return set_err(DET_ERR_ARG, "dimension out of range [0, 2^31)");
+    int64_t rc = 0;
+    const int d = cur_device(&rc);
+    if (d < 0) return rc;
+    DevState &ds = g_dev[d];
+    std::lock_guard<std::mutex> lock(ds.mu);
+    if ((rc = ensure_stream(ds))) return rc;
+    const size_t bytes_w = (size_t)rows * cols * 4, bytes_x = (size_t)cols * 4, bytes_y = (size_t)rows * 4;
+    const size_t off_x = align256(bytes_w), off_y = off_x + align256(bytes_x);
+    if ((rc = ensure(&ds.io, &ds.io_bytes, off_y + align256(bytes_y)))) return rc;
+    char *io = (char *)ds.io;
+    hipStream_t s = ds.stream;
+    DET_HIP_CHECK(hipMemcpyAsync(io, w, bytes_w, hipMemcpyHostToDevice, s));
+    DET_HIP_CHECK(hipMemcpyAsync(io + off_x, x, bytes_x, hipMemcpyHostToDevice, s));
+    DET_HIP_CHECK(det::launch_rows_f32((const float *)io, (const float *)(io + off_x), (float *)(io + off_y), rows,
+                                       cols, s));
+    DET_HIP_CHECK(hipMemcpyAsync(y, io + off_y, bytes_y, hipMemcpyDeviceToHost, s));
+    DET_HIP_CHECK(hipStreamSynchronize(s));
+    return 0;
+}
+
+// The reference's packing of an f32 result: its bits, zero-extended to int64.
+int64_t pack_f32(float v) {
+    uint32_t b;
+    memcpy(&b, &v, 4);
+    return (int64_t)(uint64_t)b;
+}
+
+int64_t dot_f32_host(int64_t a, int64_t b, int64_t len) {
+    if (len <= 0 || !a || !b) return pack_f32(0.0f);
+    float out = 0.0f;
+    if (f32_rows_host((const float *)(intptr_t)a, (const float *)(intptr_t)b, &out, 1, len) != 0) return 0;
+    return pack_f32(out);
+}
+
 }  // namespace
 
 extern "C" int64_t det_fail_hip(hipError_t e, const char *what) {
@@ -299,6 +336,17 @@ int64_t __mind_blas_dot_q16_v(int64_t a, int64_t b, int64_t len) { return dot_ho
 int64_t __mind_blas_dot_l1_q16(int64_t a, int64_t b, int64_t len) { return dot_host(det::DOT_L1, a, b, len); }
 int64_t __mind_blas_dot_l1_q16_v(int64_t a, int64_t b, int64_t len) { return dot_host(det::DOT_L1, a, b, len); }
 int64_t __mind_blas_dot_i16_v(int64_t a, int64_t b, int64_t len) { return dot_host(det::DOT_I16, a, b, len); }
+int64_t __mind_blas_dot_f32(int64_t a, int64_t b, int64_t len) { return dot_f32_host(a, b, len); }
+int64_t __mind_blas_dot_f32_v(int64_t a, int64_t b, int64_t len) { return dot_f32_host(a, b, len); }
+int64_t __mind_blas_matmul_rmajor_f32(int64_t w, int64_t x, int64_t y, int64_t rows, int64_t cols) {
+    if (!w || !x || !y) return -1;
+    if (rows <= 0 || cols <= 0) return 0;
+    return f32_rows_host((const float *)(intptr_t)w, (const float *)(intptr_t)x, (float *)(intptr_t)y, rows, cols);
+}
+int64_t __mind_blas_matmul_rmajor_f32_v(int64_t w, int64_t x, int64_t y, int64_t rows, int64_t cols) {
+    if (!w || !x || !y || rows <= 0 || cols <= 0) return 0;
+    return f32_rows_host((const float *)(intptr_t)w, (const float *)(intptr_t)x, (float *)(intptr_t)y, rows, cols);
+}
 
 // ====================================================================== layer 2
 int64_t gemmi8(int64_t a, int64_t b, int64_t c, int64_t m, int64_t k, int64_t n) {
@@ -325,6 +373,10 @@ int64_t gemvq(int64_t catalog, int64_t query, int64_t scores, int64_t m, int64_t
 int64_t dotq(int64_t a, int64_t b, int64_t n) { return __mind_blas_dot_q16_v(a, b, n); }
 int64_t dotl1q(int64_t a, int64_t b, int64_t n) { return __mind_blas_dot_l1_q16_v(a, b, n); }
 int64_t doti16(int64_t a, int64_t b, int64_t n) { return __mind_blas_dot_i16_v(a, b, n); }
+int64_t dotf32(int64_t a, int64_t b, int64_t n) { return __mind_blas_dot_f32_v(a, b, n); }
+int64_t mmf32(int64_t w, int64_t x, int64_t y, int64_t rows, int64_t cols) {
+    return __mind_blas_matmul_rmajor_f32_v(w, x, y, rows, cols);
+}
 
 // ====================================================================== layer 3
 int64_t det_matmul_i8(const int8_t *a, const int8_t *b, int32_t *c, int64_t m, int64_t k, int64_t n) {
@@ -353,6 +405,19 @@ int64_t det_dot_l1_q16(const int32_t *a, const int32_t *b, int64_t len) {
 }
 int64_t det_dot_i16(const int16_t *a, const int16_t *b, int64_t len) {
     return dot_host(det::DOT_I16, (int64_t)(intptr_t)a, (int64_t)(intptr_t)b, len);
+}
+int64_t det_dot_f32(const float *a, const float *b, int64_t len, float *out) {
+    if (!out) return set_err(DET_ERR_ARG, "null output pointer");
+    if (len <= 0 || !a || !b) {
+        *out = 0.0f;
+        return 0;
+    }
+    return f32_rows_host(a, b, out, 1, len);
+}
+int64_t det_matmul_rmajor_f32(const float *w, const float *x, float *y, int64_t rows, int64_t cols) {
+    if (rows < 0 || cols < 0) return set_err(DET_ERR_ARG, "dimension out of range [0, 2^31)");
+    if (rows == 0 || cols == 0 || !w || !x || !y) return 0;
+    return f32_rows_host(w, x, y, rows, cols);
 }
 
 int64_t det_matmul_i8_dev(const int8_t *a, const int8_t *b, int32_t *c, int64_t m, int64_t k, int64_t n,
@@ -421,6 +486,15 @@ int64_t det_gemv_i16_dev(const int16_t *w, const int16_t *x, int32_t *y, int64_t
     hipStream_t s = (hipStream_t)stream;
     if (k == 0) DET_HIP_CHECK(zero_i32(y, (size_t)m, s));
     else DET_HIP_CHECK(det::launch_gemv_i16(w, x, y, (int)m, (int)k, s));
+    return 0;
+}
+int64_t det_matmul_rmajor_f32_dev(const float *w, const float *x, float *y, int64_t rows, int64_t cols,
+                                  void *stream) {
+    if (rows < 0 || cols < 0 || rows >= (1LL << 31) || cols >= (1LL << 31))
+        return set_err(DET_ERR_ARG, "dimension out of range [0, 2^31)");
+    if (rows == 0 || cols == 0) return 0;
+    if (!w || !x || !y) return set_err(DET_ERR_ARG, "null device pointer");
+    DET_HIP_CHECK(det::launch_rows_f32(w, x, y, rows, cols, (hipStream_t)stream));
     return 0;
 }
 int64_t det_dot_dev(int64_t op, const void *a, const void *b, int64_t len, int32_t *out, void *stream) {

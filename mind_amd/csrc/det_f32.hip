@@ -1,0 +1,266 @@
+// det_f32.hip -- strict-FP f32 dot and row-major matmul, bit-identical to
+// the reference's pinned schedule (runtime-support/mind_intrinsics.c:
+// 1190-1290 dot_f32 scalar / AVX2, 1418-1444 matmul_rmajor_f32; the strict
+// vector twins __mind_blas_dot_f32_v / __mind_blas_matmul_rmajor_f32_v whose
+// golden hashes are tests/cross_substrate_identity/{dot-f32-v-4093,
+// matmul-f32-v-64x64}):
+//
+//   lane j (0..7) accumulates acc_j = acc_j + (a[i+j] * b[i+j]) over the full
+//   blocks of 8 in increasing i (product rounded, then the add rounded: no
+//   fused multiply-add); s = acc_0 + acc_1 + ... + acc_7 folded left to
+//   right; then s = s + (a[i] * b[i]) for the len % 8 tail in order.
+//
+// Float addition is not associative, so that order is the whole contract:
+// each accumulator is a sequential chain and the only parallelism is across
+// rows and the 8 chains of a row.  A row is owned by T = 8 / C consecutive
+// threads, thread q running chains qC .. qC + C - 1 (C-wide vector loads of
+// W and x per step).  The kernel is HBM-bound on W: every element is read
+// once.  With few waves per SIMD, memory parallelism comes from a two-buffer
+// register ring of U steps (each slot is reloaded U steps ahead as soon as
+// it is consumed; the ring never copies a register, so no load waits early).
+// The first thread of a row gathers the 8 chains with lane shuffles, folds
+// them in index order and adds the tail.  FP contraction is off for the
+// whole file, and f32 denormals are kept (gfx950's default IEEE mode), as on
+// the reference's CPUs.
+#include "det_common.h"
+#include "det_kernels.h"
+
+#pragma clang fp contract(off)
+
+namespace det {
+namespace f32 {
+
+constexpr int THREADS = 256;
+
+template <int C, bool VEC>
+__device__ __forceinline__ void load_step(const float *p, float (&v)[C]) {
+    if constexpr (VEC && C == 8) {
+        const float4 a = *(const float4 *)p, b = *(const float4 *)(p + 4);
+        v[0] = a.x, v[1] = a.y, v[2] = a.z, v[3] = a.w, v[4] = b.x, v[5] = b.y, v[6] = b.z, v[7] = b.w;
+    } else if constexpr (VEC && C == 4) {
+        const float4 a = *(const float4 *)p;
+        v[0] = a.x, v[1] = a.y, v[2] = a.z, v[3] = a.w;
+    } else if constexpr (VEC && C == 2) {
+        const float2 a = *(const float2 *)p;
+        v[0] = a.x, v[1] = a.y;
+    } else {
+#pragma unroll
+        for (int c = 0; c < C; ++c) v[c] = p[c];
+    }
+}
+
+// y[row] = strict dot(W row, x); rows * T threads, T = 8 / C per row.
+template <int C, int U, int G, bool VEC>
+__global__ __launch_bounds__(THREADS) void rows_kernel(const float *__restrict__ W, const float *__restrict__ x,
+                                                       float *__restrict__ y, int64_t rows, int64_t cols) {
+    constexpr int T = 8 / C;
+    const int64_t g = (int64_t)blockIdx.x * THREADS + threadIdx.x;
+    const int64_t row = g / T;
+    const int q = (int)(g % T);
+    const bool live = row < rows;
+    // Threads past the last row run the last row's loads (always in bounds)
+    // and store nothing, so the whole wave takes the same uniform loop.
+    const float *wr = W + (live ? row : rows - 1) * cols;
+    const float *w = wr + q * C, *xq = x + q * C;
+    const int64_t nsteps = cols >> 3, nmain = nsteps / U * U;
+    float acc[C];
+#pragma unroll
+    for (int c = 0; c < C; ++c) acc[c] = 0.0f;
+    if (nmain > 0) {
+        // ring of U step slots: slot u holds step s0 + u; once consumed it is
+        // reloaded with step s0 + u + U (on the last lap a re-read of the
+        // same valid step, never consumed), so U steps stay in flight and no
+        // register is ever copied
+        float wv[U][C], xv[U][C];
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+            load_step<C, VEC>(w + (int64_t)u * 8, wv[u]);
+            load_step<C, VEC>(xq + (int64_t)u * 8, xv[u]);
+            __builtin_amdgcn_sched_barrier(0);   // issue in slot order
+        }
+        for (int64_t s0 = 0; s0 < nmain; s0 += U) {
+            const int64_t nx = s0 + U < nmain ? s0 + U : s0;
+#pragma unroll
+            for (int g = 0; g < G; ++g) {
+#pragma unroll
+                for (int u = g * (U / G); u < (g + 1) * (U / G); ++u)
+#pragma unroll
+                    for (int c = 0; c < C; ++c) {
+                        const float p = wv[u][c] * xv[u][c];
+                        acc[c] = acc[c] + p;
+                    }
+#pragma unroll
+                for (int u = g * (U / G); u < (g + 1) * (U / G); ++u) {
+                    load_step<C, VEC>(w + (nx + u) * 8, wv[u]);
+                    load_step<C, VEC>(xq + (nx + u) * 8, xv[u]);
+                }
+                __builtin_amdgcn_sched_barrier(0);   // keep the ring in slot order
+            }
+        }
+    }
+    for (int64_t s = nmain; s < nsteps; ++s) {
+        float wv[C], xv[C];
+        load_step<C, VEC>(w + s * 8, wv);
+        load_step<C, VEC>(xq + s * 8, xv);
+#pragma unroll
+        for (int c = 0; c < C; ++c) {
+            const float p = wv[c] * xv[c];
+            acc[c] = acc[c] + p;
+        }
+    }
+    // gather the row's 8 chains into its first thread, in chain order
+    float lanes[8];
+    const int base = (int)(threadIdx.x & 63) - q;
+#pragma unroll
+    for (int t = 0; t < T; ++t)
+#pragma unroll
+        for (int c = 0; c < C; ++c) lanes[t * C + c] = T == 1 ? acc[c] : __shfl(acc[c], base + t);
+    if (live && q == 0) {
+        float s = lanes[0];
+#pragma unroll
+        for (int t = 1; t < 8; ++t) s = s + lanes[t];
+        for (int64_t i = nsteps * 8; i < cols; ++i) {
+            const float p = wr[i] * x[i];
+            s = s + p;
+        }
+        y[row] = s;
+    }
+}
+
+// LDS-staged variant for 16-byte aligned W / x with cols % 4 == 0: one wave
+// (one workgroup) owns 8 rows, lane 8 r + j running chain j of row r.  The
+// wave streams its rows through a private LDS ring of NS stages with
+// buffer_load ... lds DMA: a stage holds KC floats of each of the 8 rows
+// (KC * 4 contiguous bytes per row, one 1 KB DMA per 256 floats) and the
+// matching KC floats of x.  Few rows are in flight at once and each is read
+// in large contiguous bursts, which keeps HBM pages hot whatever the row
+// stride; the chains then run from LDS (row stride KC * 4 + 32 bytes, so the
+// 64 lanes' reads of W fall in 64 distinct banks; x reads are broadcasts).
+template <int KC, int NS>
+__global__ __launch_bounds__(64) void rows_dma_kernel(const float *__restrict__ W, const float *__restrict__ x,
+                                                      float *__restrict__ y, int64_t rows, int64_t cols) {
+    constexpr int RS = KC * 4 + 32;            // LDS bytes per row in a stage
+    constexpr int XO = 8 * RS;                 // x chunk offset in a stage
+    constexpr int SB = XO + KC * 4;            // stage bytes
+    constexpr int H = KC / 256;                // 1 KB DMAs per row per stage
+    constexpr int DPS = 9 * H;                 // DMAs per stage (8 rows + x)
+    static_assert(KC % 256 == 0 && NS >= 2 && DPS * (NS - 2) < 64, "stage shape");
+    __shared__ __align__(16) char lds[NS * SB];
+    const int lane = threadIdx.x, r = lane >> 3, j = lane & 7;
+    const int64_t row0 = (int64_t)blockIdx.x * 8;
+    const int nr = rows - row0 < 8 ? (int)(rows - row0) : 8;
+    const v4i32 rw = rsrc_words(W + row0 * cols, (uint32_t)(nr * cols * 4));
+    const v4i32 rx = rsrc_words(x, (uint32_t)(cols * 4));
+    const int64_t nsteps = cols >> 3;
+    const int64_t nch = (nsteps * 8 + KC - 1) / KC;   // chunks covering the full 8-blocks
+    const uint32_t l0 = lds_addr(lds);
+    // Chunk c into stage st; chunks past the end and rows past the last read
+    // nothing (out-of-range offsets land zeros), so every wave issues the
+    // same DPS loads per chunk and the in-order vmcnt count stays exact.
+    auto issue = [&](int64_t c, int st) {
+        const uint32_t sb = l0 + (uint32_t)(st * SB);
+        const bool ok = c < nch;
+#pragma unroll
+        for (int rr = 0; rr < 8; ++rr)
+#pragma unroll
+            for (int h = 0; h < H; ++h)
+                dma16(rw, sb + rr * RS + h * 1024,
+                      ok && rr < nr ? (int)(((int64_t)rr * cols + c * KC + h * 256) * 4) + lane * 16
+                                    : (int)OOB_OFFSET);
+#pragma unroll
+        for (int h = 0; h < H; ++h)
+            dma16(rx, sb + XO + h * 1024, ok ? (int)((c * KC + h * 256) * 4) + lane * 16 : (int)OOB_OFFSET);
+    };
+#pragma unroll
+    for (int s = 0; s < NS - 1; ++s) issue(s, s);
+    float acc = 0.0f;
+    for (int64_t c = 0; c < nch; ++c) {
+        DET_WAIT_VMCNT(DPS * (NS - 2));          // chunk c landed (loads complete in order)
+        DET_WAIT_LGKM0();                        // and every LDS read of the previous chunk returned
+        asm volatile("" ::: "memory");
+        issue(c + NS - 1, (int)((c + NS - 1) % NS));   // into the stage consumed last iteration
+        const int st = (int)(c % NS);
+        const float *ws = (const float *)(lds + st * SB + r * RS) + j;
+        const float *xs = (const float *)(lds + st * SB + XO) + j;
+        const int64_t left = nsteps - c * (KC / 8);
+        if (left >= KC / 8) {
+            // all of the chunk's LDS reads first (one latency per chunk), then the chain
+            float wv[KC / 8], xv[KC / 8];
+#pragma unroll
+            for (int i = 0; i < KC / 8; ++i) wv[i] = ws[8 * i], xv[i] = xs[8 * i];
+            __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+            for (int i = 0; i < KC / 8; ++i) {
+                const float p = wv[i] * xv[i];
+                acc = acc + p;
+            }
+        } else {
+            for (int i = 0; i < (int)left; ++i) {
+                const float p = ws[8 * i] * xs[8 * i];
+                acc = acc + p;
+            }
+        }
+        asm volatile("" ::: "memory");
+    }
+    DET_WAIT_VMCNT(0);
+    float lanes[8];
+#pragma unroll
+    for (int t = 0; t < 8; ++t) lanes[t] = __shfl(acc, (lane & ~7) + t);
+    if (r < nr && j == 0) {
+        float s = lanes[0];
+#pragma unroll
+        for (int t = 1; t < 8; ++t) s = s + lanes[t];
+        const float *wr = W + (row0 + r) * cols;
+        for (int64_t i = nsteps * 8; i < cols; ++i) {
+            const float p = wr[i] * x[i];
+            s = s + p;
+        }
+        y[row0 + r] = s;
+    }
+}
+
+#ifndef DET_F32_KC
+#define DET_F32_KC 256
+#endif
+#ifndef DET_F32_NS
+#define DET_F32_NS 4
+#endif
+#ifndef DET_F32_C
+#define DET_F32_C 1
+#endif
+#ifndef DET_F32_U
+#define DET_F32_U 32
+#endif
+#ifndef DET_F32_G
+#define DET_F32_G 4
+#endif
+
+}  // namespace f32
+
+hipError_t launch_rows_f32(const float *W, const float *x, float *y, int64_t rows, int64_t cols, hipStream_t s) {
+    using namespace f32;
+    constexpr int C = DET_F32_C, U = DET_F32_U, G = DET_F32_G, T = 8 / C;
+    // LDS DMA path: 16-byte aligned rows and x, and 8 rows (plus a chunk of
+    // overshoot) addressable by one 32-bit buffer offset
+    const bool dma = cols % 4 == 0 && cols <= (1LL << 25) && (((uintptr_t)W | (uintptr_t)x) % 16) == 0;
+    const bool vec = cols % C == 0 && (((uintptr_t)W | (uintptr_t)x) % (C >= 4 ? 16 : 4 * C)) == 0;
+    // row chunks keep the grid far below 2^32 threads for any rows < 2^31
+    constexpr int64_t CHUNK = 1LL << 26;
+    for (int64_t r0 = 0; r0 < rows; r0 += CHUNK) {
+        const int64_t n = rows - r0 < CHUNK ? rows - r0 : CHUNK;
+        const float *Wc = W + r0 * cols;
+        if (dma) {
+            hipLaunchKernelGGL((rows_dma_kernel<DET_F32_KC, DET_F32_NS>), dim3((unsigned)((n + 7) / 8)), dim3(64), 0,
+                               s, Wc, x, y + r0, n, cols);
+            continue;
+        }
+        const dim3 grid((unsigned)((n * T + THREADS - 1) / THREADS));
+        if (vec)
+            hipLaunchKernelGGL((rows_kernel<C, U, G, true>), grid, dim3(THREADS), 0, s, Wc, x, y + r0, n, cols);
+        else
+            hipLaunchKernelGGL((rows_kernel<C, U, G, false>), grid, dim3(THREADS), 0, s, Wc, x, y + r0, n, cols);
+    }
+    return hipGetLastError();
+}
+
+}  // namespace det

@@ -76,6 +76,19 @@ void det_gen_i16(uint64_t seed, int16_t *a, int64_t na, int16_t *b, int64_t nb) 
     parallel_fill(seed, (uint64_t)na, nb, 1, [b](int64_t i, uint64_t &s) { b[i] = (int16_t)(next_u32(s) >> 16); });
 }
 
+// A then B, sample ((float)u32 / (float)UINT32_MAX) * 2 - 1 in [-1, 1]
+// (the reference f32 canary generator, cross_substrate_identity.rs
+// make_pair_f32 / make_matvec_f32).
+void det_gen_f32_unit(uint64_t seed, float *a, int64_t na, float *b, int64_t nb) {
+    auto f = [](uint64_t &s) {
+        const float q = (float)next_u32(s) / (float)UINT32_MAX;
+        const float t = q * 2.0f;
+        return t - 1.0f;
+    };
+    parallel_fill(seed, 0, na, 1, [a, f](int64_t i, uint64_t &s) { a[i] = f(s); });
+    parallel_fill(seed, (uint64_t)na, nb, 1, [b, f](int64_t i, uint64_t &s) { b[i] = f(s); });
+}
+
 // A then B, sample (int32)u32 >> shift (12: +-8.0, 13: +-4.0, 15: +-1.0).
 void det_gen_q16(uint64_t seed, int shift, int32_t *a, int64_t na, int32_t *b, int64_t nb) {
     parallel_fill(seed, 0, na, 1, [a, shift](int64_t i, uint64_t &s) { a[i] = ((int32_t)next_u32(s)) >> shift; });

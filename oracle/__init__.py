@@ -43,9 +43,13 @@ def lib():
         L = ctypes.CDLL(LIB_PATH)
         L.det_or_lcg_next_u32.argtypes = [ctypes.POINTER(_u64)]
         L.det_or_lcg_next_u32.restype = ctypes.c_uint32
-        for name in ("det_or_gen_i8", "det_or_gen_i16"):
+        for name in ("det_or_gen_i8", "det_or_gen_i16", "det_or_gen_f32_unit"):
             getattr(L, name).argtypes = [_u64, _p, _i64, _p, _i64]
             getattr(L, name).restype = None
+        L.det_or_dot_f32.argtypes = [_p, _p, _i64]
+        L.det_or_dot_f32.restype = ctypes.c_float
+        L.det_or_matmul_rmajor_f32.argtypes = [_p, _p, _p, _i64, _i64]
+        L.det_or_matmul_rmajor_f32.restype = None
         for name in ("det_or_gen_q16", "det_or_gen_q16_sat"):
             getattr(L, name).argtypes = [_u64, ctypes.c_int, _p, _i64, _p, _i64]
             getattr(L, name).restype = None
@@ -87,9 +91,11 @@ def ref_lib():
     global _ref
     if _ref is None and os.path.exists(REF_PATH):
         R = ctypes.CDLL(REF_PATH)
-        for name in ("__mind_blas_dot_q16", "__mind_blas_dot_l1_q16"):
+        for name in ("__mind_blas_dot_q16", "__mind_blas_dot_l1_q16", "__mind_blas_dot_f32"):
             getattr(R, name).argtypes = [_i64, _i64, _i64]
             getattr(R, name).restype = _i64
+        R.__mind_blas_matmul_rmajor_f32.argtypes = [_i64] * 5
+        R.__mind_blas_matmul_rmajor_f32.restype = _i64
         R.__mind_blas_set_use_avx2.argtypes = [ctypes.c_int]
         R.__mind_blas_set_use_avx2.restype = ctypes.c_int
         _ref = R
@@ -126,6 +132,14 @@ def gen_q16(seed: int, na: int, nb: int, shift: int = 12):
     a = np.empty(na, np.int32)
     b = np.empty(nb, np.int32)
     lib().det_or_gen_q16(seed, shift, _ptr(a), na, _ptr(b), nb)
+    return a, b
+
+
+def gen_f32_unit(seed: int, na: int, nb: int):
+    """Reference f32 samples in [-1, 1) (a then b from one LCG stream)."""
+    a = np.empty(na, np.float32)
+    b = np.empty(nb, np.float32)
+    lib().det_or_gen_f32_unit(seed, _ptr(a), na, _ptr(b), nb)
     return a, b
 
 
@@ -232,6 +246,20 @@ def dot_q16(a, b):
 def dot_i16(a, b):
     a = _c(a, np.int16); b = _c(b, np.int16)
     return lib().det_or_dot_i16(_ptr(a), _ptr(b), len(a))
+
+
+def dot_f32_bits(a, b) -> int:
+    """Strict-FP f32 dot; the result's bits as the reference packs them
+    (f32 bits in the low 32 bits of a non-negative int64)."""
+    a = _c(a, np.float32); b = _c(b, np.float32)
+    return int(np.float32(lib().det_or_dot_f32(_ptr(a), _ptr(b), len(a))).view(np.uint32))
+
+
+def matmul_rmajor_f32(W, x, rows, cols):
+    W = _c(W, np.float32); x = _c(x, np.float32)
+    y = np.empty(rows, np.float32)
+    lib().det_or_matmul_rmajor_f32(_ptr(W), _ptr(x), _ptr(y), rows, cols)
+    return y
 
 
 def dot_l1_q16(a, b):

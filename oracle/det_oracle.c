@@ -167,6 +167,34 @@ int64_t det_or_dot_l1_q16(const int32_t *a, const int32_t *b, int64_t len) {
     return (int64_t)(int32_t)acc;
 }
 
+float det_or_dot_f32(const float *a, const float *b, int64_t len) {
+    if (len <= 0 || a == NULL || b == NULL) return 0.0f;
+    float acc[8] = {0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f};
+    int64_t i = 0;
+    for (; i + 8 <= len; i += 8)
+        for (int j = 0; j < 8; ++j) {
+            const float p = a[i + j] * b[i + j];
+            acc[j] = acc[j] + p;
+        }
+    float s = acc[0];
+    for (int j = 1; j < 8; ++j) s = s + acc[j];
+    for (; i < len; ++i) {
+        const float p = a[i] * b[i];
+        s = s + p;
+    }
+    return s;
+}
+
+void det_or_matmul_rmajor_f32(const float *W, const float *x, float *y, int64_t rows, int64_t cols) {
+    for (int64_t r = 0; r < rows; ++r) y[r] = det_or_dot_f32(W + r * cols, x, cols);
+}
+
+void det_or_gen_f32_unit(uint64_t seed, float *a, int64_t na, float *b, int64_t nb) {
+    uint64_t s = seed;
+    for (int64_t i = 0; i < na; ++i) a[i] = ((float)det_or_lcg_next_u32(&s) / (float)UINT32_MAX) * 2.0f - 1.0f;
+    for (int64_t i = 0; i < nb; ++i) b[i] = ((float)det_or_lcg_next_u32(&s) / (float)UINT32_MAX) * 2.0f - 1.0f;
+}
+
 void det_or_gemv_q16(const int32_t *W, const int32_t *x, int32_t *y, int64_t m, int64_t k) {
     for (int64_t i = 0; i < m; ++i) y[i] = (int32_t)det_or_dot_q16(W + i * k, x, k);
 }

@@ -24,6 +24,10 @@
  *                          brute force incl. the |INT32_MIN - INT32_MAX| extreme.
  *   det_or_gemm_i16     -> composition: every element equals det_or_dot_i16 of
  *                          (row of A, column of B); exact Python-int brute force.
+ *   det_or_dot_f32,     -> golden dot-f32-v-4093 (a132f7b9...) and
+ *   det_or_matmul_rmajor_f32  matmul-f32-v-64x64 (ec5adb99...); the reference's
+ *                          own __mind_blas_dot_f32 / __mind_blas_matmul_rmajor_f32
+ *                          on both of its dispatch paths (oracle/_ref).
  *   det_or_gen_*        -> the golden hashes above fix the reference draw order
  *                          and sample maps (next_i8 / next_i16 / next_q16).
  */
@@ -88,6 +92,19 @@ int64_t det_or_dot_i16(const int16_t *a, const int16_t *b, int64_t len);
 /* (int64)(int32) sum |a - b| in int64 (runtime-support/mind_intrinsics.c:
  * 1551-1562); len <= 0 or NULL -> 0 (:1598-1600). */
 int64_t det_or_dot_l1_q16(const int32_t *a, const int32_t *b, int64_t len);
+
+/* ---- strict-FP f32 (runtime-support/mind_intrinsics.c:1190-1290, 1418-1444;
+ * src/mlir/lowering.rs emit_vec_dot_f32 :5528-5690).  Compiled with
+ * -ffp-contract=off: every product is rounded before its add. ---- */
+/* Lane j (0..7) sums a[i+j]*b[i+j] over full blocks of 8 in increasing i;
+ * the 8 lanes are folded left to right, then the len % 8 tail is added in
+ * order.  len <= 0 or NULL -> 0.0f. */
+float det_or_dot_f32(const float *a, const float *b, int64_t len);
+/* y[r] = det_or_dot_f32(W + r*cols, x, cols). */
+void det_or_matmul_rmajor_f32(const float *W, const float *x, float *y, int64_t rows, int64_t cols);
+/* f32 samples in [-1, 1): ((float)u32 / (float)UINT32_MAX) * 2 - 1, a then b
+ * (tests/cross_substrate_identity.rs:2579-2598). */
+void det_or_gen_f32_unit(uint64_t seed, float *a, int64_t na, float *b, int64_t nb);
 
 #ifdef __cplusplus
 }

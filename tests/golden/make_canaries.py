@@ -17,6 +17,7 @@ IDS = [
     "gemm-q16-64x64x64", "gemm-q16-fused-64x64x64",
     "gemv-q16-256x256", "gemv-i16-256x256",
     "dot-i16-4096", "dot-l2-q16", "dot-l1-q16",
+    "dot-f32-v-4093", "matmul-f32-v-64x64",
 ]
 
 

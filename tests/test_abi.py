@@ -60,6 +60,8 @@ def test_product_generators_match_oracle(n):
         np.testing.assert_array_equal(x, y)
     np.testing.assert_array_equal(mind_amd.gen_i8_gauss(seed, n), O.gen_i8_gauss(seed, n))
     np.testing.assert_array_equal(mind_amd.gen_i8_sym127(seed, n), O.gen_i8_sym127(seed, n))
+    for x, y in zip(mind_amd.gen_f32_unit(seed, n, n + 5), O.gen_f32_unit(seed, n, n + 5)):
+        np.testing.assert_array_equal(x.view(np.uint32), y.view(np.uint32))
 
 
 def test_product_never_touches_the_oracle():

@@ -179,6 +179,162 @@ def test_dot_q16_reference_vectors():
         assert M.dot_q16(a, b) == c["scalar"], c
 
 
+# ------------------------------------------------------------------ strict-FP f32 dot / row matmul
+
+def f32_same(got, want):
+    """Bit equality, except that a NaN result only has to be a NaN: the
+    reference's own NaN bits differ by substrate (x86 creates 0xffc00000,
+    AArch64 and gfx950 0x7fc00000), so no bit pattern is pinned for it."""
+    got = np.asarray(got, np.float32).reshape(-1)
+    want = np.asarray(want, np.float32).reshape(-1)
+    gn, wn = np.isnan(got), np.isnan(want)
+    return bool(np.array_equal(gn, wn) and np.array_equal(got[~gn].view(np.uint32), want[~wn].view(np.uint32)))
+
+
+def bits_to_f32(v):
+    assert 0 <= v < (1 << 32), v   # the reference zero-extends the f32 bits
+    return np.array([v], np.uint32).view(np.float32)
+
+
+@pytest.mark.parametrize("sym", ["dotf32", "__mind_blas_dot_f32", "__mind_blas_dot_f32_v"])
+def test_canary_dot_f32(canaries, sym):
+    w = canaries["workloads"]["dot-f32-v-4093"]
+    a, b = O.gen_f32_unit(w["seed"], w["length"], w["length"])
+    note(f"{sym} len={w['length']}")
+    assert O.sha256_i64_le(getattr(M.lib(), sym)(addr(a), addr(b), len(a))) == w["avx2"]
+
+
+@pytest.mark.parametrize("sym", ["mmf32", "__mind_blas_matmul_rmajor_f32", "__mind_blas_matmul_rmajor_f32_v"])
+def test_canary_matmul_f32(canaries, sym):
+    w = canaries["workloads"]["matmul-f32-v-64x64"]
+    r, c = w["rows"], w["cols"]
+    W, x = O.gen_f32_unit(w["seed"], r * c, c)
+    y = np.full(r, np.nan, np.float32)
+    call5(sym, W, x, y, r, c)
+    import hashlib
+    assert hashlib.sha256(y.view("<u4").tobytes()).hexdigest() == w["avx2"]
+
+
+F32_LENS = list(range(0, 18)) + [63, 64, 65, 4093, 65541, 1 << 20]
+
+
+def f32_family(fam, seed, n):
+    rng = np.random.default_rng(seed)
+    if fam == "unit":
+        return O.gen_f32_unit(seed, n, n)
+    if fam == "wide":   # finite values over the whole exponent range, subnormals included
+        u = rng.integers(0, 1 << 32, 2 * n, dtype=np.uint64).astype(np.uint32)
+        u = np.where((u & 0x7f800000) == 0x7f800000, u & 0xbfffffff, u)
+        f = u.view(np.float32)
+        return f[:n].copy(), f[n:].copy()
+    # special: signed zeros, subnormals, extremes and infinities (inf * 0 and
+    # inf - inf make NaN along the way)
+    sp = np.array([0.0, -0.0, 1.0, -1.0, 1e-45, -1e-45, 1.1754942e-38, 3.4028235e38, -3.4028235e38,
+                   np.inf, -np.inf, 0.5, 3.0, 1e-20, 1e20, -2.5], np.float32)
+    return sp[rng.integers(0, len(sp), n)], sp[rng.integers(0, len(sp), n)]
+
+
+@pytest.mark.parametrize("n", F32_LENS)
+@pytest.mark.parametrize("fam", ["unit", "wide", "special"])
+def test_dot_f32_vs_oracle(n, fam):
+    a, b = f32_family(fam, 0xF32 ^ (n * 131) ^ len(fam), n)
+    note(f"dot_f32 {fam} n={n}")
+    assert f32_same(bits_to_f32(M.dot_f32_bits(a, b)), bits_to_f32(O.dot_f32_bits(a, b)))
+    out = np.full(1, np.nan, np.float32)
+    assert M.lib().det_dot_f32(addr(a), addr(b), n, addr(out)) == 0
+    assert f32_same(out, bits_to_f32(O.dot_f32_bits(a, b)))
+    if n >= 2:   # element offset 1
+        assert f32_same(bits_to_f32(M.dot_f32_bits(a[1:], b[:-1])), bits_to_f32(O.dot_f32_bits(a[1:], b[:-1])))
+
+
+# cols % 4 == 0 (16-byte rows) take the LDS DMA kernel: one chunk is 256
+# floats, so 4, 8, 100, 252 and 1000 end in a partial chunk, 256 / 2048 are
+# whole chunks, 260 / 772 add a tail past whole chunks; row counts that are
+# not a multiple of 8 leave dead rows in the last wave.  Other widths take the
+# register-ring kernel (its ring holds 32 steps: 33 * 8 + 1 = 265 columns
+# cross one lap).
+F32_MM = [(1, 1), (1, 9), (3, 5), (7, 8), (33, 17), (64, 64), (31, 1000), (1000, 31), (4097, 33), (5, 65541),
+          (2048, 2048), (8, 4), (3, 8), (9, 100), (13, 252), (17, 256), (5, 260), (11, 772), (4099, 1024),
+          (2, 265), (70, 777), (1, 1 << 18)]
+
+
+@pytest.mark.parametrize("rows,cols", F32_MM, ids=[f"{r}x{c}" for r, c in F32_MM])
+def test_matmul_f32_vs_oracle(rows, cols):
+    for fam in ("unit", "wide", "special"):
+        W, _ = f32_family(fam, 0xF33 ^ rows * 7 ^ cols, rows * cols)
+        x, _ = f32_family(fam, 0xF34 ^ rows ^ cols * 5, cols)
+        note(f"matmul_f32 {fam} rows={rows} cols={cols}")
+        y = M.matmul_rmajor_f32(W.reshape(rows, cols), x)
+        assert f32_same(y, O.matmul_rmajor_f32(W, x, rows, cols)), fam
+
+
+def test_matmul_f32_unaligned_operands_take_the_register_kernel():
+    # device operands 4 bytes off a 16-byte boundary: the DMA kernel needs
+    # 16-byte rows, so the register-ring kernel runs; same bits either way
+    rows, cols = 517, 1024
+    W, x = O.gen_f32_unit(0xF37, rows * cols + 1, cols + 1)
+    want = O.matmul_rmajor_f32(W[1:], x[1:], rows, cols)
+    s = M.Stream()
+    dW, dx, dy = M.DeviceBuffer.from_array(W), M.DeviceBuffer.from_array(x), M.DeviceBuffer(4 * rows)
+    for wo, xo in ((4, 0), (0, 4), (4, 4)):
+        Wv = W[wo // 4:wo // 4 + rows * cols]
+        xv = x[xo // 4:xo // 4 + cols]
+        dy.fill(0x7F)
+        note(f"det_matmul_rmajor_f32_dev rows={rows} cols={cols} W+{wo} x+{xo}")
+        M.check(M.lib().det_matmul_rmajor_f32_dev(dW.ptr + wo, dx.ptr + xo, dy.ptr, rows, cols, s.ptr))
+        s.sync()
+        assert f32_same(dy.to_array(np.float32, (rows,)), O.matmul_rmajor_f32(Wv, xv, rows, cols))
+    M.check(M.lib().det_matmul_rmajor_f32_dev(dW.ptr + 4, dx.ptr + 4, dy.ptr, rows, cols, s.ptr))
+    s.sync()
+    assert f32_same(dy.to_array(np.float32, (rows,)), want)
+    dW.free(); dx.free(); dy.free()
+
+
+def test_matmul_f32_dev_entry_point():
+    rows, cols = 3001, 777
+    W, x = O.gen_f32_unit(0xF35, rows * cols, cols)
+    want = O.matmul_rmajor_f32(W, x, rows, cols)
+    s = M.Stream()
+    dW, dx, dy = M.DeviceBuffer.from_array(W), M.DeviceBuffer.from_array(x), M.DeviceBuffer(4 * rows)
+    for _ in range(2):
+        dy.fill(0x7F)
+        note(f"det_matmul_rmajor_f32_dev rows={rows} cols={cols}")
+        M.check(M.lib().det_matmul_rmajor_f32_dev(dW.ptr, dx.ptr, dy.ptr, rows, cols, s.ptr))
+        s.sync()
+        assert f32_same(dy.to_array(np.float32, (rows,)), want)
+    # empty shapes launch nothing and leave y alone
+    assert M.lib().det_matmul_rmajor_f32_dev(dW.ptr, dx.ptr, dy.ptr, 0, cols, s.ptr) == 0
+    assert M.lib().det_matmul_rmajor_f32_dev(dW.ptr, dx.ptr, dy.ptr, rows, 0, s.ptr) == 0
+    s.sync()
+    assert f32_same(dy.to_array(np.float32, (rows,)), want)
+    assert M.lib().det_matmul_rmajor_f32_dev(dW.ptr, dx.ptr, dy.ptr, -1, cols, s.ptr) == M.DET_ERR_ARG
+    assert M.lib().det_matmul_rmajor_f32_dev(0, dx.ptr, dy.ptr, rows, cols, s.ptr) == M.DET_ERR_ARG
+    dW.free(); dx.free(); dy.free()
+
+
+def test_f32_null_and_empty_conventions():
+    # mind_intrinsics.c:1418-1427: -1 for a null pointer, 0 (y untouched) for
+    # an empty shape; the vector twin returns 0 for both; a dot of length
+    # <= 0 or with a null operand is +0.0 (bits 0)
+    L = M.lib()
+    W, x = O.gen_f32_unit(0xF36, 12, 4)
+    y = np.full(3, 7.0, np.float32)
+    assert L.__mind_blas_matmul_rmajor_f32(0, addr(x), addr(y), 3, 4) == -1
+    assert L.__mind_blas_matmul_rmajor_f32(addr(W), addr(x), 0, 3, 4) == -1
+    assert L.__mind_blas_matmul_rmajor_f32_v(0, addr(x), addr(y), 3, 4) == 0
+    for sym in ("__mind_blas_matmul_rmajor_f32", "__mind_blas_matmul_rmajor_f32_v", "mmf32"):
+        assert getattr(L, sym)(addr(W), addr(x), addr(y), 0, 4) == 0
+        assert getattr(L, sym)(addr(W), addr(x), addr(y), 3, -2) == 0
+    assert (y == 7.0).all()
+    for sym in ("__mind_blas_dot_f32", "__mind_blas_dot_f32_v", "dotf32"):
+        assert getattr(L, sym)(addr(W), addr(x), 0) == 0
+        assert getattr(L, sym)(0, addr(x), 4) == 0
+    out = np.full(1, 7.0, np.float32)
+    assert L.det_dot_f32(addr(W), addr(x), 0, addr(out)) == 0 and out[0] == 0.0
+    assert L.det_dot_f32(addr(W), addr(x), 4, 0) == M.DET_ERR_ARG
+    assert L.det_matmul_rmajor_f32(addr(W), addr(x), addr(y), 3, -1) == M.DET_ERR_ARG
+
+
 # ------------------------------------------------------------------ int8 shapes
 
 I8_SHAPES = [(1, 1, 1), (1, 64, 1), (3, 5, 7), (16, 16, 16), (17, 33, 65), (64, 64, 64), (255, 257, 129),

@@ -75,6 +75,88 @@ def test_dot_canaries(canaries):
     assert O.sha256_i64_le(O.dot_l1_q16(a, b)) == w["avx2"]
 
 
+def _f32_special_pair(n, seed):
+    """f32 inputs whose products and sums hit denormals, signed zeros and
+    magnitudes near overflow (no NaN-producing combinations: NaN payloads are
+    not pinned by the reference)."""
+    rng = np.random.default_rng(seed)
+    vals = np.array([1e-20, -1e-20, 3e-39, -0.0, 0.0, 1.0, -1.0, 1e19, -1e19, 0.5, 1e-30, 2.5e-25], np.float32)
+    a = vals[rng.integers(0, len(vals), n)]
+    b = vals[rng.integers(0, 6, n)]          # finite, |b| <= 1: no inf - inf
+    return a, b
+
+
+def test_f32_strict_canaries(canaries):
+    w = canaries["workloads"]["dot-f32-v-4093"]
+    a, b = O.gen_f32_unit(w["seed"], w["length"], w["length"])
+    assert O.sha256_i64_le(O.dot_f32_bits(a, b)) == w["avx2"]
+    w = canaries["workloads"]["matmul-f32-v-64x64"]
+    W, x = O.gen_f32_unit(w["seed"], w["rows"] * w["cols"], w["cols"])
+    y = O.matmul_rmajor_f32(W, x, w["rows"], w["cols"])
+    assert hashlib.sha256(y.view("<u4").tobytes()).hexdigest() == w["avx2"]
+
+
+def _dot_f32_variant(a, b, fused=False, pairwise=False):
+    """The reference schedule with one planted change: a single-rounding
+    multiply-add (emulated exactly in float64: a product of two f32 is exact
+    there) or a pairwise lane fold."""
+    n8 = len(a) // 8 * 8
+    acc = np.zeros(8, np.float32)
+    for i in range(0, n8, 8):
+        if fused:
+            acc = (acc.astype(np.float64) + a[i:i + 8].astype(np.float64) * b[i:i + 8].astype(np.float64)).astype(np.float32)
+        else:
+            acc = (acc + (a[i:i + 8] * b[i:i + 8])).astype(np.float32)
+    if pairwise:
+        s = np.float32(np.float32(acc[0] + acc[1]) + np.float32(acc[2] + acc[3])) + \
+            np.float32(np.float32(acc[4] + acc[5]) + np.float32(acc[6] + acc[7]))
+    else:
+        s = acc[0]
+        for j in range(1, 8):
+            s = np.float32(s + acc[j])
+    for i in range(n8, len(a)):
+        s = np.float32(np.float64(s) + np.float64(a[i]) * np.float64(b[i])) if fused else np.float32(s + np.float32(a[i] * b[i]))
+    return np.float32(s)
+
+
+def test_f32_strict_schedule_is_load_bearing(canaries):
+    # the golden hash of the 64-row matmul (64 independent 64-term dots)
+    # rejects an FMA-contracted dot, a pairwise lane fold and a float64
+    # accumulation: the schedule, not just the sum, is the contract.  (A
+    # single dot can coincide: the 4093-term dot canary rounds to the same
+    # float under both the pairwise fold and fusion.)
+    w = canaries["workloads"]["matmul-f32-v-64x64"]
+    W, x = O.gen_f32_unit(w["seed"], w["rows"] * w["cols"], w["cols"])
+    rows, cols = w["rows"], w["cols"]
+
+    def ok(rowdot):
+        y = np.array([rowdot(W[r * cols:(r + 1) * cols]) for r in range(rows)], np.float32)
+        return hashlib.sha256(y.view("<u4").tobytes()).hexdigest() == w["avx2"]
+
+    assert ok(lambda a: _dot_f32_variant(a, x))                            # the restatement itself
+    assert not ok(lambda a: _dot_f32_variant(a, x, fused=True))
+    assert not ok(lambda a: _dot_f32_variant(a, x, pairwise=True))
+    assert not ok(lambda a: np.float32(np.dot(a.astype(np.float64), x.astype(np.float64))))
+
+
+@pytest.mark.skipif(O.ref_lib() is None, reason="oracle/_ref not built (reference tree absent)")
+def test_f32_strict_matches_reference_live():
+    R = O.ref_lib()
+    prev = R.__mind_blas_set_use_avx2(0)
+    try:
+        for avx2 in (0, 1):
+            R.__mind_blas_set_use_avx2(avx2)
+            for n in list(range(0, 18)) + [4093, 65541]:
+                for a, b in (O.gen_f32_unit(0xF32 ^ n, n, n), _f32_special_pair(n, n)):
+                    assert O.dot_f32_bits(a, b) == R.__mind_blas_dot_f32(a.ctypes.data, b.ctypes.data, n)
+            W, x = O.gen_f32_unit(0xF33, 37 * 131, 131)
+            y = np.zeros(37, np.float32)
+            assert R.__mind_blas_matmul_rmajor_f32(W.ctypes.data, x.ctypes.data, y.ctypes.data, 37, 131) == 0
+            assert np.array_equal(O.matmul_rmajor_f32(W, x, 37, 131).view(np.uint32), y.view(np.uint32))
+    finally:
+        R.__mind_blas_set_use_avx2(prev)
+
+
 def test_dot_l1_q16_brute_force_and_extremes():
     # exact Python ints: (int64)(int32) sum |a - b|, including |INT32_MIN - INT32_MAX|
     # = 2^32 - 1 per term (wraps the int32 result) and the empty / length-1 cases
