@@ -6,7 +6,8 @@ exact int32 out, in TOP/s (2*M*N*K / time).  A "step" is one call of the
 kernel over device-resident synthetic inputs (the reference bench LCG,
 benches/det_matmul_i8.rs:221-226).  The secondary configs of the same
 metric (Q16.16 GEMM 1024^3 and 4096^3, int16 GEMM 2048^3, Q16 GEMV 16384^2
-at batch 1 and 8, the strict-FP f32 row matmul 16384^2, the int8 MLP layer
+at batch 1 and 8, the strict-FP f32 row matmul 16384^2, the batched Q16 FFT
+(n = 256, 2^18 transforms), the int8 MLP layer
 4096x4096x11008 and the 8192^3 probe)
 are timed the same way and reported under "secondary".  --vendor-ref adds,
 for context only, the vendor int8 GEMM (torch._int_mm) on the headline shape.
@@ -167,6 +168,65 @@ def f32_rows_workload(rows: int, cols: int, steps: int, warmup: int, stream, see
         buf.free()
     nbytes = 4.0 * rows * cols + 4.0 * cols + 4.0 * rows
     return {"ms": ev, "wall_ms": wall, "bytes": nbytes, "verify": verify, "checked_rows": len(sel)}
+
+
+def fft_workload(logn: int, batch: int, steps: int, warmup: int, stream, seed_tag: int):
+    """Batched Q16.16 FFT (fft256 semantics), in place on device-resident
+    re / im [batch][n].  Each step transforms the previous step's output, so
+    the check applies the oracle (warmup + steps) times to sampled rows."""
+    L = M.lib()
+    n = 1 << logn
+    rng = np.random.default_rng(SEED ^ seed_tag)
+    x = rng.integers(-65536, 65536, (2, batch, n)).astype(np.int64)   # harness.c's sample range
+    tw = M.fft_twiddles(n)
+    dre, dim_, dtw = M.DeviceBuffer.from_array(x[0]), M.DeviceBuffer.from_array(x[1]), M.DeviceBuffer.from_array(tw)
+    sp = stream.ptr
+
+    def launch():
+        M.check(L.det_fft_q16_dev(dre.ptr, dim_.ptr, dtw.ptr, logn, n, batch, sp))
+
+    ev, wall = time_steps(launch, steps, warmup, stream)
+    sel = sample_rows(batch, 16)
+    got_r = dre.to_array(np.int64, (batch, n))[sel]
+    got_i = dim_.to_array(np.int64, (batch, n))[sel]
+    x_sel = x[:, sel].copy()
+
+    def verify(O):
+        r, i = x_sel[0], x_sel[1]
+        for _ in range(warmup + steps):
+            out = [O.fft_q16(r[j], i[j], tw, logn) for j in range(len(sel))]
+            r = np.stack([o[0] for o in out]); i = np.stack([o[1] for o in out])
+        return bool(np.array_equal(r, got_r) and np.array_equal(i, got_i))
+
+    for buf in (dre, dim_, dtw):
+        buf.free()
+    return {"ms": ev, "wall_ms": wall, "bytes": 2.0 * 16 * batch * n, "ffts": batch, "verify": verify,
+            "checked_rows": len(sel)}
+
+
+def cpu_fft_reference(logn: int, seconds: float = 2.0):
+    """The reference's C FFT (bench/fft/fft_ref.c, built into oracle/_ref),
+    single thread, in place on one fixed buffer like its harness."""
+    import oracle as O
+
+    R = O.fft_ref_lib()
+    if R is None:
+        return None
+    n = 1 << logn
+    re, im = O.fft_input_harness(0x1234567, n)
+    tw = O.fft_twiddles(n)
+    a, b, t = re.ctypes.data, im.ctypes.data, tw.ctypes.data
+    for _ in range(2000):
+        R.fft256_c(a, b, t, logn, n)
+    calls, t0 = 0, time.perf_counter()
+    while time.perf_counter() - t0 < seconds:
+        for _ in range(2000):
+            R.fft256_c(a, b, t, logn, n)
+        calls += 2000
+    dt = time.perf_counter() - t0
+    return {"ns_per_fft": round(dt / calls * 1e9, 1), "calls": calls, "cores": 1, "kind": "reference",
+            "note": "bench/fft/fft_ref.c compiled -O3 -march=x86-64-v3 into oracle/_ref, called through ctypes "
+                    "(the per-call ctypes overhead is included)"}
 
 
 def vendor_int8_child(steps: int) -> None:
@@ -416,6 +476,20 @@ def main() -> int:
                      "roofline": {"bound": "hbm", "achieved": round(gbs, 1), "peak": PEAK_HBM_GBS,
                                   "frac": round(gbs / PEAK_HBM_GBS, 4)}}
         log(f"{name}: {r['ms'] * 1e3:.1f} us  {gbs:.0f} GB/s")
+    if want("fft_q16_256"):
+        name = "fft_q16_256"
+        batch = 1 << 18
+        log(f"{name}: det_fft_q16 n=256 x {batch} transforms (in place)")
+        r = runs[name] = fft_workload(8, batch, K, W, stream, 0xFF7)
+        ns = r["ms"] * 1e6 / r["ffts"]
+        gbs = r["bytes"] / (r["ms"] * 1e-3) / 1e9
+        sec[name] = {"ms": round(r["ms"], 5), "ns_per_fft": round(ns, 4), "value": round(10240.0 / ns, 1),
+                     "unit": "GFLOP/s-equivalent (5 N log2 N / t, the reference's FFT metric)",
+                     "batch": batch,
+                     "roofline": {"bound": "hbm", "achieved": round(gbs, 1), "peak": PEAK_HBM_GBS,
+                                  "frac": round(gbs / PEAK_HBM_GBS, 4),
+                                  "algorithmic": "read + write of re, im: 32 B per point"}}
+        log(f"{name}: {r['ms'] * 1e3:.1f} us  {ns:.3f} ns/FFT  {gbs:.0f} GB/s")
     if want("i8_mlp"):
         log("i8_mlp: det_matmul_i8 4096x4096x11008 (MLP layer)")
         r = runs["i8_mlp_4096x4096x11008"] = gemm_workload("i8_mlp", 4096, 4096, 11008, K, W, stream, 0x3117,
@@ -446,6 +520,11 @@ def main() -> int:
             checks[name] = r["verify"](O)
             log(f"oracle check {name}: {'exact' if checks[name] else 'MISMATCH'} ({r['checked_rows']} rows)")
         result["exact_vs_oracle"] = checks
+        if "fft_q16_256" in sec:
+            ref = cpu_fft_reference(8)
+            if ref is not None:
+                sec["fft_q16_256"]["cpu_reference"] = ref
+                log(f"fft cpu reference: {ref['ns_per_fft']} ns/FFT (1 thread)")
         if not all(checks.values()):
             print(json.dumps(result), flush=True)
             raise SystemExit("a timed output differs from the oracle: its number is not valid")

@@ -126,6 +126,13 @@ int64_t doti16(int64_t a, int64_t b, int64_t n);
  * matmul-f32-v-64x64}/manifest.toml (symbol), cross_substrate_identity.rs:2579-2598 */
 int64_t dotf32(int64_t a, int64_t b, int64_t n);
 int64_t mmf32(int64_t w, int64_t x, int64_t y, int64_t rows, int64_t cols);
+/* fft256: the Q16.16 radix-2 DIT FFT symbol of examples/fft_q16.mind:15
+ * (dlsym'd by benches/fft_q16.rs:255 and bench/fft/harness.c:62): re / im
+ * are n int64 Q16.16 samples, transformed in place; tw holds n / 2 (wr, wi)
+ * int64 pairs; n must be 2^logn (0 <= logn <= 30).  Returns 0; n == 0 does
+ * nothing; any other (logn, n) returns DET_ERR_ARG (the reference indexes
+ * out of its buffers there). */
+int64_t fft256(int64_t re, int64_t im, int64_t tw, int64_t logn, int64_t n);
 
 /* ------------------------------------------------------------------------
  * Layer 3: typed entry points of this build.
@@ -150,6 +157,9 @@ int64_t det_dot_i16(const int16_t *a, const int16_t *b, int64_t len);
  * dot; y[r] receives row r's dot with x.  Return 0 or a negative error. */
 int64_t det_dot_f32(const float *a, const float *b, int64_t len, float *out);
 int64_t det_matmul_rmajor_f32(const float *w, const float *x, float *y, int64_t rows, int64_t cols);
+/* batch independent fft256 transforms, transform f at re + f * n and
+ * im + f * n (the reference transforms one per call). */
+int64_t det_fft_q16(int64_t *re, int64_t *im, const int64_t *tw, int64_t logn, int64_t n, int64_t batch);
 
 /* Device-pointer, asynchronous on `stream` (a hipStream_t; NULL = default
  * stream).  Inputs must stay valid until the stream reaches the call.  The
@@ -170,6 +180,11 @@ int64_t det_gemv_i16_dev(const int16_t *w, const int16_t *x, int32_t *y, int64_t
 int64_t det_dot_dev(int64_t op, const void *a, const void *b, int64_t len, int32_t *out, void *stream);
 int64_t det_matmul_rmajor_f32_dev(const float *w, const float *x, float *y, int64_t rows, int64_t cols,
                                   void *stream);
+/* Device form of det_fft_q16 (n >= 4096 borrows the workspace arena, whose
+ * size det_fft_workspace_bytes reports). */
+int64_t det_fft_q16_dev(int64_t *re, int64_t *im, const int64_t *tw, int64_t logn, int64_t n, int64_t batch,
+                        void *stream);
+int64_t det_fft_workspace_bytes(int64_t logn, int64_t batch);
 /* Workspace bytes op (DET_OP_*) needs at this shape (0 for int8). */
 int64_t det_workspace_bytes(int64_t op, int64_t m, int64_t k, int64_t n);
 int64_t det_matmul_ws_dev(int64_t op, const void *a, const void *b, int32_t *c, int64_t m, int64_t k, int64_t n,

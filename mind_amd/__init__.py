@@ -65,6 +65,10 @@ def _bind(L):
         f = getattr(L, name); f.argtypes = [_i64] * 5; f.restype = _i64
     L.det_dot_f32.argtypes = [_p, _p, _i64, _p]; L.det_dot_f32.restype = _i64
     L.det_matmul_rmajor_f32.argtypes = [_p, _p, _p, _i64, _i64]; L.det_matmul_rmajor_f32.restype = _i64
+    L.fft256.argtypes = [_i64] * 5; L.fft256.restype = _i64
+    L.det_fft_q16.argtypes = [_p, _p, _p, _i64, _i64, _i64]; L.det_fft_q16.restype = _i64
+    L.det_fft_q16_dev.argtypes = [_p, _p, _p, _i64, _i64, _i64, _p]; L.det_fft_q16_dev.restype = _i64
+    L.det_fft_workspace_bytes.argtypes = [_i64, _i64]; L.det_fft_workspace_bytes.restype = _i64
     L.det_matmul_rmajor_f32_dev.argtypes = [_p, _p, _p, _i64, _i64, _p]
     L.det_matmul_rmajor_f32_dev.restype = _i64
     for name in ("det_matmul_i8", "det_matmul_i16", "det_matmul_q16"):
@@ -190,6 +194,25 @@ def matmul_rmajor_f32(W, x):
     y = np.zeros(rows, np.float32)
     check(lib().__mind_blas_matmul_rmajor_f32(_addr(W), _addr(x), _addr(y), rows, cols))
     return y
+
+
+def fft_q16(re, im, tw, logn=None):
+    """Batched fft256: re / im are [batch, n] (or [n]) int64 Q16.16, tw the n/2
+    (wr, wi) pairs as n int64.  Returns new (re, im) arrays; the inputs are
+    not modified."""
+    re = np.array(re, np.int64, copy=True, order="C")
+    im = np.array(im, np.int64, copy=True, order="C")
+    if re.shape != im.shape:
+        raise ValueError("re and im shapes differ")
+    n = re.shape[-1] if re.ndim else 0
+    batch = re.size // n if n else 0
+    if logn is None:
+        logn = max(n.bit_length() - 1, 0)
+    tw = _req(np.asarray(tw, np.int64), np.int64) if n >= 4 else np.zeros(2, np.int64)
+    if n >= 4 and tw.size < n:
+        raise ValueError("tw needs n int64 (n / 2 pairs)")
+    check(lib().det_fft_q16(_addr(re), _addr(im), _addr(tw), logn, n, batch))
+    return re, im
 
 
 def dot_i16(a, b) -> int:
@@ -350,6 +373,21 @@ def gen_f32_unit(seed, na, nb):
     a = np.empty(na, np.float32); b = np.empty(nb, np.float32)
     lib().det_gen_f32_unit(seed, _addr(a), na, _addr(b), nb)
     return a, b
+
+
+def fft_twiddles(n):
+    """Q16.16 twiddle table for fft256: tw[2k] = round(cos(-2 pi k / n) 2^16),
+    tw[2k+1] = round(sin(-2 pi k / n) 2^16), k < n / 2 (the reference
+    harness's table, bench/fft/fft_driver.c:23-31)."""
+    k = np.arange(n // 2, dtype=np.float64)
+    ang = -2.0 * np.pi * k / n
+    def llround(v):   # half away from zero, like C llround
+        return (np.sign(v) * np.floor(np.abs(v) + 0.5)).astype(np.int64)
+
+    tw = np.zeros(max(n, 2), np.int64)
+    tw[0:n:2] = llround(np.cos(ang) * 65536.0)
+    tw[1:n:2] = llround(np.sin(ang) * 65536.0)
+    return tw
 
 
 def gen_q16_sat(seed, na, nb, shift=13):

@@ -174,7 +174,11 @@ int64_t gemm_host(Op op, int64_t a, int64_t b, int64_t c, int64_t m, int64_t k, 
     hipStream_t s = ds.stream;
     if (bytes_a) DET_HIP_CHECK(hipMemcpyAsync(io, (const void *)a, bytes_a, hipMemcpyHostToDevice, s));
     if (bytes_b) DET_HIP_CHECK(hipMemcpyAsync(io + off_b, (const void *)b, bytes_b, hipMemcpyHostToDevice, s));
+    // the workspace arena is shared with the device-pointer entry points:
+    // start after its last user, and mark this stream as its next one
+    DET_HIP_CHECK(hipStreamWaitEvent(s, ds.ws_free, 0));
     if ((rc = gemm_dev(op, io, io + off_b, io + off_c, m, k, n, ds.ws, s))) return rc;
+    DET_HIP_CHECK(hipEventRecord(ds.ws_free, s));
     DET_HIP_CHECK(hipMemcpyAsync((void *)c, io + off_c, bytes_c, hipMemcpyDeviceToHost, s));
     DET_HIP_CHECK(hipStreamSynchronize(s));
     return 0;
@@ -298,6 +302,73 @@ int64_t dot_f32_host(int64_t a, int64_t b, int64_t len) {
     return pack_f32(out);
 }
 
+
+// ---------------------------------------------------------------- Q16 FFT
+// Argument check shared by the FFT entry points: 1 = nothing to transform
+// (n == 0 or batch == 0: the reference's loops run zero times), 0 = run,
+// negative = error.  n must be 2^logn with logn in [0, 30] (the reference
+// kernel indexes out of its buffers otherwise), and the batch must fit.
+int64_t fft_check(int64_t logn, int64_t n, int64_t batch) {
+    if (batch < 0 || n < 0) return set_err(DET_ERR_ARG, "fft: negative size");
+    if (n == 0 || batch == 0) return 1;
+    if (logn < 0 || logn > 30 || n != ((int64_t)1 << logn))
+        return set_err(DET_ERR_ARG, "fft: n must equal 2^logn with logn in [0, 30]");
+    if (batch > ((int64_t)1 << 40) / n) return set_err(DET_ERR_ARG, "fft: batch * n exceeds 2^40 points");
+    return 0;
+}
+
+// Device-pointer FFT on stream s; the n >= 4096 path borrows the workspace
+// arena (ordered after its previous user).  Call with ds.mu NOT held.
+int64_t fft_dev_run(int64_t *re, int64_t *im, const int64_t *tw, int logn, int64_t batch, hipStream_t s) {
+    const size_t need = det::fft_workspace_bytes(logn, batch);
+    if (need == 0) {
+        DET_HIP_CHECK(det::launch_fft_q16(re, im, tw, logn, batch, nullptr, s));
+        return 0;
+    }
+    int64_t rc = 0;
+    const int d = cur_device(&rc);
+    if (d < 0) return rc;
+    DevState &ds = g_dev[d];
+    std::lock_guard<std::mutex> lock(ds.mu);
+    if ((rc = ensure_stream(ds))) return rc;
+    if ((rc = ensure(&ds.ws, &ds.ws_bytes, need))) return rc;
+    DET_HIP_CHECK(hipStreamWaitEvent(s, ds.ws_free, 0));
+    DET_HIP_CHECK(det::launch_fft_q16(re, im, tw, logn, batch, ds.ws, s));
+    DET_HIP_CHECK(hipEventRecord(ds.ws_free, s));
+    return 0;
+}
+
+// Host-pointer FFT: batch transforms of n points at re / im (in place),
+// twiddle table tw (n int64 = n / 2 (wr, wi) pairs; unused for n < 4).
+int64_t fft_host(int64_t re, int64_t im, int64_t tw, int64_t logn, int64_t n, int64_t batch) {
+    int64_t rc = fft_check(logn, n, batch);
+    if (rc) return rc > 0 ? 0 : rc;
+    if (!re || !im || (!tw && n >= 4)) return set_err(DET_ERR_ARG, "fft: null pointer");
+    const int d = cur_device(&rc);
+    if (d < 0) return rc;
+    DevState &ds = g_dev[d];
+    std::lock_guard<std::mutex> lock(ds.mu);
+    if ((rc = ensure_stream(ds))) return rc;
+    const size_t bytes = (size_t)batch * n * 8, bytes_tw = n >= 4 ? (size_t)n * 8 : 0;
+    const size_t off_im = align256(bytes), off_tw = off_im + align256(bytes);
+    if ((rc = ensure(&ds.io, &ds.io_bytes, off_tw + align256(bytes_tw) + 256))) return rc;
+    const size_t need = det::fft_workspace_bytes((int)logn, batch);
+    if ((rc = ensure(&ds.ws, &ds.ws_bytes, need))) return rc;
+    char *io = (char *)ds.io;
+    hipStream_t s = ds.stream;
+    DET_HIP_CHECK(hipMemcpyAsync(io, (const void *)re, bytes, hipMemcpyHostToDevice, s));
+    DET_HIP_CHECK(hipMemcpyAsync(io + off_im, (const void *)im, bytes, hipMemcpyHostToDevice, s));
+    if (bytes_tw) DET_HIP_CHECK(hipMemcpyAsync(io + off_tw, (const void *)tw, bytes_tw, hipMemcpyHostToDevice, s));
+    if (need) DET_HIP_CHECK(hipStreamWaitEvent(s, ds.ws_free, 0));
+    DET_HIP_CHECK(det::launch_fft_q16((int64_t *)io, (int64_t *)(io + off_im), (const int64_t *)(io + off_tw),
+                                      (int)logn, batch, need ? ds.ws : nullptr, s));
+    if (need) DET_HIP_CHECK(hipEventRecord(ds.ws_free, s));
+    DET_HIP_CHECK(hipMemcpyAsync((void *)re, io, bytes, hipMemcpyDeviceToHost, s));
+    DET_HIP_CHECK(hipMemcpyAsync((void *)im, io + off_im, bytes, hipMemcpyDeviceToHost, s));
+    DET_HIP_CHECK(hipStreamSynchronize(s));
+    return 0;
+}
+
 }  // namespace
 
 extern "C" int64_t det_fail_hip(hipError_t e, const char *what) {
@@ -374,6 +445,9 @@ int64_t dotq(int64_t a, int64_t b, int64_t n) { return __mind_blas_dot_q16_v(a, 
 int64_t dotl1q(int64_t a, int64_t b, int64_t n) { return __mind_blas_dot_l1_q16_v(a, b, n); }
 int64_t doti16(int64_t a, int64_t b, int64_t n) { return __mind_blas_dot_i16_v(a, b, n); }
 int64_t dotf32(int64_t a, int64_t b, int64_t n) { return __mind_blas_dot_f32_v(a, b, n); }
+int64_t fft256(int64_t re, int64_t im, int64_t tw, int64_t logn, int64_t n) {
+    return fft_host(re, im, tw, logn, n, 1);
+}
 int64_t mmf32(int64_t w, int64_t x, int64_t y, int64_t rows, int64_t cols) {
     return __mind_blas_matmul_rmajor_f32_v(w, x, y, rows, cols);
 }
@@ -496,6 +570,20 @@ int64_t det_matmul_rmajor_f32_dev(const float *w, const float *x, float *y, int6
     if (!w || !x || !y) return set_err(DET_ERR_ARG, "null device pointer");
     DET_HIP_CHECK(det::launch_rows_f32(w, x, y, rows, cols, (hipStream_t)stream));
     return 0;
+}
+int64_t det_fft_q16(int64_t *re, int64_t *im, const int64_t *tw, int64_t logn, int64_t n, int64_t batch) {
+    return fft_host((int64_t)(intptr_t)re, (int64_t)(intptr_t)im, (int64_t)(intptr_t)tw, logn, n, batch);
+}
+int64_t det_fft_q16_dev(int64_t *re, int64_t *im, const int64_t *tw, int64_t logn, int64_t n, int64_t batch,
+                        void *stream) {
+    const int64_t rc = fft_check(logn, n, batch);
+    if (rc) return rc > 0 ? 0 : rc;
+    if (!re || !im || (!tw && n >= 4)) return set_err(DET_ERR_ARG, "fft: null device pointer");
+    return fft_dev_run(re, im, tw, (int)logn, batch, (hipStream_t)stream);
+}
+int64_t det_fft_workspace_bytes(int64_t logn, int64_t batch) {
+    if (logn < 0 || logn > 30 || batch <= 0) return 0;
+    return (int64_t)det::fft_workspace_bytes((int)logn, batch);
 }
 int64_t det_dot_dev(int64_t op, const void *a, const void *b, int64_t len, int32_t *out, void *stream) {
     if (op < det::DOT_Q16 || op > det::DOT_I16) return set_err(DET_ERR_ARG, "unknown dot op");

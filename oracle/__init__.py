@@ -21,6 +21,7 @@ import numpy as np
 HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(HERE, "liboracle_det.so")
 REF_PATH = os.path.join(HERE, "_ref", "libmind_intrinsics_ref.so")
+FFT_REF_PATH = os.path.join(HERE, "_ref", "libfft_ref.so")
 
 _i64 = ctypes.c_int64
 _u64 = ctypes.c_uint64
@@ -28,6 +29,7 @@ _p = ctypes.c_void_p
 
 _lib = None
 _ref = None
+_fft_ref = None
 
 
 def build() -> None:
@@ -78,6 +80,15 @@ def lib():
             getattr(L, name).restype = _i64
         L.det_cpu_gemv_q16.argtypes = [_p, _p, _p, _i64, _i64]
         L.det_cpu_gemv_q16.restype = _i64
+        L.det_or_fft_q16.argtypes = [_p, _p, _p, _i64, _i64]
+        L.det_or_fft_q16.restype = _i64
+        L.det_or_fft_twiddles.argtypes = [_p, _i64]
+        L.det_or_fft_twiddles.restype = None
+        for name in ("det_or_fft_input_lcg", "det_or_fft_input_harness"):
+            getattr(L, name).argtypes = [_u64, _p, _p, _i64]
+            getattr(L, name).restype = None
+        L.det_or_fnv1a_i64.argtypes = [_p, _i64]
+        L.det_or_fnv1a_i64.restype = _u64
         L.det_cpu_set_threads.argtypes = [ctypes.c_long]
         L.det_cpu_set_threads.restype = ctypes.c_long
         L.det_cpu_threads_for.argtypes = [_i64]
@@ -100,6 +111,17 @@ def ref_lib():
         R.__mind_blas_set_use_avx2.restype = ctypes.c_int
         _ref = R
     return _ref
+
+
+def fft_ref_lib():
+    """The reference's C FFT (bench/fft/fft_ref.c, fft256_c), or None if not built."""
+    global _fft_ref
+    if _fft_ref is None and os.path.exists(FFT_REF_PATH):
+        R = ctypes.CDLL(FFT_REF_PATH)
+        R.fft256_c.argtypes = [_i64] * 5
+        R.fft256_c.restype = _i64
+        _fft_ref = R
+    return _fft_ref
 
 
 def _ptr(a: np.ndarray) -> int:
@@ -281,3 +303,40 @@ def sha256_i64_le(v: int) -> str:
     import hashlib
 
     return hashlib.sha256(int(v).to_bytes(8, "little", signed=True)).hexdigest()
+
+
+# ------------------------------------------------------------------ Q16 FFT
+
+def fft_q16(re, im, tw, logn: int):
+    """Radix-2 DIT Q16.16 FFT of one transform (copies in, returns (re, im));
+    examples/fft_q16.mind semantics, wrapping int64."""
+    re = np.array(re, np.int64, copy=True)
+    im = np.array(im, np.int64, copy=True)
+    tw = np.ascontiguousarray(tw, np.int64)
+    rc = lib().det_or_fft_q16(_ptr(re), _ptr(im), _ptr(tw), logn, len(re))
+    if rc != 0:
+        raise ValueError(f"fft_q16: n={len(re)} is not 2^{logn}")
+    return re, im
+
+
+def fft_twiddles(n: int) -> np.ndarray:
+    tw = np.zeros(max(n, 2), np.int64)
+    lib().det_or_fft_twiddles(_ptr(tw), n)
+    return tw[:n] if n >= 2 else tw
+
+
+def fft_input_lcg(seed: int, n: int):
+    re = np.empty(n, np.int64); im = np.empty(n, np.int64)
+    lib().det_or_fft_input_lcg(seed, _ptr(re), _ptr(im), n)
+    return re, im
+
+
+def fft_input_harness(seed: int, n: int):
+    re = np.empty(n, np.int64); im = np.empty(n, np.int64)
+    lib().det_or_fft_input_harness(seed, _ptr(re), _ptr(im), n)
+    return re, im
+
+
+def fnv1a_i64(a) -> int:
+    a = np.ascontiguousarray(a, np.int64)
+    return int(lib().det_or_fnv1a_i64(_ptr(a), len(a)))

@@ -13,6 +13,7 @@
  */
 #include "det_oracle.h"
 
+#include <math.h>
 #include <stddef.h>
 
 /* benches/det_matmul_q16.rs:196-205:  s <- s*1664525 + 1013904223 (mod 2^64);
@@ -213,4 +214,89 @@ void det_or_gemv_q16_rows(const int32_t *W, const int32_t *X, int32_t *Y, int64_
 
 void det_or_gemv_i16(const int16_t *W, const int16_t *x, int32_t *y, int64_t rows, int64_t cols) {
     for (int64_t r = 0; r < rows; ++r) y[r] = (int32_t)det_or_dot_i16(W + r * cols, x, cols);
+}
+
+/* ---------------------------------------------------------------- Q16 FFT */
+/* Wrapping int64 arithmetic (MIND's i64 ops lower to plain LLVM add / sub /
+ * mul, which wrap); qmul is the low 64 bits of the product, then >> 16
+ * arithmetic.  Follows examples/fft_q16.mind:15-120 (the fft256 symbol the
+ * reference benches dlopen, benches/fft_q16.rs:66-168). */
+static inline int64_t fft_add(int64_t a, int64_t b) { return (int64_t)((uint64_t)a + (uint64_t)b); }
+static inline int64_t fft_sub(int64_t a, int64_t b) { return (int64_t)((uint64_t)a - (uint64_t)b); }
+static inline int64_t fft_qmul(int64_t a, int64_t b) { return ((int64_t)((uint64_t)a * (uint64_t)b)) >> 16; }
+
+int64_t det_or_fft_q16(int64_t *re, int64_t *im, const int64_t *tw, int64_t logn, int64_t n) {
+    if (logn < 0 || logn > 30 || n != ((int64_t)1 << logn)) return -1;
+    /* in-place bit-reversal permutation (fft_q16.mind:17-42) */
+    for (int64_t i = 0; i < n; ++i) {
+        int64_t r = 0;
+        for (int64_t b = 0; b < logn; ++b) r |= ((i >> b) & 1) << (logn - 1 - b);
+        if (r > i) {
+            int64_t t = re[i]; re[i] = re[r]; re[r] = t;
+            t = im[i]; im[i] = im[r]; im[r] = t;
+        }
+    }
+    if (n < 2) return 0;
+    /* span-2 stage, peeled: the kernel adds / subtracts without a twiddle
+     * (fft_q16.mind:44-70) */
+    for (int64_t a = 0; a < n; a += 2) {
+        const int64_t ur = re[a], ui = im[a], xr = re[a + 1], xi = im[a + 1];
+        re[a] = fft_add(ur, xr); im[a] = fft_add(ui, xi);
+        re[a + 1] = fft_sub(ur, xr); im[a + 1] = fft_sub(ui, xi);
+    }
+    /* spans 4 .. n: butterfly (a, a + h) with twiddle index j * (n / span)
+     * (fft_q16.mind:72-118) */
+    for (int64_t span = 4; span <= n; span <<= 1) {
+        const int64_t h = span >> 1, stride = n / span;
+        for (int64_t base = 0; base < n; base += span)
+            for (int64_t j = 0; j < h; ++j) {
+                const int64_t wr = tw[2 * j * stride], wi = tw[2 * j * stride + 1];
+                const int64_t a = base + j, b = a + h;
+                const int64_t tr = fft_sub(fft_qmul(wr, re[b]), fft_qmul(wi, im[b]));
+                const int64_t ti = fft_add(fft_qmul(wr, im[b]), fft_qmul(wi, re[b]));
+                const int64_t ur = re[a], ui = im[a];
+                re[a] = fft_add(ur, tr); im[a] = fft_add(ui, ti);
+                re[b] = fft_sub(ur, tr); im[b] = fft_sub(ui, ti);
+            }
+    }
+    return 0;
+}
+
+/* tw[2k] = llround(cos(-2 pi k / n) * 65536), tw[2k+1] = llround(sin(..) * 65536),
+ * k < n / 2 (bench/fft/fft_driver.c:23-31, benches/fft_q16.rs:277-286). */
+void det_or_fft_twiddles(int64_t *tw, int64_t n) {
+    for (int64_t k = 0; k < n / 2; ++k) {
+        const double ang = -2.0 * 3.14159265358979323846 * (double)k / (double)n;
+        tw[2 * k] = (int64_t)llround(cos(ang) * 65536.0);
+        tw[2 * k + 1] = (int64_t)llround(sin(ang) * 65536.0);
+    }
+}
+
+/* The Rust / driver signal: re then im, (i64)((i32)u32 >> 13) from the
+ * bench LCG (bench/fft/fft_driver.c:33-37, benches/fft_q16.rs:288-294). */
+void det_or_fft_input_lcg(uint64_t seed, int64_t *re, int64_t *im, int64_t n) {
+    uint64_t s = seed;
+    for (int64_t i = 0; i < n; ++i) re[i] = (int64_t)(((int32_t)det_or_lcg_next_u32(&s)) >> 13);
+    for (int64_t i = 0; i < n; ++i) im[i] = (int64_t)(((int32_t)det_or_lcg_next_u32(&s)) >> 13);
+}
+
+/* The harness.c signal (bench/fft/harness.c:50-53, 73-78): a 64-bit LCG
+ * (6364136223846793005, 1442695040888963407), re[i] then im[i] interleaved
+ * per i, sample (state mod 131072) - 65536. */
+void det_or_fft_input_harness(uint64_t seed, int64_t *re, int64_t *im, int64_t n) {
+    uint64_t s = seed;
+    for (int64_t i = 0; i < n; ++i) {
+        s = s * 6364136223846793005ULL + 1442695040888963407ULL;
+        re[i] = (int64_t)(s % 131072) - 65536;
+        s = s * 6364136223846793005ULL + 1442695040888963407ULL;
+        im[i] = (int64_t)(s % 131072) - 65536;
+    }
+}
+
+/* FNV-1a 64 over the little-endian bytes of n int64 (harness.c:40-45). */
+uint64_t det_or_fnv1a_i64(const int64_t *a, int64_t n) {
+    uint64_t h = 1469598103934665603ULL;
+    const unsigned char *p = (const unsigned char *)a;
+    for (int64_t i = 0; i < n * 8; ++i) { h ^= p[i]; h *= 1099511628211ULL; }
+    return h;
 }

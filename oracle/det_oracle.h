@@ -106,6 +106,16 @@ void det_or_matmul_rmajor_f32(const float *W, const float *x, float *y, int64_t 
  * (tests/cross_substrate_identity.rs:2579-2598). */
 void det_or_gen_f32_unit(uint64_t seed, float *a, int64_t na, float *b, int64_t nb);
 
+/* ---- Q16.16 radix-2 DIT FFT (examples/fft_q16.mind, the fft256 symbol of
+ * benches/fft_q16.rs; bench/fft/fft_ref.c is the same algorithm with the
+ * span-2 stage unpeeled).  In place, n = 2^logn; returns -1 for any other
+ * (logn, n).  Wrapping int64, qmul = low64(a*b) >> 16. ---- */
+int64_t det_or_fft_q16(int64_t *re, int64_t *im, const int64_t *tw, int64_t logn, int64_t n);
+void det_or_fft_twiddles(int64_t *tw, int64_t n);
+void det_or_fft_input_lcg(uint64_t seed, int64_t *re, int64_t *im, int64_t n);
+void det_or_fft_input_harness(uint64_t seed, int64_t *re, int64_t *im, int64_t n);
+uint64_t det_or_fnv1a_i64(const int64_t *a, int64_t n);
+
 #ifdef __cplusplus
 }
 #endif

@@ -64,6 +64,12 @@ def test_product_generators_match_oracle(n):
         np.testing.assert_array_equal(x.view(np.uint32), y.view(np.uint32))
 
 
+def test_product_fft_twiddles_match_oracle():
+    for logn in range(1, 21):
+        n = 1 << logn
+        np.testing.assert_array_equal(mind_amd.fft_twiddles(n)[:n], O.fft_twiddles(n)[:n])
+
+
 def test_product_never_touches_the_oracle():
     """The shipped package and its native sources must not import, link or
     load anything under oracle/ (no CPU fallback path)."""

@@ -335,6 +335,83 @@ def test_f32_null_and_empty_conventions():
     assert L.det_matmul_rmajor_f32(addr(W), addr(x), addr(y), 3, -1) == M.DET_ERR_ARG
 
 
+# ------------------------------------------------------------------ Q16 FFT
+
+def test_canary_fft256_harness(canaries):
+    c = canaries["fft_q16_256_harness"]
+    re, im = O.fft_input_harness(c["seed"], c["n"])
+    tw = O.fft_twiddles(c["n"])
+    note("fft256 n=256 (harness.c signal)")
+    assert M.lib().fft256(addr(re), addr(im), addr(tw), c["logn"], c["n"]) == 0
+    assert format(O.fnv1a_i64(re) ^ O.fnv1a_i64(im), "016x") == c["fnv_xor"]
+
+
+def _fft_oracle_batch(re, im, tw, logn):
+    out_r, out_i = np.empty_like(re), np.empty_like(im)
+    for f in range(re.shape[0]):
+        out_r[f], out_i[f] = O.fft_q16(re[f], im[f], tw, logn)
+    return out_r, out_i
+
+
+FFT_CASES = [(logn, batch) for logn in range(0, 15) for batch in (1, 3, 37)] + [(8, 1000), (5, 513), (11, 9)]
+
+
+@pytest.mark.parametrize("logn,batch", FFT_CASES, ids=[f"n{1 << l}_b{b}" for l, b in FFT_CASES])
+def test_fft_vs_oracle(logn, batch):
+    n = 1 << logn
+    rng = np.random.default_rng(logn * 131 + batch)
+    tw_std = O.fft_twiddles(n) if n >= 2 else np.zeros(2, np.int64)
+    tw_rand = rng.integers(-(1 << 20), 1 << 20, max(n, 2)).astype(np.int64)
+    for fam in ("q16", "wide", "full"):
+        if fam == "q16":
+            x = np.stack([np.concatenate(O.fft_input_lcg(0xF00 + f + logn, n)) for f in range(batch)])
+        elif fam == "wide":
+            x = rng.integers(-(1 << 40), 1 << 40, (batch, 2 * n))
+        else:   # full int64 range: every add, product and shift wraps
+            x = rng.integers(np.iinfo(np.int64).min, np.iinfo(np.int64).max, (batch, 2 * n), dtype=np.int64,
+                             endpoint=True)
+        re, im = np.ascontiguousarray(x[:, :n]), np.ascontiguousarray(x[:, n:])
+        for tw in ((tw_std, tw_rand) if fam != "q16" else (tw_std,)):
+            note(f"fft {fam} n={n} batch={batch}")
+            got = M.fft_q16(re, im, tw, logn)
+            want = _fft_oracle_batch(re, im, tw, logn)
+            assert np.array_equal(got[0], want[0]) and np.array_equal(got[1], want[1]), (fam, logn)
+
+
+def test_fft_dev_entry_point_and_workspace_path():
+    s = M.Stream()
+    for logn, batch in ((8, 4099), (12, 3), (13, 2)):
+        n = 1 << logn
+        x = np.random.default_rng(logn).integers(-(1 << 30), 1 << 30, (2, batch, n))
+        re, im = np.ascontiguousarray(x[0]), np.ascontiguousarray(x[1])
+        tw = O.fft_twiddles(n)
+        sel = sorted({0, batch - 1, batch // 2})
+        want = _fft_oracle_batch(re[sel], im[sel], tw, logn)
+        dre, dim_, dtw = M.DeviceBuffer.from_array(re), M.DeviceBuffer.from_array(im), M.DeviceBuffer.from_array(tw)
+        for rep in range(2):   # in place: the second call transforms the first call's output
+            note(f"det_fft_q16_dev n={n} batch={batch} rep={rep}")
+            M.check(M.lib().det_fft_q16_dev(dre.ptr, dim_.ptr, dtw.ptr, logn, n, batch, s.ptr))
+            s.sync()
+            gr = dre.to_array(np.int64, (batch, n))
+            gi = dim_.to_array(np.int64, (batch, n))
+            assert np.array_equal(gr[sel], want[0]) and np.array_equal(gi[sel], want[1])
+            want = _fft_oracle_batch(want[0], want[1], tw, logn)
+        assert M.lib().det_fft_workspace_bytes(logn, batch) == (0 if logn <= 11 else 16 * batch * n)
+        dre.free(); dim_.free(); dtw.free()
+
+
+def test_fft_argument_conventions():
+    L = M.lib()
+    z = np.zeros(16, np.int64)
+    assert L.fft256(addr(z), addr(z), addr(z), 3, 6) == M.DET_ERR_ARG        # n != 2^logn
+    assert L.fft256(addr(z), addr(z), addr(z), 31, 1 << 31) == M.DET_ERR_ARG
+    assert L.fft256(addr(z), addr(z), addr(z), 4, 0) == 0                     # nothing to do
+    assert L.fft256(0, addr(z), addr(z), 4, 16) == M.DET_ERR_ARG
+    assert L.det_fft_q16(addr(z), addr(z), addr(z), 4, 16, 0) == 0
+    one_r, one_i = np.array([12345], np.int64), np.array([-7], np.int64)
+    assert L.fft256(addr(one_r), addr(one_i), 0, 0, 1) == 0 and one_r[0] == 12345 and one_i[0] == -7
+
+
 # ------------------------------------------------------------------ int8 shapes
 
 I8_SHAPES = [(1, 1, 1), (1, 64, 1), (3, 5, 7), (16, 16, 16), (17, 33, 65), (64, 64, 64), (255, 257, 129),

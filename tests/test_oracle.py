@@ -398,3 +398,141 @@ def test_config_generators_shape():
     sat = np.abs(a) == 2147483647
     assert 0.005 < sat.mean() < 0.015
     assert np.abs(a[~sat]).max() <= 4 << 16
+
+
+# ------------------------------------------------------------------ Q16 FFT
+
+def _fft_harness_case(canaries):
+    c = canaries["fft_q16_256_harness"]
+    re, im = O.fft_input_harness(c["seed"], c["n"])
+    return c, re, im, O.fft_twiddles(c["n"])
+
+
+def test_fft_golden_harness_hash(canaries):
+    c, re, im, tw = _fft_harness_case(canaries)
+    r, i = O.fft_q16(re, im, tw, c["logn"])
+    assert format(O.fnv1a_i64(r) ^ O.fnv1a_i64(i), "016x") == c["fnv_xor"]
+
+
+def _py_fft(re, im, tw, logn, mistake=None):
+    """Independent pure-Python restatement (Python ints, wrapped to int64),
+    with an optional planted mistake."""
+    n = 1 << logn
+    m64 = (1 << 64) - 1
+
+    def s64(v):
+        v &= m64
+        return v - (1 << 64) if v >> 63 else v
+
+    def qmul(a, b):
+        return s64(a * b) >> 16
+
+    re, im = [int(v) for v in re], [int(v) for v in im]
+    if mistake != "no_bitrev":
+        perm = [int(format(i, f"0{logn}b")[::-1], 2) if logn else 0 for i in range(n)]
+        re, im = [re[p] for p in perm], [im[p] for p in perm]
+    span = 2
+    while span <= n:
+        h = span // 2
+        for base in range(0, n, span):
+            for j in range(h):
+                a, b = base + j, base + j + h
+                if span == 2:
+                    tr, ti = re[b], im[b]
+                else:
+                    k = (j * (n // span) + (1 if mistake == "tw_index" else 0)) % (n // 2)
+                    wr, wi = int(tw[2 * k]), int(tw[2 * k + 1])
+                    if mistake == "conj":
+                        wi = -wi
+                    if mistake == "round":
+                        tr = s64(wr * re[b] - wi * im[b]) >> 16
+                        ti = s64(wr * im[b] + wi * re[b]) >> 16
+                    else:
+                        tr = s64(qmul(wr, re[b]) - qmul(wi, im[b]))
+                        ti = s64(qmul(wr, im[b]) + qmul(wi, re[b]))
+                re[a], im[a], re[b], im[b] = (s64(re[a] + tr), s64(im[a] + ti), s64(re[a] - tr), s64(im[a] - ti))
+        span *= 2
+    return np.array(re, np.int64), np.array(im, np.int64)
+
+
+def test_fft_python_restatement_and_planted_mistakes(canaries):
+    # the hash rejects a missing bit reversal, a shifted twiddle index, the
+    # conjugate twiddle and a floor after the sum instead of per product
+    c, re, im, tw = _fft_harness_case(canaries)
+
+    def h(v):
+        return format(O.fnv1a_i64(v[0]) ^ O.fnv1a_i64(v[1]), "016x")
+
+    assert h(_py_fft(re, im, tw, 8)) == c["fnv_xor"]
+    for mistake in ("no_bitrev", "tw_index", "conj", "round"):
+        assert h(_py_fft(re, im, tw, 8, mistake)) != c["fnv_xor"], mistake
+    rng = np.random.default_rng(5)
+    for logn in (0, 1, 2, 3, 5, 7):
+        n = 1 << logn
+        x = rng.integers(-(1 << 40), 1 << 40, (2, n))
+        t = O.fft_twiddles(n) if n >= 2 else np.zeros(2, np.int64)
+        got = O.fft_q16(x[0], x[1], t, logn)
+        want = _py_fft(x[0], x[1], t, logn)
+        assert np.array_equal(got[0], want[0]) and np.array_equal(got[1], want[1]), logn
+
+
+@pytest.mark.skipif(O.fft_ref_lib() is None, reason="oracle/_ref not built (reference tree absent)")
+@pytest.mark.parametrize("logn", list(range(1, 14)))
+def test_fft_matches_reference_c_live(logn):
+    # bench/fft/fft_ref.c (span-2 stage unpeeled) equals the peeled kernel
+    # whenever tw[0] = (65536, 0) and |x| < 2^47; inputs below 2^30 keep
+    # every intermediate far from int64 overflow (the C file's products are
+    # signed, so overflow would be undefined there)
+    R = O.fft_ref_lib()
+    n = 1 << logn
+    rng = np.random.default_rng(logn)
+    tws = [O.fft_twiddles(n)]
+    rt = rng.integers(-(1 << 20), 1 << 20, n).astype(np.int64)
+    rt[0], rt[1] = 65536, 0
+    tws.append(rt)
+    for tw in tws:
+        for x in (O.fft_input_harness(0x1234567 + logn, n), O.fft_input_lcg(0x12345678 ^ logn, n),
+                  tuple(rng.integers(-(1 << 30), 1 << 30, (2, n)))):
+            a, b = np.array(x[0], np.int64), np.array(x[1], np.int64)
+            got = O.fft_q16(a, b, tw, logn)
+            R.fft256_c(a.ctypes.data, b.ctypes.data, tw.ctypes.data, logn, n)
+            assert np.array_equal(got[0], a) and np.array_equal(got[1], b)
+
+
+def test_fft_close_to_the_float_dft():
+    # each stage floors every product (error < 1 unit per product) on top of
+    # twiddles rounded to 2^-16: the result is within a few units * n of the
+    # exact DFT of the input; a wrong index, sign or permutation is off by
+    # O(|X|)
+    for logn in (2, 4, 8, 10):
+        n = 1 << logn
+        re, im = O.fft_input_lcg(0xF0F0 + logn, n)
+        got = O.fft_q16(re, im, O.fft_twiddles(n), logn)
+        X = np.fft.fft(re.astype(np.float64) + 1j * im.astype(np.float64))
+        err = np.max(np.abs((got[0] + 1j * got[1]) - X))
+        bound = 4.0 * logn * (n + np.max(np.abs(X)) * 2.0 ** -16)
+        assert err <= bound, (logn, err, bound)
+        assert np.max(np.abs(X)) > 100 * bound
+
+
+@pytest.mark.skipif(O.fft_ref_lib() is None, reason="oracle/_ref not built (reference tree absent)")
+def test_fft_peeled_stage_differs_from_the_c_file_when_tw0_is_not_one():
+    # The kernel this build follows (examples/fft_q16.mind) peels the span-2
+    # stage as a plain add / subtract; bench/fft/fft_ref.c multiplies by tw[0].
+    # They agree for the standard table (tw[0] = (65536, 0)); with another
+    # tw[0] they differ, and this build returns the peeled kernel's values.
+    n, logn = 16, 4
+    tw = O.fft_twiddles(n)
+    tw[0], tw[1] = 32768, 0
+    re, im = O.fft_input_lcg(7, n)
+    a, b = re.copy(), im.copy()
+    O.fft_ref_lib().fft256_c(a.ctypes.data, b.ctypes.data, tw.ctypes.data, logn, n)
+    got = O.fft_q16(re, im, tw, logn)
+    assert not np.array_equal(got[0], a)
+    want = _py_fft(re, im, tw, logn)
+    assert np.array_equal(got[0], want[0]) and np.array_equal(got[1], want[1])
+
+
+def test_fft_rejects_non_power_of_two():
+    with pytest.raises(ValueError):
+        O.fft_q16(np.zeros(6, np.int64), np.zeros(6, np.int64), np.zeros(6, np.int64), 2)
