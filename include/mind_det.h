@@ -184,6 +184,10 @@ int64_t det_matmul_rmajor_f32_dev(const float *w, const float *x, float *y, int6
  * size det_fft_workspace_bytes reports). */
 int64_t det_fft_q16_dev(int64_t *re, int64_t *im, const int64_t *tw, int64_t logn, int64_t n, int64_t batch,
                         void *stream);
+/* Out-of-place form: reads in_re / in_im, writes out_re / out_im (each pair
+ * either identical, which is in place, or not overlapping). */
+int64_t det_fft_q16_oop_dev(const int64_t *in_re, const int64_t *in_im, int64_t *out_re, int64_t *out_im,
+                            const int64_t *tw, int64_t logn, int64_t n, int64_t batch, void *stream);
 int64_t det_fft_workspace_bytes(int64_t logn, int64_t batch);
 /* Workspace bytes op (DET_OP_*) needs at this shape (0 for int8). */
 int64_t det_workspace_bytes(int64_t op, int64_t m, int64_t k, int64_t n);

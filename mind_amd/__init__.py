@@ -68,6 +68,8 @@ def _bind(L):
     L.fft256.argtypes = [_i64] * 5; L.fft256.restype = _i64
     L.det_fft_q16.argtypes = [_p, _p, _p, _i64, _i64, _i64]; L.det_fft_q16.restype = _i64
     L.det_fft_q16_dev.argtypes = [_p, _p, _p, _i64, _i64, _i64, _p]; L.det_fft_q16_dev.restype = _i64
+    L.det_fft_q16_oop_dev.argtypes = [_p, _p, _p, _p, _p, _i64, _i64, _i64, _p]
+    L.det_fft_q16_oop_dev.restype = _i64
     L.det_fft_workspace_bytes.argtypes = [_i64, _i64]; L.det_fft_workspace_bytes.restype = _i64
     L.det_matmul_rmajor_f32_dev.argtypes = [_p, _p, _p, _i64, _i64, _p]
     L.det_matmul_rmajor_f32_dev.restype = _i64

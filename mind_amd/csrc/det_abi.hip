@@ -319,10 +319,11 @@ int64_t fft_check(int64_t logn, int64_t n, int64_t batch) {
 
 // Device-pointer FFT on stream s; the n >= 4096 path borrows the workspace
 // arena (ordered after its previous user).  Call with ds.mu NOT held.
-int64_t fft_dev_run(int64_t *re, int64_t *im, const int64_t *tw, int logn, int64_t batch, hipStream_t s) {
+int64_t fft_dev_run(const int64_t *sre, const int64_t *sim, int64_t *dre, int64_t *dim, const int64_t *tw, int logn,
+                    int64_t batch, hipStream_t s) {
     const size_t need = det::fft_workspace_bytes(logn, batch);
     if (need == 0) {
-        DET_HIP_CHECK(det::launch_fft_q16(re, im, tw, logn, batch, nullptr, s));
+        DET_HIP_CHECK(det::launch_fft_q16(sre, sim, dre, dim, tw, logn, batch, nullptr, s));
         return 0;
     }
     int64_t rc = 0;
@@ -333,7 +334,7 @@ int64_t fft_dev_run(int64_t *re, int64_t *im, const int64_t *tw, int logn, int64
     if ((rc = ensure_stream(ds))) return rc;
     if ((rc = ensure(&ds.ws, &ds.ws_bytes, need))) return rc;
     DET_HIP_CHECK(hipStreamWaitEvent(s, ds.ws_free, 0));
-    DET_HIP_CHECK(det::launch_fft_q16(re, im, tw, logn, batch, ds.ws, s));
+    DET_HIP_CHECK(det::launch_fft_q16(sre, sim, dre, dim, tw, logn, batch, ds.ws, s));
     DET_HIP_CHECK(hipEventRecord(ds.ws_free, s));
     return 0;
 }
@@ -360,8 +361,9 @@ int64_t fft_host(int64_t re, int64_t im, int64_t tw, int64_t logn, int64_t n, in
     DET_HIP_CHECK(hipMemcpyAsync(io + off_im, (const void *)im, bytes, hipMemcpyHostToDevice, s));
     if (bytes_tw) DET_HIP_CHECK(hipMemcpyAsync(io + off_tw, (const void *)tw, bytes_tw, hipMemcpyHostToDevice, s));
     if (need) DET_HIP_CHECK(hipStreamWaitEvent(s, ds.ws_free, 0));
-    DET_HIP_CHECK(det::launch_fft_q16((int64_t *)io, (int64_t *)(io + off_im), (const int64_t *)(io + off_tw),
-                                      (int)logn, batch, need ? ds.ws : nullptr, s));
+    int64_t *dre = (int64_t *)io, *dim = (int64_t *)(io + off_im);
+    DET_HIP_CHECK(det::launch_fft_q16(dre, dim, dre, dim, (const int64_t *)(io + off_tw), (int)logn, batch,
+                                      need ? ds.ws : nullptr, s));
     if (need) DET_HIP_CHECK(hipEventRecord(ds.ws_free, s));
     DET_HIP_CHECK(hipMemcpyAsync((void *)re, io, bytes, hipMemcpyDeviceToHost, s));
     DET_HIP_CHECK(hipMemcpyAsync((void *)im, io + off_im, bytes, hipMemcpyDeviceToHost, s));
@@ -579,7 +581,23 @@ int64_t det_fft_q16_dev(int64_t *re, int64_t *im, const int64_t *tw, int64_t log
     const int64_t rc = fft_check(logn, n, batch);
     if (rc) return rc > 0 ? 0 : rc;
     if (!re || !im || (!tw && n >= 4)) return set_err(DET_ERR_ARG, "fft: null device pointer");
-    return fft_dev_run(re, im, tw, (int)logn, batch, (hipStream_t)stream);
+    return fft_dev_run(re, im, re, im, tw, (int)logn, batch, (hipStream_t)stream);
+}
+int64_t det_fft_q16_oop_dev(const int64_t *in_re, const int64_t *in_im, int64_t *out_re, int64_t *out_im,
+                            const int64_t *tw, int64_t logn, int64_t n, int64_t batch, void *stream) {
+    const int64_t rc = fft_check(logn, n, batch);
+    if (rc) return rc > 0 ? 0 : rc;
+    if (!in_re || !in_im || !out_re || !out_im || (!tw && n >= 4))
+        return set_err(DET_ERR_ARG, "fft: null device pointer");
+    const int64_t *ranges[4] = {in_re, in_im, out_re, out_im};
+    const size_t bytes = (size_t)batch * n * 8;
+    for (int a = 0; a < 2; ++a)
+        for (int b = 2; b < 4; ++b) {
+            const uintptr_t x = (uintptr_t)ranges[a], y = (uintptr_t)ranges[b];
+            if (x != y && x < y + bytes && y < x + bytes)
+                return set_err(DET_ERR_ARG, "fft: input and output overlap without being the same buffer");
+        }
+    return fft_dev_run(in_re, in_im, out_re, out_im, tw, (int)logn, batch, (hipStream_t)stream);
 }
 int64_t det_fft_workspace_bytes(int64_t logn, int64_t batch) {
     if (logn < 0 || logn > 30 || batch <= 0) return 0;

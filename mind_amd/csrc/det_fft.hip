@@ -21,7 +21,11 @@
 //   * n <= 16        : one FFT per thread (fft_small_kernel);
 //   * 32 <= n <= 2048: n / 16 lanes per FFT, passes separated by an LDS
 //                      transpose, bit reversal folded into the first load,
-//                      one HBM read and one write per point (fft_lds_kernel);
+//                      one HBM read and one write per point; in int32 when a
+//                      bound on the inputs proves that every intermediate
+//                      fits (same integers, cheaper products:
+//                      fft_lds_kernel), the other groups in int64
+//                      (fft_lds_general_kernel);
 //   * n >= 4096      : one global-memory pass per 4-bit window, out of place
 //                      through a workspace (fft_pass_kernel).
 #include "det_common.h"
@@ -30,26 +34,46 @@
 namespace det {
 namespace fft {
 
-__device__ __forceinline__ int64_t wadd(int64_t a, int64_t b) { return (int64_t)((uint64_t)a + (uint64_t)b); }
-__device__ __forceinline__ int64_t wsub(int64_t a, int64_t b) { return (int64_t)((uint64_t)a - (uint64_t)b); }
-__device__ __forceinline__ int64_t qmul(int64_t w, int64_t v) {
-    return ((int64_t)((uint64_t)w * (uint64_t)v)) >> 16;
+// Value arithmetic.  int64_t: the general path, wrapping like MIND's i64.
+// int32_t: the bounded path, only taken when every intermediate value is
+// known to fit in int32 (then 32-bit arithmetic gives the same integers):
+// one signed 32 x 32 -> 64 product per qmul, and the shifted product fits in
+// int32 because |qmul(w, x)| <= |x| for |w| <= 2^16.
+__device__ __forceinline__ int64_t vadd(int64_t a, int64_t b) { return (int64_t)((uint64_t)a + (uint64_t)b); }
+__device__ __forceinline__ int64_t vsub(int64_t a, int64_t b) { return (int64_t)((uint64_t)a - (uint64_t)b); }
+__device__ __forceinline__ int32_t vadd(int32_t a, int32_t b) { return (int32_t)((uint32_t)a + (uint32_t)b); }
+__device__ __forceinline__ int32_t vsub(int32_t a, int32_t b) { return (int32_t)((uint32_t)a - (uint32_t)b); }
+__device__ __forceinline__ int64_t qm(int64_t w, int64_t v) { return ((int64_t)((uint64_t)w * (uint64_t)v)) >> 16; }
+__device__ __forceinline__ int32_t qm(int64_t w, int32_t v) {
+    const int64_t p = (int64_t)(int32_t)w * (int64_t)v;
+    return (int32_t)(p >> 16);
 }
 
-// One butterfly of stage b (b == 0: the peeled span-2 stage) on (a, b).
-__device__ __forceinline__ void butterfly(int64_t &ar, int64_t &ai, int64_t &br, int64_t &bi, int64_t wr, int64_t wi,
-                                          bool peeled) {
-    int64_t tr, ti;
+// One butterfly (peeled: the span-2 stage, no twiddle) on (a, b).
+template <typename V>
+__device__ __forceinline__ void butterfly(V &ar, V &ai, V &br, V &bi, int64_t wr, int64_t wi, bool peeled) {
+    V tr, ti;
     if (peeled) {
         tr = br, ti = bi;
     } else {
-        tr = wsub(qmul(wr, br), qmul(wi, bi));
-        ti = wadd(qmul(wr, bi), qmul(wi, br));
+        tr = vsub(qm(wr, br), qm(wi, bi));
+        ti = vadd(qm(wr, bi), qm(wi, br));
     }
-    const int64_t ur = ar, ui = ai;
-    ar = wadd(ur, tr), ai = wadd(ui, ti);
-    br = wsub(ur, tr), bi = wsub(ui, ti);
+    const V ur = ar, ui = ai;
+    ar = vadd(ur, tr), ai = vadd(ui, ti);
+    br = vsub(ur, tr), bi = vsub(ui, ti);
 }
+
+// Largest input magnitude for which a 2^logn-point transform stays in int32
+// when every twiddle component is within [-2^16, 2^16]: |qmul(w, x)| <= |x|,
+// so a span-2 stage at most doubles the largest magnitude and each later
+// stage at most triples it (|a +- (qmul - qmul)| <= 3 max).
+__host__ __device__ constexpr int64_t i32_input_bound(int logn) {
+    int64_t g = logn >= 1 ? 2 : 1;
+    for (int i = 1; i < logn; ++i) g *= 3;
+    return 2147483647LL / g;
+}
+constexpr int64_t TW_SMALL = 65536;
 
 __device__ __forceinline__ uint32_t bitrev(uint32_t v, int bits) { return bits ? __brev(v) >> (32 - bits) : 0u; }
 
@@ -58,35 +82,110 @@ __device__ __forceinline__ uint32_t win_pos(uint32_t t, int r, int s) {
     return ((t >> s) << (s + 4)) | ((uint32_t)r << s) | (t & ((1u << s) - 1u));
 }
 
-// Stages [b0, b1) of a window at s on the 16 registers of one lane.
-__device__ __forceinline__ void run_window(int64_t (&xr)[16], int64_t (&xi)[16], const int64_t *__restrict__ tw,
+// Stage b = s + RB of a window at s: butterflies between registers r and
+// r | 2^RB (register indices are compile-time, so the points stay in VGPRs).
+template <int RB, typename V>
+__device__ __forceinline__ void window_stage(V (&xr)[16], V (&xi)[16], const int64_t *__restrict__ tw,
+                                             uint32_t t, int s, int logn) {
+    const int b = s + RB;
+    const uint32_t half_mask = (1u << b) - 1u;
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+        if (r & (1 << RB)) continue;
+        constexpr int bit = 1 << RB;
+        int64_t wr = 0, wi = 0;
+        if (b > 0) {
+            const uint32_t k = (win_pos(t, r, s) & half_mask) << (logn - 1 - b);
+            wr = tw[2 * k], wi = tw[2 * k + 1];
+        }
+        butterfly(xr[r], xi[r], xr[r | bit], xi[r | bit], wr, wi, b == 0);
+    }
+}
+
+// Stages [b0, b1) of a window at s (b0 >= s, b1 <= s + 4), in order.
+template <typename V>
+__device__ __forceinline__ void run_window(V (&xr)[16], V (&xi)[16], const int64_t *__restrict__ tw,
                                            uint32_t t, int s, int b0, int b1, int logn) {
-    for (int b = b0; b < b1; ++b) {
-        const int rb = b - s;   // register bit of this stage
-        const uint32_t half_mask = (1u << b) - 1u;
+    if (b0 <= s && s < b1) window_stage<0>(xr, xi, tw, t, s, logn);
+    if (b0 <= s + 1 && s + 1 < b1) window_stage<1>(xr, xi, tw, t, s, logn);
+    if (b0 <= s + 2 && s + 2 < b1) window_stage<2>(xr, xi, tw, t, s, logn);
+    if (b0 <= s + 3 && s + 3 < b1) window_stage<3>(xr, xi, tw, t, s, logn);
+}
+
+// ---- int32 path: twiddles preloaded as int32 (valid when every component
+// is within [-2^16, 2^16]).  Slot (2^rb - 1) + j of a window's table holds
+// the twiddle of stage s + rb for butterflies whose register index has low
+// bits j (the position bits below the stage bit are those low bits and the
+// lane's own bits, so 1 + 2 + 4 + 8 slots cover a window).
+struct WinTw {
+    int32_t r[15], i[15];
+};
+
+template <int S, int B0, int B1, int LOGN>
+__device__ __forceinline__ void load_win_tw(WinTw &w, const int64_t *__restrict__ tw, uint32_t t) {
+#pragma unroll
+    for (int rb = 0; rb < 4; ++rb) {
+        const int b = S + rb;
+        if (b < B0 || b >= B1 || b == 0) continue;
+#pragma unroll
+        for (int j = 0; j < (1 << rb); ++j) {
+            const uint32_t k = (win_pos(t, j, S) & ((1u << b) - 1u)) << (LOGN - 1 - b);
+            int32_t wr = (int32_t)tw[2 * k], wi = (int32_t)tw[2 * k + 1];
+            if (S == 0) {   // window 0: the same twiddles in every lane
+                wr = __builtin_amdgcn_readfirstlane(wr);
+                wi = __builtin_amdgcn_readfirstlane(wi);
+            }
+            w.r[(1 << rb) - 1 + j] = wr, w.i[(1 << rb) - 1 + j] = wi;
+        }
+    }
+}
+
+template <int S, int B0, int B1>
+__device__ __forceinline__ void window32(int32_t (&xr)[16], int32_t (&xi)[16], const WinTw &w) {
+#pragma unroll
+    for (int rb = 0; rb < 4; ++rb) {
+        const int b = S + rb;
+        if (b < B0 || b >= B1) continue;
 #pragma unroll
         for (int r = 0; r < 16; ++r) {
             if (r & (1 << rb)) continue;
+            const int slot = (1 << rb) - 1 + (r & ((1 << rb) - 1));
             const int q = r | (1 << rb);
-            int64_t wr = 0, wi = 0;
-            if (b > 0) {
-                const uint32_t k = (win_pos(t, r, s) & half_mask) << (logn - 1 - b);
-                wr = tw[2 * k], wi = tw[2 * k + 1];
-            }
-            butterfly(xr[r], xi[r], xr[q], xi[q], wr, wi, b == 0);
+            butterfly(xr[r], xi[r], xr[q], xi[q], (int64_t)w.r[slot], (int64_t)w.i[slot], b == 0);
         }
     }
+}
+
+// Re-layout from window SP to window S through LDS, (re, im) as one 8-byte
+// element at index pos + pos / 16.
+template <int SP, int S>
+__device__ __forceinline__ void transpose32(int32_t (&xr)[16], int32_t (&xi)[16], uint32_t t, uint64_t *smf) {
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+        const uint32_t pos = win_pos(t, r, SP);
+        smf[pos + (pos >> 4)] = (uint64_t)(uint32_t)xr[r] | ((uint64_t)(uint32_t)xi[r] << 32);
+    }
+    __syncthreads();
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+        const uint32_t pos = win_pos(t, r, S);
+        const uint64_t v = smf[pos + (pos >> 4)];
+        xr[r] = (int32_t)(uint32_t)v, xi[r] = (int32_t)(uint32_t)(v >> 32);
+    }
+    __syncthreads();
 }
 
 // ---------------------------------------------------------------- n <= 16
 // One thread per FFT; registers indexed by position.
 template <int LOGN>
-__global__ __launch_bounds__(256) void fft_small_kernel(int64_t *__restrict__ re, int64_t *__restrict__ im,
-                                                        const int64_t *__restrict__ tw, int64_t batch) {
+__global__ __launch_bounds__(256) void fft_small_kernel(const int64_t *__restrict__ sre,
+                                                        const int64_t *__restrict__ sim, int64_t *__restrict__ dre,
+                                                        int64_t *__restrict__ dim, const int64_t *__restrict__ tw,
+                                                        int64_t batch) {
     constexpr int N = 1 << LOGN;
     const int64_t f = (int64_t)blockIdx.x * 256 + threadIdx.x;
     if (f >= batch) return;
-    int64_t *R = re + f * N, *I = im + f * N;
+    const int64_t *R = sre + f * N, *I = sim + f * N;
     int64_t xr[N], xi[N];
 #pragma unroll
     for (int p = 0; p < N; ++p) {
@@ -106,68 +205,157 @@ __global__ __launch_bounds__(256) void fft_small_kernel(int64_t *__restrict__ re
             butterfly(xr[p], xi[p], xr[p | (1 << b)], xi[p | (1 << b)], wr, wi, b == 0);
         }
 #pragma unroll
-    for (int p = 0; p < N; ++p) R[p] = xr[p], I[p] = xi[p];
+    for (int p = 0; p < N; ++p) dre[f * N + p] = xr[p], dim[f * N + p] = xi[p];
 }
 
 // ---------------------------------------------------------------- 32 <= n <= 2048
 // L = n / 16 lanes per FFT, 256 / L FFTs per 256-thread block, a block-
-// uniform grid-stride loop over the batch.  LDS holds one component of every
-// FFT of the block at a time (index pos + pos / 16: one pad int64 per 16, so
-// the 16 lanes of a window write 16 distinct bank pairs).
-template <int LOGN>
-__global__ __launch_bounds__(256) void fft_lds_kernel(int64_t *__restrict__ re, int64_t *__restrict__ im,
-                                                      const int64_t *__restrict__ tw, int64_t batch) {
-    constexpr int N = 1 << LOGN, L = N / 16, FPB = 256 / L, NP = (LOGN + 3) / 4;
-    constexpr int STRIDE = N + N / 16;
-    static_assert(LOGN >= 5 && LOGN <= 11, "LDS FFT size");
-    __shared__ int64_t sm[FPB * STRIDE];
-    const int f = threadIdx.x / L;
-    const uint32_t t = threadIdx.x % L;
-    int64_t *smf = sm + f * STRIDE;
-    for (int64_t f0 = (int64_t)blockIdx.x * FPB; f0 < batch; f0 += (int64_t)gridDim.x * FPB) {
-        const int64_t fi = f0 + f;
-        const bool live = fi < batch;
-        int64_t *R = re + (live ? fi : 0) * N, *I = im + (live ? fi : 0) * N;
-        int64_t xr[16], xi[16];
-        // window 0 (s = 0): position 16 t + r holds x[bitrev(16 t + r)]
-        const uint32_t tb = bitrev(t, LOGN - 4);
+// uniform grid-stride loop over the batch.  Reads src, writes dst (equal for
+// in place: a lane group holds its whole transform before storing).  LDS
+// holds one component of every FFT of the block at a time, index
+// pos + pos / 16 (one pad element per 16, so the 16 lanes of a window hit
+// distinct banks).  Per block of transforms the path is chosen once, block-
+// uniformly (the LDS transposes need the whole block): int32 when the table
+// is small and every loaded value is within i32_input_bound, else int64.
+template <int LOGN, typename V>
+__device__ __forceinline__ void lds_transform(V (&xr)[16], V (&xi)[16], const int64_t *__restrict__ tw, uint32_t t,
+                                              V *smf) {
+    constexpr int N = 1 << LOGN, NP = (LOGN + 3) / 4;
+    run_window(xr, xi, tw, t, 0, 0, 4, LOGN);
 #pragma unroll
-        for (int r = 0; r < 16; ++r) {
-            const uint32_t src = (bitrev((uint32_t)r, 4) << (LOGN - 4)) | tb;
-            xr[r] = live ? R[src] : 0;
-            xi[r] = live ? I[src] : 0;
-        }
-        run_window(xr, xi, tw, t, 0, 0, 4, LOGN);
+    for (int p = 1; p < NP; ++p) {
+        const int sp = 4 * (p - 1) < LOGN - 4 ? 4 * (p - 1) : LOGN - 4;   // previous window
+        const int s = 4 * p < LOGN - 4 ? 4 * p : LOGN - 4;
 #pragma unroll
-        for (int p = 1; p < NP; ++p) {
-            const int sp = 4 * (p - 1) < LOGN - 4 ? 4 * (p - 1) : LOGN - 4;   // previous window
-            const int s = 4 * p < LOGN - 4 ? 4 * p : LOGN - 4;
+        for (int c = 0; c < 2; ++c) {
+            V(&x)[16] = c ? xi : xr;
 #pragma unroll
-            for (int c = 0; c < 2; ++c) {
-                int64_t(&x)[16] = c ? xi : xr;
-#pragma unroll
-                for (int r = 0; r < 16; ++r) {
-                    const uint32_t pos = win_pos(t, r, sp);
-                    smf[pos + (pos >> 4)] = x[r];
-                }
-                __syncthreads();
-#pragma unroll
-                for (int r = 0; r < 16; ++r) {
-                    const uint32_t pos = win_pos(t, r, s);
-                    x[r] = smf[pos + (pos >> 4)];
-                }
-                __syncthreads();
+            for (int r = 0; r < 16; ++r) {
+                const uint32_t pos = win_pos(t, r, sp);
+                smf[pos + (pos >> 4)] = x[r];
             }
-            run_window(xr, xi, tw, t, s, 4 * p, 4 * p + 4 < LOGN ? 4 * p + 4 : LOGN, LOGN);
-        }
-        if (live) {
-            const int s = 4 * (NP - 1) < LOGN - 4 ? 4 * (NP - 1) : LOGN - 4;
+            __syncthreads();
 #pragma unroll
             for (int r = 0; r < 16; ++r) {
                 const uint32_t pos = win_pos(t, r, s);
-                R[pos] = xr[r], I[pos] = xi[r];
+                x[r] = smf[pos + (pos >> 4)];
             }
+            __syncthreads();
         }
+        run_window(xr, xi, tw, t, s, 4 * p, 4 * p + 4 < LOGN ? 4 * p + 4 : LOGN, LOGN);
+    }
+    (void)N;
+}
+
+// A block handles FPB transforms at a time ("group" f0 .. f0 + FPB - 1);
+// lane t of slot f loads window 0 of transform f0 + f.
+template <int LOGN>
+__device__ __forceinline__ bool load_group(const int64_t *__restrict__ sre, const int64_t *__restrict__ sim,
+                                           int64_t fi, bool live, uint32_t t, int64_t (&xr)[16], int64_t (&xi)[16]) {
+    constexpr int N = 1 << LOGN;
+    constexpr int64_t BOUND = i32_input_bound(LOGN);
+    const int64_t off = (live ? fi : 0) * N;
+    // window 0 (s = 0): position 16 t + r holds x[bitrev(16 t + r)]
+    const uint32_t tb = bitrev(t, LOGN - 4);
+    bool fits = true;
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+        const uint32_t src = (bitrev((uint32_t)r, 4) << (LOGN - 4)) | tb;
+        xr[r] = live ? sre[off + src] : 0;
+        xi[r] = live ? sim[off + src] : 0;
+        fits = fits && xr[r] >= -BOUND && xr[r] <= BOUND && xi[r] >= -BOUND && xi[r] <= BOUND;
+    }
+    return fits;
+}
+
+template <int LOGN, typename V>
+__device__ __forceinline__ void store_group(int64_t *__restrict__ dre, int64_t *__restrict__ dim, int64_t fi,
+                                            uint32_t t, const V (&xr)[16], const V (&xi)[16]) {
+    constexpr int N = 1 << LOGN, NP = (LOGN + 3) / 4;
+    constexpr int S_LAST = 4 * (NP - 1) < LOGN - 4 ? 4 * (NP - 1) : LOGN - 4;
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+        const uint32_t pos = win_pos(t, r, S_LAST);
+        dre[fi * N + pos] = (int64_t)xr[r], dim[fi * N + pos] = (int64_t)xi[r];
+    }
+}
+
+// int32 kernel: every group whose inputs are within i32_input_bound (and a
+// table within [-2^16, 2^16]) is transformed here; the others are left to
+// fft_lds_general_kernel.  deferred[g] is written for every group g (1 =
+// left over), so the flags need no clearing between calls.
+template <int LOGN>
+__global__ __launch_bounds__(256) void fft_lds_kernel(const int64_t *__restrict__ sre, const int64_t *__restrict__ sim,
+                                                      int64_t *__restrict__ dre, int64_t *__restrict__ dim,
+                                                      const int64_t *__restrict__ tw, int64_t batch,
+                                                      uint32_t *__restrict__ deferred) {
+    constexpr int N = 1 << LOGN, L = N / 16, FPB = 256 / L, NP = (LOGN + 3) / 4;
+    constexpr int STRIDE = N + N / 16;
+    constexpr int S1 = 4 < LOGN - 4 ? 4 : LOGN - 4, S2 = 8 < LOGN - 4 ? 8 : LOGN - 4;
+    static_assert(LOGN >= 5 && LOGN <= 11, "LDS FFT size");
+    __shared__ uint64_t sm[FPB * STRIDE];
+    const int f = threadIdx.x / L;
+    const uint32_t t = threadIdx.x % L;
+    // every twiddle component within [-2^16, 2^16] (the standard table is)
+    bool small = true;
+    for (int i = threadIdx.x; i < N; i += 256) {
+        const int64_t w = tw[i];
+        small = small && w >= -TW_SMALL && w <= TW_SMALL;
+    }
+    const bool tw_small = __syncthreads_and(small);
+    WinTw w0, w1, w2;
+    if (tw_small) {
+        load_win_tw<0, 0, 4, LOGN>(w0, tw, t);
+        if constexpr (NP > 1) load_win_tw<S1, 4, (8 < LOGN ? 8 : LOGN), LOGN>(w1, tw, t);
+        if constexpr (NP > 2) load_win_tw<S2, 8, LOGN, LOGN>(w2, tw, t);
+    }
+    uint64_t *smf = sm + f * STRIDE;
+    for (int64_t f0 = (int64_t)blockIdx.x * FPB; f0 < batch; f0 += (int64_t)gridDim.x * FPB) {
+        const int64_t fi = f0 + f;
+        const bool live = fi < batch;
+        int64_t xr[16], xi[16];
+        const bool fits = load_group<LOGN>(sre, sim, fi, live, t, xr, xi);
+        const bool fast = __syncthreads_and(fits && tw_small);
+        if (threadIdx.x == 0) deferred[f0 / FPB] = fast ? 0u : 1u;
+        if (!fast) continue;
+        int32_t yr[16], yi[16];
+#pragma unroll
+        for (int r = 0; r < 16; ++r) yr[r] = (int32_t)xr[r], yi[r] = (int32_t)xi[r];
+        window32<0, 0, 4>(yr, yi, w0);
+        if constexpr (NP > 1) {
+            transpose32<0, S1>(yr, yi, t, smf);
+            window32<S1, 4, (8 < LOGN ? 8 : LOGN)>(yr, yi, w1);
+        }
+        if constexpr (NP > 2) {
+            transpose32<S1, S2>(yr, yi, t, smf);
+            window32<S2, 8, LOGN>(yr, yi, w2);
+        }
+        if (live) store_group<LOGN>(dre, dim, fi, t, yr, yi);
+    }
+}
+
+// int64 kernel for the groups flagged in `deferred` (any inputs, any table;
+// twiddles read from the table as they are needed).
+template <int LOGN>
+__global__ __launch_bounds__(256) void fft_lds_general_kernel(const int64_t *__restrict__ sre,
+                                                              const int64_t *__restrict__ sim,
+                                                              int64_t *__restrict__ dre, int64_t *__restrict__ dim,
+                                                              const int64_t *__restrict__ tw, int64_t batch,
+                                                              const uint32_t *__restrict__ deferred) {
+    constexpr int N = 1 << LOGN, L = N / 16, FPB = 256 / L;
+    constexpr int STRIDE = N + N / 16;
+    __shared__ int64_t sm[FPB * STRIDE];
+    const int f = threadIdx.x / L;
+    const uint32_t t = threadIdx.x % L;
+    const int64_t groups = (batch + FPB - 1) / FPB;
+    for (int64_t g = blockIdx.x; g < groups; g += gridDim.x) {
+        if (!deferred[g]) continue;   // block-uniform
+        const int64_t fi = g * FPB + f;
+        const bool live = fi < batch;
+        int64_t xr[16], xi[16];
+        load_group<LOGN>(sre, sim, fi, live, t, xr, xi);
+        lds_transform<LOGN>(xr, xi, tw, t, sm + f * STRIDE);
+        if (live) store_group<LOGN>(dre, dim, fi, t, xr, xi);
     }
 }
 
@@ -207,30 +395,42 @@ __global__ void copy_i64_kernel(const int64_t *__restrict__ src, int64_t *__rest
 }  // namespace fft
 
 size_t fft_workspace_bytes(int logn, int64_t batch) {
-    if (logn <= 11) return 0;
+    if (logn <= 4) return 0;
+    if (logn <= 11) {   // one deferred flag per group of transforms
+        const int64_t fpb = 256 / ((1 << logn) / 16);
+        return (size_t)((batch + fpb - 1) / fpb) * sizeof(uint32_t);
+    }
     return 2 * (size_t)batch * ((size_t)1 << logn) * sizeof(int64_t);
 }
 
-// batch transforms of n = 2^logn points, transform f at re + f n / im + f n,
-// in place.  logn in [0, 30]; ws: fft_workspace_bytes(logn, batch) bytes.
-hipError_t launch_fft_q16(int64_t *re, int64_t *im, const int64_t *tw, int logn, int64_t batch, void *ws,
-                          hipStream_t s) {
+// batch transforms of n = 2^logn points: transform f read from sre / sim
+// + f n and written to dre / dim + f n (the same pointers for in place).
+// logn in [0, 30]; ws: fft_workspace_bytes(logn, batch) bytes.
+hipError_t launch_fft_q16(const int64_t *sre, const int64_t *sim, int64_t *dre, int64_t *dim, const int64_t *tw,
+                          int logn, int64_t batch, void *ws, hipStream_t s) {
     using namespace fft;
     if (batch <= 0) return hipSuccess;
     if (logn < 0 || logn > 30) return hipErrorInvalidValue;
     const int64_t n = (int64_t)1 << logn;
     const unsigned cap = 256 * 16;   // resident-size grid for the grid-stride kernels
     switch (logn) {
-#define SMALL(LG) \
-    case LG: hipLaunchKernelGGL(fft_small_kernel<LG>, dim3((unsigned)((batch + 255) / 256)), dim3(256), 0, s, re, im, tw, batch); break;
+#define SMALL(LG)                                                                                              \
+    case LG:                                                                                                   \
+        hipLaunchKernelGGL(fft_small_kernel<LG>, dim3((unsigned)((batch + 255) / 256)), dim3(256), 0, s, sre, sim, \
+                           dre, dim, tw, batch);                                                               \
+        break;
     SMALL(0) SMALL(1) SMALL(2) SMALL(3) SMALL(4)
 #undef SMALL
-#define LDS(LG)                                                                                                 \
-    case LG: {                                                                                                  \
-        const int64_t fpb = 256 / ((1 << LG) / 16), blocks = (batch + fpb - 1) / fpb;                         \
-        hipLaunchKernelGGL(fft_lds_kernel<LG>, dim3((unsigned)(blocks < cap ? blocks : cap)), dim3(256), 0, s, re, im, tw, \
-                           batch);                                                                              \
-        break;                                                                                                  \
+#define LDS(LG)                                                                                                \
+    case LG: {                                                                                                 \
+        if (!ws) return hipErrorInvalidValue;                                                                  \
+        uint32_t *deferred = (uint32_t *)ws;                                                                   \
+        const int64_t fpb = 256 / ((1 << LG) / 16), blocks = (batch + fpb - 1) / fpb;                        \
+        const unsigned grid = (unsigned)(blocks < cap ? blocks : cap);                                         \
+        hipLaunchKernelGGL(fft_lds_kernel<LG>, dim3(grid), dim3(256), 0, s, sre, sim, dre, dim, tw, batch, deferred); \
+        hipLaunchKernelGGL(fft_lds_general_kernel<LG>, dim3(grid < 1024 ? grid : 1024), dim3(256), 0, s, sre, sim, \
+                           dre, dim, tw, batch, deferred);                                                     \
+        break;                                                                                                 \
     }
     LDS(5) LDS(6) LDS(7) LDS(8) LDS(9) LDS(10) LDS(11)
 #undef LDS
@@ -240,21 +440,23 @@ hipError_t launch_fft_q16(int64_t *re, int64_t *im, const int64_t *tw, int logn,
         const int np = (logn + 3) / 4;
         const int64_t threads = batch * (n >> 4);
         const dim3 grid((unsigned)((threads + 255) / 256));
-        // passes alternate buffers; an odd count ends in the workspace
-        int64_t *src_re = re, *src_im = im;
+        // pass 0 reads the source through the bit reversal into the
+        // workspace; later passes alternate dst and workspace; an odd pass
+        // count ends in the workspace and is copied to dst
+        const int64_t *src_re = sre, *src_im = sim;
         for (int p = 0; p < np; ++p) {
             const int sw = 4 * p < logn - 4 ? 4 * p : logn - 4;
             const int b1 = 4 * p + 4 < logn ? 4 * p + 4 : logn;
-            int64_t *dst_re = (p % 2 == 0) ? wre : re, *dst_im = (p % 2 == 0) ? wim : im;
-            hipLaunchKernelGGL(fft_pass_kernel, grid, dim3(256), 0, s, src_re, src_im, dst_re, dst_im, tw, logn, sw,
+            int64_t *to_re = (p % 2 == 0) ? wre : dre, *to_im = (p % 2 == 0) ? wim : dim;
+            hipLaunchKernelGGL(fft_pass_kernel, grid, dim3(256), 0, s, src_re, src_im, to_re, to_im, tw, logn, sw,
                                4 * p, b1, p == 0, batch);
-            src_re = dst_re, src_im = dst_im;
+            src_re = to_re, src_im = to_im;
         }
-        if (src_re != re) {
+        if (src_re == wre) {
             const int64_t cnt = batch * n;
             const unsigned gb = (unsigned)((cnt + 255) / 256 < cap ? (cnt + 255) / 256 : cap);
-            hipLaunchKernelGGL(copy_i64_kernel, dim3(gb), dim3(256), 0, s, wre, re, cnt);
-            hipLaunchKernelGGL(copy_i64_kernel, dim3(gb), dim3(256), 0, s, wim, im, cnt);
+            hipLaunchKernelGGL(copy_i64_kernel, dim3(gb), dim3(256), 0, s, wre, dre, cnt);
+            hipLaunchKernelGGL(copy_i64_kernel, dim3(gb), dim3(256), 0, s, wim, dim, cnt);
         }
         break;
     }

@@ -56,10 +56,11 @@ hipError_t launch_rows_f32(const float *W, const float *x, float *y, int64_t row
 // y[M] = int16 GEMV.
 hipError_t launch_gemv_i16(const int16_t *W, const int16_t *x, int32_t *y, int M, int K, hipStream_t s);
 
-// Q16.16 radix-2 DIT FFT (det_fft.hip): batch transforms of 2^logn points,
-// in place; ws holds fft_workspace_bytes(logn, batch) bytes (0 for logn <= 11).
+// Q16.16 radix-2 DIT FFT (det_fft.hip): batch transforms of 2^logn points
+// from (sre, sim) to (dre, dim) (the same pointers for in place); ws holds
+// fft_workspace_bytes(logn, batch) bytes (0 for logn <= 11).
 size_t fft_workspace_bytes(int logn, int64_t batch);
-hipError_t launch_fft_q16(int64_t *re, int64_t *im, const int64_t *tw, int logn, int64_t batch, void *ws,
-                          hipStream_t s);
+hipError_t launch_fft_q16(const int64_t *sre, const int64_t *sim, int64_t *dre, int64_t *dim, const int64_t *tw,
+                          int logn, int64_t batch, void *ws, hipStream_t s);
 
 }  // namespace det

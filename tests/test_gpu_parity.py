@@ -396,8 +396,53 @@ def test_fft_dev_entry_point_and_workspace_path():
             gi = dim_.to_array(np.int64, (batch, n))
             assert np.array_equal(gr[sel], want[0]) and np.array_equal(gi[sel], want[1])
             want = _fft_oracle_batch(want[0], want[1], tw, logn)
-        assert M.lib().det_fft_workspace_bytes(logn, batch) == (0 if logn <= 11 else 16 * batch * n)
+        fpb = 256 // (n // 16) if logn <= 11 else 1
+        want_ws = 4 * -(-batch // fpb) if logn <= 11 else 16 * batch * n
+        assert M.lib().det_fft_workspace_bytes(logn, batch) == want_ws
         dre.free(); dim_.free(); dtw.free()
+
+
+def test_fft_out_of_place_and_path_choice():
+    # det_fft_q16_oop_dev leaves the input alone; a block of transforms takes
+    # the int32 path only when every input is within the growth bound, and a
+    # batch that mixes small and large transforms, or sits exactly on the
+    # bound, gives the oracle's integers either way
+    s = M.Stream()
+    logn, n, batch = 8, 256, 1000
+    bound = (2 ** 31 - 1) // (2 * 3 ** 7)
+    rng = np.random.default_rng(88)
+    x = rng.integers(-bound, bound + 1, (2, batch, n))
+    x[:, ::7] *= 1 << 20          # every 7th transform far outside the bound
+    x[0, 3, 5], x[1, 4, 9] = bound, -bound
+    x[0, 6, 1] = bound + 1        # just outside
+    tw = O.fft_twiddles(n)
+    re, im = np.ascontiguousarray(x[0]), np.ascontiguousarray(x[1])
+    want = _fft_oracle_batch(re, im, tw, logn)
+    sre, sim = M.DeviceBuffer.from_array(re), M.DeviceBuffer.from_array(im)
+    dre, dim_, dtw = M.DeviceBuffer(re.nbytes), M.DeviceBuffer(im.nbytes), M.DeviceBuffer.from_array(tw)
+    for rep in range(2):
+        dre.fill(0x11)
+        note(f"det_fft_q16_oop_dev n={n} batch={batch} rep={rep}")
+        M.check(M.lib().det_fft_q16_oop_dev(sre.ptr, sim.ptr, dre.ptr, dim_.ptr, dtw.ptr, logn, n, batch, s.ptr))
+        s.sync()
+        assert np.array_equal(dre.to_array(np.int64, (batch, n)), want[0])
+        assert np.array_equal(dim_.to_array(np.int64, (batch, n)), want[1])
+        assert np.array_equal(sre.to_array(np.int64, (batch, n)), re)
+    # a twiddle table with a component above 2^16 keeps every block on int64
+    tw2 = tw.copy(); tw2[201] = 70000
+    dtw2 = M.DeviceBuffer.from_array(tw2)
+    small = np.ascontiguousarray(x[:, 1:64:7]) // (1 << 20)
+    want2 = _fft_oracle_batch(small[0], small[1], tw2, logn)
+    s0, s1 = M.DeviceBuffer.from_array(small[0]), M.DeviceBuffer.from_array(small[1])
+    note("det_fft_q16_dev with a large twiddle component")
+    M.check(M.lib().det_fft_q16_dev(s0.ptr, s1.ptr, dtw2.ptr, logn, n, small.shape[1], s.ptr))
+    s.sync()
+    assert np.array_equal(s0.to_array(np.int64, small[0].shape), want2[0])
+    assert np.array_equal(s1.to_array(np.int64, small[1].shape), want2[1])
+    assert M.lib().det_fft_q16_oop_dev(sre.ptr, sim.ptr, sre.ptr + 8, dim_.ptr, dtw.ptr, logn, n, batch,
+                                       s.ptr) == M.DET_ERR_ARG
+    for b in (sre, sim, dre, dim_, dtw, dtw2, s0, s1):
+        b.free()
 
 
 def test_fft_argument_conventions():
