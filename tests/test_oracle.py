@@ -536,3 +536,45 @@ def test_fft_peeled_stage_differs_from_the_c_file_when_tw0_is_not_one():
 def test_fft_rejects_non_power_of_two():
     with pytest.raises(ValueError):
         O.fft_q16(np.zeros(6, np.int64), np.zeros(6, np.int64), np.zeros(6, np.int64), 2)
+
+
+def test_fft_int32_growth_bound():
+    # The GPU's int32 path relies on: with |w| <= 2^16, |qmul(w, x)| <= |x|;
+    # the span-2 stage at most doubles the largest magnitude and each later
+    # stage at most triples it, so inputs within (2^31 - 1) // (2 * 3^(logn-1))
+    # keep every intermediate in int32.  Checked on edge values and on
+    # instrumented transforms of worst-sign inputs at exactly the bound.
+    edges = [0, 1, -1, 2, -2, 65535, -65535, 65536, -65536, 3, -3, 12345, -12345]
+    for w in edges:
+        for x in [0, 1, -1, 7, -7, (1 << 31) - 1, -(1 << 31), 123456789, -123456789]:
+            assert abs((w * x) >> 16) <= abs(x), (w, x)
+    for logn in (1, 2, 5, 8, 11):
+        n = 1 << logn
+        bound = (2 ** 31 - 1) // (2 * 3 ** (logn - 1))
+        tw = [int(v) for v in O.fft_twiddles(n)] if n >= 2 else [65536, 0]
+        rng = np.random.default_rng(logn)
+        for trial in range(3):
+            re = [bound * int(s) for s in rng.choice([-1, 1], n)]
+            im = [bound * int(s) for s in rng.choice([-1, 1], n)]
+            perm = [int(format(i, f"0{logn}b")[::-1], 2) for i in range(n)]
+            re, im = [re[p] for p in perm], [im[p] for p in perm]
+            peak, span, stage = bound, 2, 0
+            while span <= n:
+                h = span // 2
+                for base in range(0, n, span):
+                    for j in range(h):
+                        a, b = base + j, base + j + h
+                        if span == 2:
+                            tr, ti = re[b], im[b]
+                        else:
+                            k = j * (n // span)
+                            wr, wi = tw[2 * k], tw[2 * k + 1]
+                            tr = ((wr * re[b]) >> 16) - ((wi * im[b]) >> 16)
+                            ti = ((wr * im[b]) >> 16) + ((wi * re[b]) >> 16)
+                        re[a], im[a], re[b], im[b] = re[a] + tr, im[a] + ti, re[a] - tr, im[a] - ti
+                stage += 1
+                m = max(max(abs(v) for v in re), max(abs(v) for v in im))
+                assert m <= peak * (2 if stage == 1 else 3), (logn, stage)
+                peak = m
+                assert m <= 2 ** 31 - 1, (logn, stage, m)
+                span *= 2
