@@ -230,6 +230,57 @@ def cpu_fft_reference(logn: int, seconds: float = 2.0):
                     "(the per-call ctypes overhead is included)"}
 
 
+def host_abi_timings(reps: int = 3) -> dict:
+    """End-to-end time of the reference-ABI host-pointer entry points (H2D,
+    kernel, D2H on the library stream, synchronous), pageable numpy buffers:
+    the PCIe-inclusive rate a drop-in caller sees.  Never the bench value."""
+    L = M.lib()
+    res = {}
+
+    def timed(fn):
+        fn()
+        ts = []
+        for _ in range(reps):
+            t0 = time.perf_counter()
+            rc = fn()
+            ts.append(time.perf_counter() - t0)
+            M.check(rc)
+        return sorted(ts)[len(ts) // 2] * 1e3
+
+    m = k = n = 4096
+    a, b = M.gen_i8(SEED ^ 0x4096, m * k, k * n)
+    c = np.empty(m * n, np.int32)
+    ms = timed(lambda: L.gemmi8(a.ctypes.data, b.ctypes.data, c.ctypes.data, m, k, n))
+    res["gemmi8_4096"] = {"ms": round(ms, 3), "tops": round(2.0 * m * n * k / ms / 1e9, 1),
+                          "pcie_bytes": a.nbytes + b.nbytes + c.nbytes}
+    del a, b, c
+    M_, K_ = 16384, 16384
+    W, x = M.gen_q16(SEED ^ 0x6E3F, M_ * K_, K_, 15)
+    y = np.empty(M_, np.int32)
+    ms = timed(lambda: L.gemvq(W.ctypes.data, x.ctypes.data, y.ctypes.data, M_, K_))
+    res["gemvq_16384"] = {"ms": round(ms, 3), "gbs": round(4.0 * M_ * K_ / ms / 1e6, 1), "pcie_bytes": W.nbytes}
+    del W, x, y
+    Wf, xf = M.gen_f32_unit(SEED ^ 0xF32, M_ * K_, K_)
+    yf = np.empty(M_, np.float32)
+    ms = timed(lambda: L.mmf32(Wf.ctypes.data, xf.ctypes.data, yf.ctypes.data, M_, K_))
+    res["mmf32_16384"] = {"ms": round(ms, 3), "gbs": round(4.0 * M_ * K_ / ms / 1e6, 1), "pcie_bytes": Wf.nbytes}
+    del Wf, xf, yf
+    tw = M.fft_twiddles(256)
+    re = np.random.default_rng(1).integers(-65536, 65536, 256).astype(np.int64)
+    im = re[::-1].copy()
+    ms = timed(lambda: L.fft256(re.ctypes.data, im.ctypes.data, tw.ctypes.data, 8, 256))
+    res["fft256_one"] = {"us": round(ms * 1e3, 1), "note": "one 256-point transform per call (4 KiB each way)"}
+    batch = 1 << 18
+    R = np.random.default_rng(2).integers(-65536, 65536, (batch, 256)).astype(np.int64)
+    I = R[::-1].copy()
+    ms = timed(lambda: L.det_fft_q16(R.ctypes.data, I.ctypes.data, tw.ctypes.data, 8, 256, batch))
+    res["det_fft_q16_2e18"] = {"ms": round(ms, 3), "ns_per_fft": round(ms * 1e6 / batch, 2),
+                               "pcie_bytes": 2 * (R.nbytes + I.nbytes)}
+    res["note"] = ("median of %d synchronous calls after one warm-up; pageable host buffers; times include the "
+                   "host-to-device and device-to-host copies" % reps)
+    return res
+
+
 def vendor_int8_child(steps: int) -> None:
     """Child-process body of --vendor-ref: time the vendor int8 GEMM
     (torch._int_mm, which dispatches to hipBLASLt on ROCm) on the headline
@@ -358,6 +409,8 @@ def main() -> int:
     ap.add_argument("--vendor-ref", action="store_true",
                     help="also time the vendor int8 GEMM (torch._int_mm) on the headline shape, for context")
     ap.add_argument("--vendor-child", action="store_true", help=argparse.SUPPRESS)
+    ap.add_argument("--host-abi", action="store_true",
+                    help="also time the reference-ABI host-pointer calls end to end (PCIe included)")
     args = ap.parse_args()
     if args.vendor_child:
         vendor_int8_child(args.steps)
@@ -509,6 +562,10 @@ def main() -> int:
         log(f"i8_8192: {r['ms'] * 1e3:.1f} us  {t:.1f} TOP/s")
     result["secondary"] = sec
     stream.destroy()
+    if args.host_abi:
+        log("host_abi: reference-ABI host-pointer calls, PCIe copies included")
+        result["host_abi"] = host_abi_timings()
+        log(f"host_abi: {result['host_abi']}")
     if vendor is not None:
         result["vendor_int8_gemm"] = vendor
 
