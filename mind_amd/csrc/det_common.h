@@ -117,6 +117,13 @@ __device__ __forceinline__ void dma16(v4i32 rsrc, uint32_t lds, int voff) {
     asm volatile("s_mov_b32 m0, %0\n\tbuffer_load_dwordx4 %1, %2, 0 offen lds" ::"s"(lds), "v"(voff), "s"(rsrc)
                  : "memory", "m0");
 }
+// The same with a uniform byte offset added from an SGPR (soffset), so a
+// loop can advance every lane's address without a vector add.
+__device__ __forceinline__ void dma16s(v4i32 rsrc, uint32_t lds, int voff, uint32_t soff) {
+    asm volatile("s_mov_b32 m0, %0\n\tbuffer_load_dwordx4 %1, %2, %3 offen lds" ::"s"(lds), "v"(voff), "s"(rsrc),
+                 "s"(soff)
+                 : "memory", "m0");
+}
 __device__ __forceinline__ uint32_t lds_addr(const void *p) {
     return __builtin_amdgcn_readfirstlane((uint32_t)(uintptr_t)(lds_i8_ptr)(const int8_t *)(p));
 }

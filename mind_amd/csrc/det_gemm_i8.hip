@@ -26,6 +26,8 @@
 //    reads form the 16-byte B operand.
 // Loads run two K steps ahead of the MFMAs (two register sets, two LDS
 // buffers, one barrier per step).
+#include <type_traits>
+
 #include "det_common.h"
 #include "det_kernels.h"
 
@@ -271,7 +273,12 @@ struct I16Epi {
     uint32_t bias_c, kc2;              // c = 0x80, K c^2 mod 2^32
 };
 
-template <int EPI>
+// FULL: M % BM == 0, N % BN == 0 and K % (BK * NSTAGE) == 0 -- no bounds
+// checks, and the K loop unrolled by NSTAGE so every LDS stage address is a
+// compile-time offset and the DMA advances through its SGPR soffset: the
+// loop issues almost no VALU besides the MFMAs (VALU and MFMA work of one
+// SIMD do not overlap on gfx950).
+template <int EPI, bool FULL>
 __global__ __launch_bounds__(THREADS, 1) void gemm_i8_dma_kernel(const int8_t *__restrict__ A,
                                                                  const int8_t *__restrict__ B,
                                                                  int32_t *__restrict__ C, int M, int N, int K,
@@ -357,6 +364,55 @@ __global__ __launch_bounds__(THREADS, 1) void gemm_i8_dma_kernel(const int8_t *_
     };
 
     const int nk = (K + BK - 1) / BK;
+    if constexpr (FULL) {
+        // lane offsets without k; steps past the end point beyond the buffer
+        // (soffset = its size), which the DMA turns into zero fills
+        const uint32_t lim_a = (uint32_t)M * (uint32_t)K, lim_b = (uint32_t)K * (uint32_t)N;
+        auto issue_f = [&](auto st_c, int k0) {
+            constexpr int st = decltype(st_c)::value;
+            const bool in = k0 < K;
+            const uint32_t sa = in ? (uint32_t)k0 : lim_a;
+            const uint32_t sb = in ? (uint32_t)k0 * (uint32_t)N : lim_b;
+#pragma unroll
+            for (int j = 0; j < 2; ++j) {
+                const int blk = 2 * wave + j;
+                dma16s(ra, lds_addr(smem[st][0] + blk * 1024), (int)a_off[j], sa);
+                dma16s(rb, lds_addr(smem[st][1] + blk * 1024), (int)b_off[j], sb);
+            }
+        };
+        using S0 = std::integral_constant<int, 0>;
+        using S1 = std::integral_constant<int, 1>;
+        using S2 = std::integral_constant<int, 2>;
+        using S3 = std::integral_constant<int, 3>;
+        static_assert(NSTAGE == 4, "the unrolled loop below assumes 4 stages");
+        issue_f(S0{}, 0);
+        issue_f(S1{}, BK);
+        issue_f(S2{}, 2 * BK);
+        DET_WAIT_VMCNT(DMA_PER_STAGE * (NSTAGE - 2));   // step 0 landed
+        __builtin_amdgcn_s_barrier();
+        Ops p0, p1;
+        read_ops(p0, 0, 0);
+        auto step = [&](auto cur_c, int kt) {
+            constexpr int cur = decltype(cur_c)::value, nxt = (cur + 1) % NSTAGE;
+            read_ops(p1, cur, 1);
+            mma(p0);
+            DET_WAIT_VMCNT(DMA_PER_STAGE * (NSTAGE - 3));
+            __builtin_amdgcn_s_waitcnt(0xc07f & ~(15 << 8));   // lgkmcnt(0)
+            __builtin_amdgcn_s_barrier();
+            issue_f(std::integral_constant<int, (cur + NSTAGE - 1) % NSTAGE>{}, (kt + NSTAGE - 1) * BK);
+            __builtin_amdgcn_sched_barrier(0);
+            read_ops(p0, nxt, 0);
+            mma(p1);
+            __builtin_amdgcn_sched_barrier(0);
+        };
+        for (int kt = 0; kt < nk; kt += NSTAGE) {
+            step(S0{}, kt);
+            step(S1{}, kt + 1);
+            step(S2{}, kt + 2);
+            step(S3{}, kt + 3);
+        }
+        DET_WAIT_VMCNT(0);
+    } else {
 #pragma unroll
     for (int st = 0; st < NSTAGE - 1; ++st) issue(st, st * BK);
     DET_WAIT_VMCNT(DMA_PER_STAGE * (NSTAGE - 2));   // step 0 landed
@@ -381,6 +437,7 @@ __global__ __launch_bounds__(THREADS, 1) void gemm_i8_dma_kernel(const int8_t *_
     // the loads issued past the end of K are zero fills; none may still be
     // writing LDS when the workgroup ends
     DET_WAIT_VMCNT(0);
+    }
 
     if (EPI == EPI_I8) {
         // lane holds C[8*(r >> 2) + 4*lh + (r & 3)][l32] of each 32x32 block;
@@ -466,8 +523,12 @@ hipError_t launch_gemm_i8(const int8_t *A, const int8_t *B, int32_t *C, int M, i
     const dim3 grid(tiles_m * tiles_n), block(THREADS);
     const bool fast = (K % 16 == 0) && (N % 16 == 0) && (((uintptr_t)A & 15) == 0) && (((uintptr_t)B & 15) == 0) &&
                       (size_t)M * K < 0x80000000ull && (size_t)K * N < 0x80000000ull;
-    if (fast)
-        hipLaunchKernelGGL(gemm_i8_dma_kernel<EPI_I8>, grid, block, 0, s, A, B, C, M, N, K, tiles_m, tiles_n,
+    const bool full = fast && M % BM == 0 && N % BN == 0 && K % (BK * NSTAGE) == 0;
+    if (full)
+        hipLaunchKernelGGL((gemm_i8_dma_kernel<EPI_I8, true>), grid, block, 0, s, A, B, C, M, N, K, tiles_m, tiles_n,
+                           I16Epi{});
+    else if (fast)
+        hipLaunchKernelGGL((gemm_i8_dma_kernel<EPI_I8, false>), grid, block, 0, s, A, B, C, M, N, K, tiles_m, tiles_n,
                            I16Epi{});
     else
         hipLaunchKernelGGL(gemm_i8_kernel<false>, grid, block, 0, s, A, B, C, M, N, K, tiles_m, tiles_n);
@@ -482,8 +543,13 @@ hipError_t launch_gemm_i8_i16epi(const int8_t *A2, const int8_t *B2, int M2, int
     using namespace i8g;
     const int tiles_m = (M2 + BM - 1) / BM, tiles_n = (N2 + BN - 1) / BN;
     I16Epi e{rowsum, colsum, C, M16, N16, 0x80u, (uint32_t)((uint64_t)(uint32_t)K16 * 0x4000u)};
-    hipLaunchKernelGGL(gemm_i8_dma_kernel<EPI_I16>, dim3(tiles_m * tiles_n), dim3(THREADS), 0, s, A2, B2,
-                       (int32_t *)nullptr, M2, N2, Kp, tiles_m, tiles_n, e);
+    const bool full = M2 % BM == 0 && N2 % BN == 0 && Kp % (BK * NSTAGE) == 0;
+    if (full)
+        hipLaunchKernelGGL((gemm_i8_dma_kernel<EPI_I16, true>), dim3(tiles_m * tiles_n), dim3(THREADS), 0, s, A2, B2,
+                           (int32_t *)nullptr, M2, N2, Kp, tiles_m, tiles_n, e);
+    else
+        hipLaunchKernelGGL((gemm_i8_dma_kernel<EPI_I16, false>), dim3(tiles_m * tiles_n), dim3(THREADS), 0, s, A2, B2,
+                           (int32_t *)nullptr, M2, N2, Kp, tiles_m, tiles_n, e);
     return hipGetLastError();
 }
 
