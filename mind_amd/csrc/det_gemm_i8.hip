@@ -368,6 +368,8 @@ __global__ __launch_bounds__(THREADS, 1) void gemm_i8_dma_kernel(const int8_t *_
         // lane offsets without k; steps past the end point beyond the buffer
         // (soffset = its size), which the DMA turns into zero fills
         const uint32_t lim_a = (uint32_t)M * (uint32_t)K, lim_b = (uint32_t)K * (uint32_t)N;
+        // LDS destinations by scalar arithmetic from one base
+        const uint32_t lds_w = lds_addr(smem) + (uint32_t)(2 * wave) * 1024u;
         auto issue_f = [&](auto st_c, int k0) {
             constexpr int st = decltype(st_c)::value;
             const bool in = k0 < K;
@@ -375,9 +377,8 @@ __global__ __launch_bounds__(THREADS, 1) void gemm_i8_dma_kernel(const int8_t *_
             const uint32_t sb = in ? (uint32_t)k0 * (uint32_t)N : lim_b;
 #pragma unroll
             for (int j = 0; j < 2; ++j) {
-                const int blk = 2 * wave + j;
-                dma16s(ra, lds_addr(smem[st][0] + blk * 1024), (int)a_off[j], sa);
-                dma16s(rb, lds_addr(smem[st][1] + blk * 1024), (int)b_off[j], sb);
+                dma16s(ra, lds_w + (uint32_t)((2 * st + 0) * TILE_BYTES + j * 1024), (int)a_off[j], sa);
+                dma16s(rb, lds_w + (uint32_t)((2 * st + 1) * TILE_BYTES + j * 1024), (int)b_off[j], sb);
             }
         };
         using S0 = std::integral_constant<int, 0>;
