@@ -457,6 +457,101 @@ def test_fft_argument_conventions():
     assert L.fft256(addr(one_r), addr(one_i), 0, 0, 1) == 0 and one_r[0] == 12345 and one_i[0] == -7
 
 
+# ------------------------------------------------------------------ concurrency
+
+def test_host_abi_concurrent_callers():
+    # The host-pointer entry points are called from several threads at once
+    # (ctypes releases the GIL): one device mutex serialises them, the
+    # library stream and staging are shared, and every result must still be
+    # the oracle's.  Q16 GEMM and the FFT also use the workspace arena.
+    import threading
+    L = M.lib()
+    a8, b8 = O.gen_i8(0x7A1, 256 * 320, 320 * 192)
+    c8 = O.gemm_i8(a8, b8, 256, 320, 192).ravel()
+    aq, bq = O.gen_q16(0x7A2, 128 * 96, 96 * 256)
+    cq = O.gemm_q16(aq, bq, 128, 96, 256).ravel()
+    W, x = O.gen_q16(0x7A3, 1000 * 513, 513)
+    y = O.gemv_q16(W, x, 1000, 513)
+    fr, fi = O.fft_input_lcg(0x7A4, 256)
+    tw = O.fft_twiddles(256)
+    fw = O.fft_q16(fr, fi, tw, 8)
+    da, db = O.gen_q16(0x7A5, 100003, 100003)
+    dq = O.dot_q16(da, db)
+    Wf, xf = O.gen_f32_unit(0x7A6, 300 * 777, 777)
+    yf = O.matmul_rmajor_f32(Wf, xf, 300, 777)
+
+    def job_i8():
+        c = np.empty(256 * 192, np.int32)
+        assert L.gemmi8(addr(a8), addr(b8), addr(c), 256, 320, 192) == 0
+        return np.array_equal(c, c8)
+
+    def job_q16():
+        c = np.empty(128 * 256, np.int32)
+        assert L.gemmqmm(addr(aq), addr(bq), addr(c), 128, 96, 256) == 0
+        return np.array_equal(c, cq)
+
+    def job_gemv():
+        yy = np.empty(1000, np.int32)
+        assert L.gemvq(addr(W), addr(x), addr(yy), 1000, 513) == 0
+        return np.array_equal(yy, y)
+
+    def job_fft():
+        r, i = fr.copy(), fi.copy()
+        assert L.fft256(addr(r), addr(i), addr(tw), 8, 256) == 0
+        return np.array_equal(r, fw[0]) and np.array_equal(i, fw[1])
+
+    def job_dot():
+        return L.dotq(addr(da), addr(db), len(da)) == dq
+
+    def job_f32():
+        yy = np.empty(300, np.float32)
+        assert L.mmf32(addr(Wf), addr(xf), addr(yy), 300, 777) == 0
+        return np.array_equal(yy.view(np.uint32), yf.view(np.uint32))
+
+    jobs = [job_i8, job_q16, job_gemv, job_fft, job_dot, job_f32]
+    results, errors = [], []
+
+    def run(job):
+        try:
+            for _ in range(5):
+                results.append((job.__name__, job()))
+        except Exception as e:   # reported below, not lost in the thread
+            errors.append((job.__name__, repr(e)))
+
+    note("host ABI: 6 threads x 5 calls")
+    threads = [threading.Thread(target=run, args=(j,)) for j in jobs]
+    for t in threads:
+        t.start()
+    for t in threads:
+        t.join(timeout=120)
+    assert not errors, errors
+    assert len(results) == 30 and all(ok for _, ok in results), [r for r in results if not r[1]]
+
+
+def test_device_arena_shared_by_two_streams():
+    # det_matmul_q16_dev on two streams: both use the library's workspace
+    # arena, ordered by its event, so interleaved calls of different shapes
+    # must each give the oracle's C
+    L = M.lib()
+    shapes = [(192, 160, 224), (320, 96, 128)]
+    data = []
+    for si, (m, k, n) in enumerate(shapes):
+        a, b = O.gen_q16(0x7B0 + si, m * k, k * n, shift=0)
+        data.append((m, k, n, M.DeviceBuffer.from_array(a), M.DeviceBuffer.from_array(b), M.DeviceBuffer(m * n * 4),
+                     O.gemm_q16(a, b, m, k, n).ravel()))
+    streams = [M.Stream(), M.Stream()]
+    for rep in range(4):
+        for si, (m, k, n, dA, dB, dC, _) in enumerate(data):
+            dC.fill(0x33)
+            note(f"det_matmul_q16_dev stream {si} rep {rep}")
+            M.check(L.det_matmul_q16_dev(dA.ptr, dB.ptr, dC.ptr, m, k, n, streams[si].ptr))
+        for si, (m, k, n, dA, dB, dC, want) in enumerate(data):
+            streams[si].sync()
+            assert np.array_equal(dC.to_array(np.int32, (m * n,)), want), (si, rep)
+    for _, _, _, dA, dB, dC, _ in data:
+        dA.free(); dB.free(); dC.free()
+
+
 # ------------------------------------------------------------------ int8 shapes
 
 I8_SHAPES = [(1, 1, 1), (1, 64, 1), (3, 5, 7), (16, 16, 16), (17, 33, 65), (64, 64, 64), (255, 257, 129),
