@@ -261,8 +261,8 @@ __device__ __forceinline__ bool load_group(const int64_t *__restrict__ sre, cons
 #pragma unroll
     for (int r = 0; r < 16; ++r) {
         const uint32_t src = (bitrev((uint32_t)r, 4) << (LOGN - 4)) | tb;
-        xr[r] = live ? sre[off + src] : 0;
-        xi[r] = live ? sim[off + src] : 0;
+        xr[r] = live ? __builtin_nontemporal_load(sre + off + src) : 0;   // each point is read once
+        xi[r] = live ? __builtin_nontemporal_load(sim + off + src) : 0;
         fits = fits && xr[r] >= -BOUND && xr[r] <= BOUND && xi[r] >= -BOUND && xi[r] <= BOUND;
     }
     return fits;
@@ -276,7 +276,8 @@ __device__ __forceinline__ void store_group(int64_t *__restrict__ dre, int64_t *
 #pragma unroll
     for (int r = 0; r < 16; ++r) {
         const uint32_t pos = win_pos(t, r, S_LAST);
-        dre[fi * N + pos] = (int64_t)xr[r], dim[fi * N + pos] = (int64_t)xi[r];
+        __builtin_nontemporal_store((int64_t)xr[r], dre + fi * N + pos);   // streamed: read by no one here
+        __builtin_nontemporal_store((int64_t)xi[r], dim + fi * N + pos);
     }
 }
 
