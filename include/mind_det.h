@@ -158,7 +158,8 @@ int64_t det_dot_i16(const int16_t *a, const int16_t *b, int64_t len);
 int64_t det_dot_f32(const float *a, const float *b, int64_t len, float *out);
 int64_t det_matmul_rmajor_f32(const float *w, const float *x, float *y, int64_t rows, int64_t cols);
 /* batch independent fft256 transforms, transform f at re + f * n and
- * im + f * n (the reference transforms one per call). */
+ * im + f * n (the reference transforms one per call); batch * n <= 2^31
+ * points, else DET_ERR_ARG. */
 int64_t det_fft_q16(int64_t *re, int64_t *im, const int64_t *tw, int64_t logn, int64_t n, int64_t batch);
 
 /* Device-pointer, asynchronous on `stream` (a hipStream_t; NULL = default

@@ -307,13 +307,14 @@ int64_t dot_f32_host(int64_t a, int64_t b, int64_t len) {
 // Argument check shared by the FFT entry points: 1 = nothing to transform
 // (n == 0 or batch == 0: the reference's loops run zero times), 0 = run,
 // negative = error.  n must be 2^logn with logn in [0, 30] (the reference
-// kernel indexes out of its buffers otherwise), and the batch must fit.
+// kernel indexes out of its buffers otherwise), and batch * n <= 2^31.
 int64_t fft_check(int64_t logn, int64_t n, int64_t batch) {
     if (batch < 0 || n < 0) return set_err(DET_ERR_ARG, "fft: negative size");
     if (n == 0 || batch == 0) return 1;
     if (logn < 0 || logn > 30 || n != ((int64_t)1 << logn))
         return set_err(DET_ERR_ARG, "fft: n must equal 2^logn with logn in [0, 30]");
-    if (batch > ((int64_t)1 << 40) / n) return set_err(DET_ERR_ARG, "fft: batch * n exceeds 2^40 points");
+    // 2^31 points = 32 GiB of re + im; keeps every FFT grid far below 2^32 work-items
+    if (batch > ((int64_t)1 << 31) / n) return set_err(DET_ERR_ARG, "fft: batch * n exceeds 2^31 points");
     return 0;
 }
 

@@ -453,6 +453,7 @@ def test_fft_argument_conventions():
     assert L.fft256(addr(z), addr(z), addr(z), 4, 0) == 0                     # nothing to do
     assert L.fft256(0, addr(z), addr(z), 4, 16) == M.DET_ERR_ARG
     assert L.det_fft_q16(addr(z), addr(z), addr(z), 4, 16, 0) == 0
+    assert L.det_fft_q16(addr(z), addr(z), addr(z), 4, 16, (1 << 27) + 1) == M.DET_ERR_ARG   # > 2^31 points
     one_r, one_i = np.array([12345], np.int64), np.array([-7], np.int64)
     assert L.fft256(addr(one_r), addr(one_i), 0, 0, 1) == 0 and one_r[0] == 12345 and one_i[0] == -7
 
