@@ -270,7 +270,7 @@ struct I16Epi {
     const uint32_t *rowsum, *colsum;   // exact sums mod 2^32 of A rows / B columns
     int32_t *C;                        // [M16][N16] int32
     int M16, N16;
-    uint32_t bias_c, kc2;              // c = 0x80, K c^2 mod 2^32
+    uint32_t bias_c, kc2;              // c = 0x80 (the epilogue relies on it), K c^2 mod 2^32
 };
 
 // FULL: M % BM == 0, N % BN == 0 and K % (BK * NSTAGE) == 0 -- no bounds
@@ -461,59 +461,56 @@ __global__ __launch_bounds__(THREADS, 1) void gemm_i8_dma_kernel(const int8_t *_
         // Elements 2p, 2p+1 of a lane are rows 2i', 2i'+1 (low / high A limb)
         // of one column; lanes l, l^1 hold columns 2j', 2j'+1 (low / high B
         // limb).  The even lane forms c00 + 2^8 c10, the odd lane
-        // 2^8 c01 + 2^16 c11; one exchange completes pairs 0..3 on the even
-        // lane and pairs 4..7 on the odd lane.  The 128x128 int16-output tile
-        // is staged in LDS (the stages are free) and written back with the
-        // bias terms as coalesced 16-byte rows.
-        constexpr int OS = 132;   // u32 row stride of the staged tile
-        uint32_t *sO = (uint32_t *)&smem[0][0][0];
-        __syncthreads();          // every wave is done with the stages
-        const bool odd = l32 & 1;
+        // 2^8 c01 + 2^16 c11; one lane exchange (a DPP quad permute)
+        // completes pairs 0..3 on the even lane and pairs 4..7 on the odd
+        // lane, which then add the bias terms and store straight from
+        // registers: no LDS staging, no barrier, no divergent branch when the
+        // wave's 64 x 32 output block is inside C.
+        const uint32_t odd = l32 & 1, oddm = 0u - odd;   // oddm: all ones on odd lanes
+        const int m16_0 = (m0 + wm) >> 1, n16_0 = (n0 + wn) >> 1;
+        // this lane's stored rows: pair p = 4 odd + kk is int16 row
+        // m16_0 + 16 i + 4 (p >> 1) + 2 lh + (p & 1) = row_l + 16 i + 4 (kk >> 1) + (kk & 1)
+        const int row_l = m16_0 + 8 * (int)odd + 2 * lh;
+        const int col_l = n16_0 + (l32 >> 1);
+        uint32_t rs[4][4], cs[2];
+        // bias terms c (rowsum + colsum) - K c^2 with c = 0x80 (the limb
+        // scheme's constant): rs holds (rowsum << 7) - K c^2, cs colsum << 7
+#pragma unroll
+        for (int j = 0; j < 2; ++j) cs[j] = e16.colsum[min(col_l + 16 * j, e16.N16 - 1)] << 7;
 #pragma unroll
         for (int i = 0; i < 4; ++i)
 #pragma unroll
-            for (int j = 0; j < 2; ++j) {
-                uint32_t part[8];
+            for (int kk = 0; kk < 4; ++kk)
+                rs[i][kk] = (e16.rowsum[min(row_l + 16 * i + 4 * (kk >> 1) + (kk & 1), e16.M16 - 1)] << 7) - e16.kc2;
+        auto epilogue = [&](auto checked_c) {
+            constexpr bool checked = decltype(checked_c)::value;
 #pragma unroll
-                for (int p = 0; p < 8; ++p) {
-                    const uint32_t lo = (uint32_t)acc[i][j][2 * p], hi = (uint32_t)acc[i][j][2 * p + 1];
-                    part[p] = odd ? (lo << 8) + (hi << 16) : lo + (hi << 8);
+            for (int i = 0; i < 4; ++i)
+#pragma unroll
+                for (int j = 0; j < 2; ++j) {
+                    uint32_t part[8];
+#pragma unroll
+                    for (int pp = 0; pp < 8; ++pp) {
+                        const uint32_t lo = (uint32_t)acc[i][j][2 * pp], hi = (uint32_t)acc[i][j][2 * pp + 1];
+                        part[pp] = (lo + (hi << 8)) << (8 * odd);   // odd lane: 2^8 c01 + 2^16 c11
+                    }
+                    const int col = col_l + 16 * j;
+#pragma unroll
+                    for (int kk = 0; kk < 4; ++kk) {
+                        const uint32_t send = (part[kk] & oddm) | (part[4 + kk] & ~oddm);
+                        const uint32_t keep = (part[4 + kk] & oddm) | (part[kk] & ~oddm);
+                        // lanes 2c <-> 2c+1: quad_perm [1, 0, 3, 2]
+                        const uint32_t recv = (uint32_t)__builtin_amdgcn_mov_dpp((int)send, 0xB1, 0xF, 0xF, false);
+                        const int row = row_l + 16 * i + 4 * (kk >> 1) + (kk & 1);
+                        const uint32_t o = keep + recv + rs[i][kk] + cs[j];
+                        int32_t *dst = e16.C + (size_t)row * e16.N16 + col;
+                        if (!checked || (row < e16.M16 && col < e16.N16)) __builtin_nontemporal_store((int32_t)o, dst);
+                    }
                 }
-                const int lc = (wn + j * 32 + l32) >> 1;
-#pragma unroll
-                for (int k = 0; k < 4; ++k) {
-                    const uint32_t recv = (uint32_t)__shfl_xor((int)(odd ? part[k] : part[4 + k]), 1);
-                    const int p = odd ? 4 + k : k;
-                    const int lr = (wm + i * 32 + 8 * (p >> 1) + 4 * lh + 2 * (p & 1)) >> 1;
-                    sO[lr * OS + lc] = (odd ? part[4 + k] : part[k]) + recv;
-                }
-            }
-        __syncthreads();
-        const int r0 = m0 >> 1, c0 = n0 >> 1;
-        const int cq = (tid & 31) * 4;             // 4 consecutive columns
-        const int col = c0 + cq;
-        uint32_t cs[4];
-#pragma unroll
-        for (int e = 0; e < 4; ++e) cs[e] = col + e < e16.N16 ? e16.colsum[col + e] : 0u;
-        const bool vec = (e16.N16 & 3) == 0 && col + 4 <= e16.N16;
-#pragma unroll
-        for (int q = 0; q < 8; ++q) {
-            const int lr = (tid >> 5) + 16 * q, row = r0 + lr;
-            if (row >= e16.M16 || col >= e16.N16) continue;
-            const uint32_t rs = e16.rowsum[row];
-            const uint4 v = *(const uint4 *)(sO + lr * OS + cq);
-            uint32_t o[4] = {v.x, v.y, v.z, v.w};
-#pragma unroll
-            for (int e = 0; e < 4; ++e) o[e] += e16.bias_c * (rs + cs[e]) - e16.kc2;
-            int32_t *dst = e16.C + (size_t)row * e16.N16 + col;
-            if (vec) {
-                __builtin_nontemporal_store(__builtin_bit_cast(v4i32, make_uint4(o[0], o[1], o[2], o[3])), (v4i32 *)dst);
-            } else {
-#pragma unroll
-                for (int e = 0; e < 4; ++e)
-                    if (col + e < e16.N16) dst[e] = (int32_t)o[e];
-            }
-        }
+        };
+        // wave-uniform: is the wave's 64 x 32 output block inside C?
+        if (m16_0 + 64 <= e16.M16 && n16_0 + 32 <= e16.N16) epilogue(std::false_type{});
+        else epilogue(std::true_type{});
     }
 }
 }  // namespace i8g
