@@ -448,12 +448,12 @@ __global__ __launch_bounds__(THREADS, 1) void gemm_i8_dma_kernel(const int8_t *_
 #pragma unroll
             for (int r = 0; r < 16; ++r) {
                 const int row = m0 + wm + i * 32 + 8 * (r >> 2) + 4 * lh + (r & 3);
-                if (row >= M) continue;
+                if (!FULL && row >= M) continue;   // full tiles: always inside
                 int32_t *crow = C + (size_t)row * N;
 #pragma unroll
                 for (int j = 0; j < 2; ++j) {
                     const int col = n0 + wn + j * 32 + l32;
-                    if (col < N) __builtin_nontemporal_store(acc[i][j][r], crow + col);
+                    if (FULL || col < N) __builtin_nontemporal_store(acc[i][j][r], crow + col);
                 }
             }
         }
