@@ -254,7 +254,9 @@ __global__ __launch_bounds__(THREADS, 1) void gemm_i8_kernel(const int8_t *__res
 //   issue step kt-1+NSTAGE into that buffer;
 //   read p0 of step kt+1;  MFMAs on p1.
 // The wait is explicit (s_waitcnt vmcnt) and the barrier is a bare
-// s_barrier: the loads of later steps stay in flight across it.
+// s_barrier: the loads of later steps stay in flight across it.  (This is
+// the schedule of the edge-tile path; full tiles use the ping-pong schedule
+// described at the FULL loop.)
 constexpr int NSTAGE = 4;
 constexpr int DMA_PER_STAGE = 4;     // instructions per wave per stage
 
@@ -386,32 +388,84 @@ __global__ __launch_bounds__(THREADS, 1) void gemm_i8_dma_kernel(const int8_t *_
         using S2 = std::integral_constant<int, 2>;
         using S3 = std::integral_constant<int, 3>;
         static_assert(NSTAGE == 4, "the unrolled loop below assumes 4 stages");
+        // Ping-pong schedule.  Waves w and w + 4 share a SIMD; group 0
+        // (waves 0-3) runs the 16 MFMAs of step j while group 1 (waves 4-7)
+        // reads step j's fragments and issues its DMA share, then the groups
+        // swap, so one wave's LDS / DMA phase always overlaps the other
+        // wave's MFMA phase on the same SIMD (with both groups in the same
+        // phase, the SIMD's MFMA pipe idled while both waited on LDS).
+        // Slots between barriers:
+        //   A_j = {group 0: MFMA(j),   group 1: MEM(j)}
+        //   B_j = {group 0: MEM(j+1), group 1: MFMA(j)}
+        // MEM(s) reads both K halves of step s (stage s % 4) and issues the
+        // wave's DMA share of step s + 3 into stage (s + 3) % 4; it ends with
+        // lgkmcnt(0), so every read of a stage is complete at the barrier
+        // closing its slot.  Stage s % 4 is read in B_{s-1} and A_s and
+        // refilled (step s + 4) in B_s and A_{s+1}: after both reads.  Before
+        // the barrier closing A_j every wave waits for its own share of step
+        // j + 1 (vmcnt(8): its shares of steps j + 2 and j + 3 stay in
+        // flight), so the reads of step j + 1 in B_j and A_{j+1} find it in
+        // LDS.  Both groups pass the same barriers (2 + 2 per step).
         issue_f(S0{}, 0);
         issue_f(S1{}, BK);
         issue_f(S2{}, 2 * BK);
-        DET_WAIT_VMCNT(DMA_PER_STAGE * (NSTAGE - 2));   // step 0 landed
+        DET_WAIT_VMCNT(DMA_PER_STAGE * 2);   // step 0 landed
         __builtin_amdgcn_s_barrier();
-        Ops p0, p1;
-        read_ops(p0, 0, 0);
-        auto step = [&](auto cur_c, int kt) {
-            constexpr int cur = decltype(cur_c)::value, nxt = (cur + 1) % NSTAGE;
-            read_ops(p1, cur, 1);
-            mma(p0);
-            DET_WAIT_VMCNT(DMA_PER_STAGE * (NSTAGE - 3));
-            __builtin_amdgcn_s_waitcnt(0xc07f & ~(15 << 8));   // lgkmcnt(0)
-            __builtin_amdgcn_s_barrier();
-            issue_f(std::integral_constant<int, (cur + NSTAGE - 1) % NSTAGE>{}, (kt + NSTAGE - 1) * BK);
-            __builtin_amdgcn_sched_barrier(0);
-            read_ops(p0, nxt, 0);
-            mma(p1);
-            __builtin_amdgcn_sched_barrier(0);
+        Ops q0, q1;
+        auto mem = [&](auto st_c, int s) {
+            constexpr int st = decltype(st_c)::value;
+            read_ops(q0, st, 0);
+            read_ops(q1, st, 1);
+            issue_f(std::integral_constant<int, (st + 3) % NSTAGE>{}, (s + 3) * BK);
         };
-        for (int kt = 0; kt < nk; kt += NSTAGE) {
-            step(S0{}, kt);
-            step(S1{}, kt + 1);
-            step(S2{}, kt + 2);
-            step(S3{}, kt + 3);
+        auto lgkm0 = [&]() { __builtin_amdgcn_s_waitcnt(0xc07f & ~(15 << 8)); };
+        if (wave < 4) {
+            mem(S0{}, 0);
+            lgkm0();
+            __builtin_amdgcn_s_barrier();
+            auto step0 = [&](auto cur_c, int kt) {
+                constexpr int nxt = (decltype(cur_c)::value + 1) % NSTAGE;
+                __builtin_amdgcn_sched_barrier(0);
+                mma(q0);
+                mma(q1);
+                __builtin_amdgcn_sched_barrier(0);
+                DET_WAIT_VMCNT(DMA_PER_STAGE * 2);
+                __builtin_amdgcn_s_barrier();
+                __builtin_amdgcn_sched_barrier(0);
+                if (kt + 1 < nk) mem(std::integral_constant<int, nxt>{}, kt + 1);
+                lgkm0();
+                __builtin_amdgcn_sched_barrier(0);
+                __builtin_amdgcn_s_barrier();
+            };
+            for (int kt = 0; kt < nk; kt += NSTAGE) {
+                step0(S0{}, kt);
+                step0(S1{}, kt + 1);
+                step0(S2{}, kt + 2);
+                step0(S3{}, kt + 3);
+            }
+        } else {
+            __builtin_amdgcn_s_barrier();
+            auto step1 = [&](auto cur_c, int kt) {
+                __builtin_amdgcn_sched_barrier(0);
+                mem(cur_c, kt);
+                DET_WAIT_VMCNT(DMA_PER_STAGE * 2);
+                lgkm0();
+                __builtin_amdgcn_s_barrier();
+                __builtin_amdgcn_sched_barrier(0);
+                mma(q0);
+                mma(q1);
+                __builtin_amdgcn_sched_barrier(0);
+                __builtin_amdgcn_s_barrier();
+            };
+            for (int kt = 0; kt < nk; kt += NSTAGE) {
+                step1(S0{}, kt);
+                step1(S1{}, kt + 1);
+                step1(S2{}, kt + 2);
+                step1(S3{}, kt + 3);
+            }
         }
+        // the loads issued past the end of K are zero fills; none may still
+        // be writing LDS when the workgroup ends
         DET_WAIT_VMCNT(0);
     } else {
 #pragma unroll
