@@ -45,22 +45,9 @@ __global__ __launch_bounds__(256) void prep_i16_a(const int16_t *__restrict__ sr
     const int row = blockIdx.x * 4 + (tid >> 6);
     if (row >= M) return;
     const int16_t *s = src + (size_t)row * K;
-    const bool vec = ((K & 7) == 0) && ((((uintptr_t)src) & 15) == 0);
     uint32_t sum = 0;
-    for (int k0 = lane * 16; k0 < Kp; k0 += 1024) {
-        const int nv = min(max(K - k0, 0), 16);
-        uint32_t d[8];   // 16 int16, two per dword
-        if (vec && nv == 16) {
-            const uint4 v0 = *(const uint4 *)(s + k0), v1 = *(const uint4 *)(s + k0 + 8);
-            d[0] = v0.x, d[1] = v0.y, d[2] = v0.z, d[3] = v0.w, d[4] = v1.x, d[5] = v1.y, d[6] = v1.z, d[7] = v1.w;
-        } else {
-#pragma unroll
-            for (int h = 0; h < 8; ++h) {
-                const uint32_t lo = 2 * h < nv ? (uint16_t)s[k0 + 2 * h] : 0u;
-                const uint32_t hi = 2 * h + 1 < nv ? (uint16_t)s[k0 + 2 * h + 1] : 0u;
-                d[h] = lo | (hi << 16);
-            }
-        }
+    // 16 int16 (two per dword) at k0, nv of them valid -> the two limb rows
+    auto emit = [&](const uint32_t (&d)[8], int k0, int nv) {
 #pragma unroll
         for (int h = 0; h < 8; ++h) sum += (uint32_t)(int32_t)(int16_t)(d[h] & 0xffff) + (uint32_t)((int32_t)d[h] >> 16);
         uint32_t lo[4], hi[4];
@@ -71,6 +58,39 @@ __global__ __launch_bounds__(256) void prep_i16_a(const int16_t *__restrict__ sr
         }
         *(uint4 *)(A2 + (size_t)(2 * row) * Kp + k0) = make_uint4(lo[0], lo[1], lo[2], lo[3]);
         *(uint4 *)(A2 + (size_t)(2 * row + 1) * Kp + k0) = make_uint4(hi[0], hi[1], hi[2], hi[3]);
+    };
+    if (((K & 15) == 0) && ((((uintptr_t)src) & 15) == 0)) {
+        // every 16-element chunk is full (Kp == K): up to 4 chunks per lane
+        // loaded before any is processed, so 128 bytes per lane are in flight
+        constexpr int U = 4;
+        for (int k0 = lane * 16; k0 < K; k0 += 1024 * U) {
+            uint4 v[U][2];
+#pragma unroll
+            for (int u = 0; u < U; ++u)
+                if (k0 + 1024 * u < K) {
+                    v[u][0] = *(const uint4 *)(s + k0 + 1024 * u);
+                    v[u][1] = *(const uint4 *)(s + k0 + 1024 * u + 8);
+                }
+#pragma unroll
+            for (int u = 0; u < U; ++u)
+                if (k0 + 1024 * u < K) {
+                    const uint32_t d[8] = {v[u][0].x, v[u][0].y, v[u][0].z, v[u][0].w,
+                                           v[u][1].x, v[u][1].y, v[u][1].z, v[u][1].w};
+                    emit(d, k0 + 1024 * u, 16);
+                }
+        }
+    } else {
+        for (int k0 = lane * 16; k0 < Kp; k0 += 1024) {
+            const int nv = min(max(K - k0, 0), 16);
+            uint32_t d[8];
+#pragma unroll
+            for (int h = 0; h < 8; ++h) {
+                const uint32_t lo = 2 * h < nv ? (uint16_t)s[k0 + 2 * h] : 0u;
+                const uint32_t hi = 2 * h + 1 < nv ? (uint16_t)s[k0 + 2 * h + 1] : 0u;
+                d[h] = lo | (hi << 16);
+            }
+            emit(d, k0, nv);
+        }
     }
 #pragma unroll
     for (int off = 32; off > 0; off >>= 1) sum += (uint32_t)__shfl_xor((int)sum, off);
@@ -87,28 +107,35 @@ __global__ __launch_bounds__(256) void prep_i16_b(const int16_t *__restrict__ sr
     const int tid = threadIdx.x, cg = tid & 15, rg = tid >> 4;
     const int c0 = blockIdx.x * 128 + cg * 8;   // first int16 column of this thread
     const int k0 = blockIdx.y * 64;
-    const bool vec = ((N & 7) == 0) && ((((uintptr_t)src) & 15) == 0);
     uint32_t cs[8] = {0, 0, 0, 0, 0, 0, 0, 0};
     const bool out_col = 2 * c0 < N2;           // this 16-byte chunk exists in B2
+    uint32_t dq[4][4];
+    // block-uniform: the whole 64 x 128 tile inside B with 16-byte rows
+    if (((N & 7) == 0) && ((((uintptr_t)src) & 15) == 0) && blockIdx.x * 128 + 128 <= N && k0 + 64 <= K) {
+        // the thread's 4 rows are loaded before any is processed
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+            const uint4 v = *(const uint4 *)(src + (size_t)(k0 + rg + 16 * q) * N + c0);
+            dq[q][0] = v.x, dq[q][1] = v.y, dq[q][2] = v.z, dq[q][3] = v.w;
+        }
+    } else {
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+            const int k = k0 + rg + 16 * q;
+#pragma unroll
+            for (int h = 0; h < 4; ++h) {
+                const int16_t *p = src + (size_t)k * N + c0;
+                const uint32_t lo = k < K && c0 + 2 * h < N ? (uint16_t)p[2 * h] : 0u;
+                const uint32_t hi = k < K && c0 + 2 * h + 1 < N ? (uint16_t)p[2 * h + 1] : 0u;
+                dq[q][h] = lo | (hi << 16);
+            }
+        }
+    }
 #pragma unroll
     for (int q = 0; q < 4; ++q) {
         const int k = k0 + rg + 16 * q;
         if (k >= Kp) continue;
-        uint32_t d[4] = {0, 0, 0, 0};
-        if (k < K) {
-            const int16_t *p = src + (size_t)k * N + c0;
-            if (vec && c0 + 8 <= N) {
-                const uint4 v = *(const uint4 *)p;
-                d[0] = v.x, d[1] = v.y, d[2] = v.z, d[3] = v.w;
-            } else {
-#pragma unroll
-                for (int h = 0; h < 4; ++h) {
-                    const uint32_t lo = c0 + 2 * h < N ? (uint16_t)p[2 * h] : 0u;
-                    const uint32_t hi = c0 + 2 * h + 1 < N ? (uint16_t)p[2 * h + 1] : 0u;
-                    d[h] = lo | (hi << 16);
-                }
-            }
-        }
+        const uint32_t(&d)[4] = dq[q];
         uint32_t o[4];
 #pragma unroll
         for (int h = 0; h < 4; ++h) {

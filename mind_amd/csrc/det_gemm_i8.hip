@@ -515,51 +515,50 @@ __global__ __launch_bounds__(THREADS, 1) void gemm_i8_dma_kernel(const int8_t *_
         // Elements 2p, 2p+1 of a lane are rows 2i', 2i'+1 (low / high A limb)
         // of one column; lanes l, l^1 hold columns 2j', 2j'+1 (low / high B
         // limb).  The even lane forms c00 + 2^8 c10, the odd lane
-        // 2^8 c01 + 2^16 c11; one lane exchange (a DPP quad permute)
-        // completes pairs 0..3 on the even lane and pairs 4..7 on the odd
-        // lane, which then add the bias terms and store straight from
-        // registers: no LDS staging, no barrier, no divergent branch when the
-        // wave's 64 x 32 output block is inside C.
+        // 2^8 c01 + 2^16 c11, for each of the wave's two 32-column blocks
+        // j = 0, 1.  One lane exchange (a DPP quad permute) per row pair
+        // completes block 0's output on the even lane (it keeps its block-0
+        // part and receives the odd lane's) and block 1's on the odd lane:
+        // even lane 2c holds int16 column c, odd lane 2c+1 column c + 16, of
+        // the same row, so every store instruction writes 2 rows x 32
+        // consecutive int32 (two whole 128-byte lines).  The lanes add the
+        // bias terms and store straight from registers: no LDS staging, no
+        // barrier, no divergent branch when the wave's 64 x 32 output block
+        // is inside C.
         const uint32_t odd = l32 & 1, oddm = 0u - odd;   // oddm: all ones on odd lanes
         const int m16_0 = (m0 + wm) >> 1, n16_0 = (n0 + wn) >> 1;
-        // this lane's stored rows: pair p = 4 odd + kk is int16 row
-        // m16_0 + 16 i + 4 (p >> 1) + 2 lh + (p & 1) = row_l + 16 i + 4 (kk >> 1) + (kk & 1)
-        const int row_l = m16_0 + 8 * (int)odd + 2 * lh;
-        const int col_l = n16_0 + (l32 >> 1);
-        uint32_t rs[4][4], cs[2];
+        // pair p of block row i is int16 row m16_0 + 16 i + 4 (p >> 1) + 2 lh + (p & 1)
+        const int row_l = m16_0 + 2 * lh;
+        const int col = n16_0 + (l32 >> 1) + 16 * (int)odd;
         // bias terms c (rowsum + colsum) - K c^2 with c = 0x80 (the limb
-        // scheme's constant): rs holds (rowsum << 7) - K c^2, cs colsum << 7
-#pragma unroll
-        for (int j = 0; j < 2; ++j) cs[j] = e16.colsum[min(col_l + 16 * j, e16.N16 - 1)] << 7;
+        // scheme's constant): rs = (rowsum << 7) - K c^2 + (colsum << 7)
+        const uint32_t cs = e16.colsum[min(col, e16.N16 - 1)] << 7;
+        uint32_t rs[4][8];
 #pragma unroll
         for (int i = 0; i < 4; ++i)
 #pragma unroll
-            for (int kk = 0; kk < 4; ++kk)
-                rs[i][kk] = (e16.rowsum[min(row_l + 16 * i + 4 * (kk >> 1) + (kk & 1), e16.M16 - 1)] << 7) - e16.kc2;
+            for (int p = 0; p < 8; ++p)
+                rs[i][p] = (e16.rowsum[min(row_l + 16 * i + 4 * (p >> 1) + (p & 1), e16.M16 - 1)] << 7) - e16.kc2 + cs;
         auto epilogue = [&](auto checked_c) {
             constexpr bool checked = decltype(checked_c)::value;
 #pragma unroll
             for (int i = 0; i < 4; ++i)
 #pragma unroll
-                for (int j = 0; j < 2; ++j) {
-                    uint32_t part[8];
+                for (int p = 0; p < 8; ++p) {
+                    uint32_t part[2];
 #pragma unroll
-                    for (int pp = 0; pp < 8; ++pp) {
-                        const uint32_t lo = (uint32_t)acc[i][j][2 * pp], hi = (uint32_t)acc[i][j][2 * pp + 1];
-                        part[pp] = (lo + (hi << 8)) << (8 * odd);   // odd lane: 2^8 c01 + 2^16 c11
+                    for (int j = 0; j < 2; ++j) {
+                        const uint32_t lo = (uint32_t)acc[i][j][2 * p], hi = (uint32_t)acc[i][j][2 * p + 1];
+                        part[j] = (lo + (hi << 8)) << (8 * odd);   // odd lane: 2^8 c01 + 2^16 c11
                     }
-                    const int col = col_l + 16 * j;
-#pragma unroll
-                    for (int kk = 0; kk < 4; ++kk) {
-                        const uint32_t send = (part[kk] & oddm) | (part[4 + kk] & ~oddm);
-                        const uint32_t keep = (part[4 + kk] & oddm) | (part[kk] & ~oddm);
-                        // lanes 2c <-> 2c+1: quad_perm [1, 0, 3, 2]
-                        const uint32_t recv = (uint32_t)__builtin_amdgcn_mov_dpp((int)send, 0xB1, 0xF, 0xF, false);
-                        const int row = row_l + 16 * i + 4 * (kk >> 1) + (kk & 1);
-                        const uint32_t o = keep + recv + rs[i][kk] + cs[j];
-                        int32_t *dst = e16.C + (size_t)row * e16.N16 + col;
-                        if (!checked || (row < e16.M16 && col < e16.N16)) __builtin_nontemporal_store((int32_t)o, dst);
-                    }
+                    const uint32_t send = (part[0] & oddm) | (part[1] & ~oddm);
+                    const uint32_t keep = (part[1] & oddm) | (part[0] & ~oddm);
+                    // lanes 2c <-> 2c+1: quad_perm [1, 0, 3, 2]
+                    const uint32_t recv = (uint32_t)__builtin_amdgcn_mov_dpp((int)send, 0xB1, 0xF, 0xF, false);
+                    const int row = row_l + 16 * i + 4 * (p >> 1) + (p & 1);
+                    const uint32_t o = keep + recv + rs[i][p];
+                    int32_t *dst = e16.C + (size_t)row * e16.N16 + col;
+                    if (!checked || (row < e16.M16 && col < e16.N16)) __builtin_nontemporal_store((int32_t)o, dst);
                 }
         };
         // wave-uniform: is the wave's 64 x 32 output block inside C?

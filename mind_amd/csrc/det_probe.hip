@@ -12,13 +12,34 @@ namespace probe {
 // the loop holds nothing else: the compiler's register allocation cannot add
 // accumulator moves, and each accumulator chain has 7 other MFMAs between its
 // dependent issues.  SHAPE 0: 16x16x64 (16384 MACs), SHAPE 1: 32x32x32
-// (32768 MACs).
+// (32768 MACs), both with one operand pair for all MFMAs.  SHAPE 2:
+// 32x32x32 with 8 different operand pairs (A from in[64 c + l], B from
+// in[512 + 64 c + l]), cycled so consecutive MFMAs see different data: with
+// random operands this is the issue rate a GEMM's data allows, since the
+// clock under int8 MFMA load depends on how many operand bits toggle.
 template <int SHAPE>
 __global__ __launch_bounds__(256) void mfma_i8_kernel(const v2i64 *__restrict__ in, int *__restrict__ out, int iters) {
     const int l = threadIdx.x & 63;
     const v2i64 a = in[l], b = in[64 + l];
     int s = 0;
-    if (SHAPE == 0) {
+    if (SHAPE == 2) {
+        v2i64 x[8], y[8];
+#pragma unroll
+        for (int c = 0; c < 8; ++c) {
+            x[c] = in[64 * c + l];
+            y[c] = in[512 + 64 * c + l];
+        }
+        v16i32 c0 = {0}, c1 = c0, c2 = c0, c3 = c0, c4 = c0, c5 = c0, c6 = c0, c7 = c0;
+        for (int it = 0; it < iters; ++it) {
+#define MF(c, i, j) asm volatile("v_mfma_i32_32x32x32_i8 %0, %1, %2, %0" : "+v"(c) : "v"(x[i]), "v"(y[j]))
+            MF(c0, 0, 0); MF(c1, 1, 1); MF(c2, 2, 2); MF(c3, 3, 3); MF(c4, 4, 4); MF(c5, 5, 5); MF(c6, 6, 6); MF(c7, 7, 7);
+            MF(c0, 1, 2); MF(c1, 2, 3); MF(c2, 3, 4); MF(c3, 4, 5); MF(c4, 5, 6); MF(c5, 6, 7); MF(c6, 7, 0); MF(c7, 0, 1);
+#undef MF
+        }
+        asm volatile("s_nop 7\n s_nop 7\n s_nop 7" ::);
+        const v16i32 t = c0 ^ c1 ^ c2 ^ c3 ^ c4 ^ c5 ^ c6 ^ c7;
+        for (int i = 0; i < 16; ++i) s ^= t[i];
+    } else if (SHAPE == 0) {
         v4i32 c0 = {0, 0, 0, 1}, c1 = c0, c2 = c0, c3 = c0, c4 = c0, c5 = c0, c6 = c0, c7 = c0;
         for (int it = 0; it < iters; ++it) {
 #define MF(c) asm volatile("v_mfma_i32_16x16x64_i8 %0, %1, %2, %0" : "+v"(c) : "v"(a), "v"(b))
@@ -62,17 +83,22 @@ __global__ __launch_bounds__(256) void copy_kernel(uint4 *__restrict__ dst, cons
 
 extern "C" {
 
-// in: 128 x 16 bytes of operands, out: blocks*256 ints.  Returns the launch
-// status; ops per launch = blocks * 4 waves * iters * 8 * MACs(shape) * 2,
-// MACs = 16384 (shape 0, 16x16x64) or 32768 (shape 1, 32x32x32).
+// in: 128 x 16 bytes of operands (shapes 0, 1) or 1024 x 16 (shape 2), out:
+// blocks*256 ints.  Returns the launch status; ops per launch = blocks * 4
+// waves * iters * MFMAs * MACs * 2: 8 x 16384 (shape 0, 16x16x64),
+// 8 x 32768 (shape 1, 32x32x32), 16 x 32768 (shape 2, 32x32x32 cycling
+// 8 operand pairs).
 int64_t det_probe_mfma_i8(const void *in, int32_t *out, int64_t blocks, int64_t iters, int64_t shape, void *stream) {
-    if (!in || !out || blocks <= 0 || iters <= 0 || blocks > (1 << 20) || iters > (1 << 30) || shape < 0 || shape > 1)
+    if (!in || !out || blocks <= 0 || iters <= 0 || blocks > (1 << 20) || iters > (1 << 30) || shape < 0 || shape > 2)
         return det_fail(DET_ERR_ARG, "bad det_probe_mfma_i8 arguments");
     if (shape == 0)
         hipLaunchKernelGGL(det::probe::mfma_i8_kernel<0>, dim3((unsigned)blocks), dim3(256), 0, (hipStream_t)stream,
                            (const det::v2i64 *)in, out, (int)iters);
-    else
+    else if (shape == 1)
         hipLaunchKernelGGL(det::probe::mfma_i8_kernel<1>, dim3((unsigned)blocks), dim3(256), 0, (hipStream_t)stream,
+                           (const det::v2i64 *)in, out, (int)iters);
+    else
+        hipLaunchKernelGGL(det::probe::mfma_i8_kernel<2>, dim3((unsigned)blocks), dim3(256), 0, (hipStream_t)stream,
                            (const det::v2i64 *)in, out, (int)iters);
     DET_HIP_CHECK(hipGetLastError());
     return 0;
