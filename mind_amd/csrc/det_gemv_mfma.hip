@@ -227,6 +227,16 @@ __global__ __launch_bounds__(THREADS8, 1) void gemv8_kernel(const int32_t *__res
             for (int j = 0; j < 4; ++j)
                 wb[d][j] = buf_load16(rw, ls + DEPTH < half ? wbase + (uint32_t)(64 * (st + DEPTH) + 16 * j) * 4u
                                                             : OOB_OFFSET);
+            // query low halves of this step: the first half is read here, so
+            // its LDS latency hides behind the MFMAs, the second half after
+            // them, behind the first half's residues (reading each at its
+            // point of use made the compiler wait on every read: 16 LDS round
+            // trips per step in series)
+            uint4 XV[4][4];
+#pragma unroll
+            for (int j = 0; j < 2; ++j)
+#pragma unroll
+                for (int bp = 0; bp < 4; ++bp) XV[j][bp] = sxl[((d8 * 4 + j) * 4 + bp) * 4 + g];
             v2i64 B[4];
 #pragma unroll
             for (int q = 0; q < 4; ++q) B[q] = __builtin_bit_cast(v2i64, sxp[(d8 * 4 + q) * 64 + lane]);
@@ -239,12 +249,17 @@ __global__ __launch_bounds__(THREADS8, 1) void gemv8_kernel(const int32_t *__res
                     if (p + q <= 5) acc[p + q] = mfma16x16x64(A, B[q], acc[p + q]);
             }
             // residues for every query vector
+            __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+            for (int j = 2; j < 4; ++j)
+#pragma unroll
+                for (int bp = 0; bp < 4; ++bp) XV[j][bp] = sxl[((d8 * 4 + j) * 4 + bp) * 4 + g];
 #pragma unroll
             for (int j = 0; j < 4; ++j) {
                 const uint32_t L0 = L[j][0], L1 = L[j][1];
 #pragma unroll
                 for (int bp = 0; bp < 4; ++bp) {
-                    const uint4 xv = sxl[((d8 * 4 + j) * 4 + bp) * 4 + g];
+                    const uint4 xv = XV[j][bp];
                     racc[2 * bp] = residue2(L1, xv.y, residue2(L0, xv.x, racc[2 * bp]));
                     racc[2 * bp + 1] = residue2(L1, xv.w, residue2(L0, xv.z, racc[2 * bp + 1]));
                 }
