@@ -16,16 +16,17 @@
 // each 2x2 block, with the bias terms, into one int32 output.  Every step is
 // mod 2^32, which is the i64 sum truncated to 32 bits: no flush, any K.
 //
-// Prep: prep_i16_a (one wave per A row: limb split, exact row sum, zeroes
-// the column-sum buffer) and prep_i16_b (64 x 128 tiles of B: the XOR, zero
-// padding, column sums by one atomic per column per tile).
+// Prep: one launch, prep_i16 (one wave per A row: limb split, exact row
+// sum; 64 x 128 tiles of B: the XOR, zero padding, up to MAX_CS exact partial
+// column sums per column, added by the GEMM epilogue).
 #include "det_common.h"
 #include "det_kernels.h"
 
 namespace det {
 
 hipError_t launch_gemm_i8_i16epi(const int8_t *A2, const int8_t *B2, int M2, int N2, int Kp, const uint32_t *rowsum,
-                                 const uint32_t *colsum, int32_t *C, int M16, int N16, int K16, hipStream_t s);
+                                 const uint32_t *colsum, int ncs, int32_t *C, int M16, int N16, int K16,
+                                 hipStream_t s);
 
 namespace i16x {
 
@@ -36,13 +37,12 @@ __device__ __forceinline__ uint32_t valid_mask(int nv, int d) {
     return r >= 4 ? 0xffffffffu : (r <= 0 ? 0u : (1u << (8 * r)) - 1u);
 }
 
-// A [M][K] int16 -> A2 [2M][Kp] int8 limb rows, rowsum [M] (mod 2^32).
-__global__ __launch_bounds__(256) void prep_i16_a(const int16_t *__restrict__ src, int M, int K, int Kp,
-                                                  int8_t *__restrict__ A2, uint32_t *__restrict__ rowsum,
-                                                  uint32_t *__restrict__ zero, int nzero) {
+// A [M][K] int16 -> A2 [2M][Kp] int8 limb rows, rowsum [M] (mod 2^32):
+// rows 4 blk .. 4 blk + 3, one wave per row.
+__device__ __forceinline__ void prep_a_rows(const int16_t *__restrict__ src, int M, int K, int Kp,
+                                            int8_t *__restrict__ A2, uint32_t *__restrict__ rowsum, int blk) {
     const int tid = threadIdx.x, lane = tid & 63;
-    for (int i = blockIdx.x * 256 + tid; i < nzero; i += gridDim.x * 256) zero[i] = 0;
-    const int row = blockIdx.x * 4 + (tid >> 6);
+    const int row = blk * 4 + (tid >> 6);
     if (row >= M) return;
     const int16_t *s = src + (size_t)row * K;
     uint32_t sum = 0;
@@ -98,20 +98,18 @@ __global__ __launch_bounds__(256) void prep_i16_a(const int16_t *__restrict__ sr
 }
 
 // B [K][N] int16 -> B2 [Kp][N2] int8 (N2 = round_up(2N, 16)): the bytes of B
-// with every low byte ^ 0x80, zero in padding rows / columns; colsum [N]
-// (mod 2^32, atomic, zeroed by prep_i16_a).  256 threads per 64 x 128 tile:
-// thread t handles 8 columns (16 bytes) of rows (t >> 4) + 16 q, q = 0..3.
-__global__ __launch_bounds__(256) void prep_i16_b(const int16_t *__restrict__ src, int K, int N, int Kp, int N2,
-                                                  int8_t *__restrict__ B2, uint32_t *__restrict__ colsum) {
-    __shared__ uint32_t part[16][129];
+// with every low byte ^ 0x80, zero in padding rows / columns.  One 64 x 128
+// tile (rows k0.., int16 columns 128 bx..): thread t handles 8 columns
+// (16 bytes) of rows (t >> 4) + 16 q, q = 0..3, and adds its columns' values
+// into cs (mod 2^32).
+__device__ __forceinline__ void prep_b_tile(const int16_t *__restrict__ src, int K, int N, int Kp, int N2,
+                                            int8_t *__restrict__ B2, int bx, int k0, uint32_t (&cs)[8]) {
     const int tid = threadIdx.x, cg = tid & 15, rg = tid >> 4;
-    const int c0 = blockIdx.x * 128 + cg * 8;   // first int16 column of this thread
-    const int k0 = blockIdx.y * 64;
-    uint32_t cs[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+    const int c0 = bx * 128 + cg * 8;           // first int16 column of this thread
     const bool out_col = 2 * c0 < N2;           // this 16-byte chunk exists in B2
     uint32_t dq[4][4];
     // block-uniform: the whole 64 x 128 tile inside B with 16-byte rows
-    if (((N & 7) == 0) && ((((uintptr_t)src) & 15) == 0) && blockIdx.x * 128 + 128 <= N && k0 + 64 <= K) {
+    if (((N & 7) == 0) && ((((uintptr_t)src) & 15) == 0) && bx * 128 + 128 <= N && k0 + 64 <= K) {
         // the thread's 4 rows are loaded before any is processed
 #pragma unroll
         for (int q = 0; q < 4; ++q) {
@@ -147,17 +145,45 @@ __global__ __launch_bounds__(256) void prep_i16_b(const int16_t *__restrict__ sr
         }
         if (out_col) *(uint4 *)(B2 + (size_t)k * N2 + 2 * c0) = make_uint4(o[0], o[1], o[2], o[3]);
     }
+}
+
+// Column-sum partials: at most MAX_CS per column (det_kernels.h).
+__host__ __device__ inline int i16_nkt(int Kp) { return (Kp + 63) / 64; }   // 64-row B tiles (Kp % 16 == 0)
+__host__ __device__ inline int i16_ktp(int Kp) { return (i16_nkt(Kp) + MAX_CS - 1) / MAX_CS; }
+__host__ __device__ inline int i16_ncs(int Kp) { return (i16_nkt(Kp) + i16_ktp(Kp) - 1) / i16_ktp(Kp); }
+
+// Both operands in one launch (the two preps are independent; each alone is
+// a few microseconds of fixed launch latency).  Blocks [0, na) split the A
+// rows; block na + by * nbx + bx prepares the 64-row B tiles
+// [by * ktp, (by + 1) * ktp) of column strip bx and writes its exact partial
+// column sums to colsum[by][N] -- the GEMM epilogue adds the ncs partials,
+// so no atomics and no zeroed buffer are needed.
+__global__ __launch_bounds__(256) void prep_i16(const int16_t *__restrict__ A, const int16_t *__restrict__ B,
+                                                int M, int N, int K, int Kp, int N2, int8_t *__restrict__ A2,
+                                                int8_t *__restrict__ B2, uint32_t *__restrict__ rowsum,
+                                                uint32_t *__restrict__ colsum, int na, int nbx, int ktp) {
+    if ((int)blockIdx.x < na) {
+        prep_a_rows(A, M, K, Kp, A2, rowsum, blockIdx.x);
+        return;
+    }
+    __shared__ uint32_t part[16][129];
+    const int t = blockIdx.x - na, bx = t % nbx, by = t / nbx;
+    const int kt_end = min((by + 1) * ktp, i16_nkt(Kp));
+    uint32_t cs[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+    for (int kt = by * ktp; kt < kt_end; ++kt) prep_b_tile(B, K, N, Kp, N2, B2, bx, kt * 64, cs);
+    const int tid = threadIdx.x, cg = tid & 15, rg = tid >> 4;
 #pragma unroll
     for (int e = 0; e < 8; ++e) part[rg][cg * 8 + e] = cs[e];
     __syncthreads();
     if (tid < 128) {
-        uint32_t t = 0;
+        uint32_t sum = 0;
 #pragma unroll
-        for (int r = 0; r < 16; ++r) t += part[r][tid];
-        const int col = blockIdx.x * 128 + tid;
-        if (col < N) atomicAdd(colsum + col, t);
+        for (int r = 0; r < 16; ++r) sum += part[r][tid];
+        const int col = bx * 128 + tid;
+        if (col < N) colsum[(size_t)by * N + col] = sum;
     }
 }
+
 
 }  // namespace i16x
 
@@ -170,7 +196,8 @@ bool i16x_eligible(int M, int N, int K) {
 
 size_t i16x_workspace_bytes(int M, int N, int K) {
     const size_t Kp = ((size_t)K + 15) / 16 * 16, N2 = (2 * (size_t)N + 15) / 16 * 16;
-    return align256(2 * (size_t)M * Kp) + align256(Kp * N2) + align256(4 * (size_t)M) + align256(4 * (size_t)N);
+    return align256(2 * (size_t)M * Kp) + align256(Kp * N2) + align256(4 * (size_t)M) +
+           align256(4 * (size_t)i16x::i16_ncs((int)Kp) * N);
 }
 
 hipError_t launch_gemm_i16x(const int16_t *A, const int16_t *B, int32_t *C, int M, int N, int K, void *ws,
@@ -181,12 +208,12 @@ hipError_t launch_gemm_i16x(const int16_t *A, const int16_t *B, int32_t *C, int 
     int8_t *B2 = A2 + align256(2 * (size_t)M * Kp);
     uint32_t *rowsum = (uint32_t *)(B2 + align256((size_t)Kp * N2));
     uint32_t *colsum = (uint32_t *)((int8_t *)rowsum + align256(4 * (size_t)M));
-    hipLaunchKernelGGL(prep_i16_a, dim3((M + 3) / 4), dim3(256), 0, s, A, M, K, Kp, A2, rowsum, colsum, N);
-    hipLaunchKernelGGL(prep_i16_b, dim3((N + 127) / 128, (Kp + 63) / 64), dim3(256), 0, s, B, K, N, Kp, N2, B2,
-                       colsum);
+    const int na = (M + 3) / 4, nbx = (N + 127) / 128, ktp = i16_ktp(Kp), ncs = i16_ncs(Kp);
+    hipLaunchKernelGGL(prep_i16, dim3(na + nbx * ncs), dim3(256), 0, s, A, B, M, N, K, Kp, N2, A2, B2, rowsum,
+                       colsum, na, nbx, ktp);
     const hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
-    return launch_gemm_i8_i16epi(A2, B2, 2 * M, N2, Kp, rowsum, colsum, C, M, N, K, s);
+    return launch_gemm_i8_i16epi(A2, B2, 2 * M, N2, Kp, rowsum, colsum, ncs, C, M, N, K, s);
 }
 
 }  // namespace det

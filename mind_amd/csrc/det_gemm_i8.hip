@@ -269,9 +269,10 @@ constexpr int DMA_PER_STAGE = 4;     // instructions per wave per stage
 // and adds the bias terms, all mod 2^32.
 enum { EPI_I8 = 0, EPI_I16 = 1 };
 struct I16Epi {
-    const uint32_t *rowsum, *colsum;   // exact sums mod 2^32 of A rows / B columns
+    const uint32_t *rowsum;            // exact sums mod 2^32 of A rows
+    const uint32_t *colsum;            // [ncs][N16] partial sums mod 2^32 of B columns (added here)
     int32_t *C;                        // [M16][N16] int32
-    int M16, N16;
+    int M16, N16, ncs;
     uint32_t bias_c, kc2;              // c = 0x80 (the epilogue relies on it), K c^2 mod 2^32
 };
 
@@ -301,6 +302,16 @@ __global__ __launch_bounds__(THREADS, 1) void gemm_i8_dma_kernel(const int8_t *_
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int wm = (wave >> 2) * WM, wn = (wave & 3) * WN;
     const int l32 = lane & 31, lh = lane >> 5;
+    // EPI_I16: this lane's column-sum partials are loaded here and held in
+    // registers, so their latency hides behind the K loop (the epilogue's
+    // column is known from the start: see the EPI_I16 epilogue)
+    uint32_t cs_part[EPI == EPI_I16 ? MAX_CS : 1];
+    if constexpr (EPI == EPI_I16) {
+        const int odd = l32 & 1;
+        const int cc = min(((n0 + wn) >> 1) + (l32 >> 1) + 16 * odd, e16.N16 - 1);
+#pragma unroll
+        for (int i = 0; i < MAX_CS; ++i) cs_part[i] = e16.colsum[(size_t)min(i, e16.ncs - 1) * e16.N16 + cc];
+    }
     const int tg = lane >> 4, ti = lane & 15;
     const int tr_row = 16 * (tg >> 1) + (ti >> 1);
     const int tr_col = 16 * (tg & 1) + 8 * (ti & 1);
@@ -532,7 +543,12 @@ __global__ __launch_bounds__(THREADS, 1) void gemm_i8_dma_kernel(const int8_t *_
         const int col = n16_0 + (l32 >> 1) + 16 * (int)odd;
         // bias terms c (rowsum + colsum) - K c^2 with c = 0x80 (the limb
         // scheme's constant): rs = (rowsum << 7) - K c^2 + (colsum << 7)
-        const uint32_t cs = e16.colsum[min(col, e16.N16 - 1)] << 7;
+        // the ncs column-sum partials (loaded at the start: clamped index,
+        // masked add)
+        uint32_t cs = 0;
+#pragma unroll
+        for (int i = 0; i < MAX_CS; ++i) cs += i < e16.ncs ? cs_part[i] : 0u;
+        cs <<= 7;
         uint32_t rs[4][8];
 #pragma unroll
         for (int i = 0; i < 4; ++i)
@@ -590,10 +606,11 @@ hipError_t launch_gemm_i8(const int8_t *A, const int8_t *B, int32_t *C, int M, i
 // det_gemm_i16x.hip): A2 [2*M16][Kp], B2 [Kp][N2] with Kp % 16 == 0,
 // N2 % 16 == 0, both 16-byte aligned, 2*M16*Kp and Kp*N2 below 2^31.
 hipError_t launch_gemm_i8_i16epi(const int8_t *A2, const int8_t *B2, int M2, int N2, int Kp, const uint32_t *rowsum,
-                                 const uint32_t *colsum, int32_t *C, int M16, int N16, int K16, hipStream_t s) {
+                                 const uint32_t *colsum, int ncs, int32_t *C, int M16, int N16, int K16,
+                                 hipStream_t s) {
     using namespace i8g;
     const int tiles_m = (M2 + BM - 1) / BM, tiles_n = (N2 + BN - 1) / BN;
-    I16Epi e{rowsum, colsum, C, M16, N16, 0x80u, (uint32_t)((uint64_t)(uint32_t)K16 * 0x4000u)};
+    I16Epi e{rowsum, colsum, C, M16, N16, ncs, 0x80u, (uint32_t)((uint64_t)(uint32_t)K16 * 0x4000u)};
     const bool full = M2 % BM == 0 && N2 % BN == 0 && Kp % (BK * NSTAGE) == 0;
     if (full)
         hipLaunchKernelGGL((gemm_i8_dma_kernel<EPI_I16, true>), dim3(tiles_m * tiles_n), dim3(THREADS), 0, s, A2, B2,

@@ -10,10 +10,10 @@
 // The derivation and the limb / bias algebra are the same as the first
 // generation kernel in det_gemm_limb.hip; this file changes the schedule:
 //
-//  * Prep: one wave per source row (A, or B^T) with no atomics, and a
-//    transposing 64x64 tile kernel for row-major B.  Both write the limb
+//  * Prep (one launch for both operands): one wave per source row (A, or
+//    B^T), and transposing 64x64 tiles for row-major B.  Both write the limb
 //    planes [p][rows][Kp] (K-contiguous, biased bytes), the low-16 halves
-//    [rows][Kp] and the exact int64 row / column sums.
+//    [rows][Kp] and exact int64 row sums / column-sum partials (no atomics).
 //  * Main kernel: 64x64 output tile per 512-thread workgroup, 48 KiB LDS
 //    stages (limb planes + low halves of A and B for 64 k) filled by
 //    direct global->LDS DMA two steps ahead (3 stages).  The waves are
@@ -78,16 +78,13 @@ __device__ __forceinline__ void split16(const uint32_t (&w)[16], int nv, uint4 (
 
 // ------------------------------------------------------------------ prep
 // Rows of src[R][K] (operand A, or B given as B^T): one wave per row, lane
-// chunks of 16 k.  Also zeroes `zero[0..nzero)` (the other operand's sum
-// buffer, accumulated atomically by a later launch on the same stream).
-__global__ __launch_bounds__(256) void prep_rows_kernel(const int32_t *__restrict__ src, int R, int K, int Kp,
-                                                        uint8_t *__restrict__ planes, size_t plane_stride,
-                                                        uint16_t *__restrict__ lo16,
-                                                        unsigned long long *__restrict__ sums,
-                                                        unsigned long long *__restrict__ zero, int nzero) {
+// chunks of 16 k; rows 4 blk .. 4 blk + 3.
+__device__ __forceinline__ void prep_rows(const int32_t *__restrict__ src, int R, int K, int Kp,
+                                          uint8_t *__restrict__ planes, size_t plane_stride,
+                                          uint16_t *__restrict__ lo16, unsigned long long *__restrict__ sums,
+                                          int blk) {
     const int tid = threadIdx.x, lane = tid & 63;
-    for (int i = blockIdx.x * 256 + tid; i < nzero; i += gridDim.x * 256) zero[i] = 0;
-    const int row = blockIdx.x * 4 + (tid >> 6);
+    const int row = blk * 4 + (tid >> 6);
     if (row >= R) return;
     const int32_t *s = src + (size_t)row * K;
     const bool vec = ((K & 3) == 0) && ((((uintptr_t)src) & 15) == 0);
@@ -120,16 +117,15 @@ __global__ __launch_bounds__(256) void prep_rows_kernel(const int32_t *__restric
     if (lane == 0) sums[row] = (unsigned long long)sum;
 }
 
-// Row-major B[K][N] -> B^T planes [p][N][Kp], low halves [N][Kp], column
-// sums (atomic; zeroed by prep_rows_kernel).  One 64 (k) x 64 (n) tile per
-// 256-thread workgroup; lane = 4 * column + k-quarter so that each column's
-// 64 plane bytes are written by four neighbouring lanes.
-__global__ __launch_bounds__(256) void prep_cols_kernel(const int32_t *__restrict__ src, int K, int N, int Kp,
-                                                        uint8_t *__restrict__ planes, size_t plane_stride,
-                                                        uint16_t *__restrict__ lo16,
-                                                        unsigned long long *__restrict__ sums) {
-    __shared__ int32_t tile[64][65];
-    const int n0 = blockIdx.x * 64, k0 = blockIdx.y * 64;
+// Row-major B[K][N] -> B^T planes [p][N][Kp], low halves [N][Kp]: one
+// 64 (k) x 64 (n) tile (rows k0.., columns 64 bx..); lane = 4 * column +
+// k-quarter so that each column's 64 plane bytes are written by four
+// neighbouring lanes.  Adds the thread's 16 values of its column into sum.
+__device__ __forceinline__ void prep_cols_tile(const int32_t *__restrict__ src, int K, int N, int Kp,
+                                               uint8_t *__restrict__ planes, size_t plane_stride,
+                                               uint16_t *__restrict__ lo16, int32_t (*tile)[65], int bx, int k0,
+                                               long long &sum) {
+    const int n0 = bx * 64;
     const int tid = threadIdx.x;
     const bool vec = ((N & 3) == 0) && ((((uintptr_t)src) & 15) == 0);
 #pragma unroll
@@ -155,12 +151,12 @@ __global__ __launch_bounds__(256) void prep_cols_kernel(const int32_t *__restric
     const int nl = wave * 16 + (lane >> 2), kq = lane & 3;
     const int n = n0 + nl, kb = k0 + kq * 16;
     uint32_t w[16];
-    long long sum = 0;
 #pragma unroll
     for (int e = 0; e < 16; ++e) {
         w[e] = (uint32_t)tile[kq * 16 + e][nl];
         sum += (int32_t)w[e];
     }
+    __syncthreads();   // the tile is refilled by the next call
     const int nv = min(max(K - kb, 0), 16);
     uint4 pl[4], lo[2];
     split16(w, nv, pl, lo);
@@ -171,9 +167,45 @@ __global__ __launch_bounds__(256) void prep_cols_kernel(const int32_t *__restric
         *(uint4 *)(lo16 + o) = lo[0];
         *(uint4 *)(lo16 + o + 8) = lo[1];
     }
+}
+
+// Column-sum partials of row-major B: at most MAX_CS per column (det_kernels.h).
+__host__ __device__ inline int q16_ktp(int Kp) { return (Kp / 64 + MAX_CS - 1) / MAX_CS; }
+__host__ __device__ inline int q16_ncs(int Kp) { return (Kp / 64 + q16_ktp(Kp) - 1) / q16_ktp(Kp); }
+
+// Both operands in one launch (the two preps are independent; each alone is
+// a few microseconds of fixed launch latency).  Blocks [0, na) split the A
+// rows.  With B given as B^T the remaining blocks split its rows the same
+// way (exact column sums, one partial).  Otherwise block na + by * nbx + bx
+// prepares the 64-row tiles [by * ktp, (by + 1) * ktp) of column strip bx and
+// writes its exact partial column sums to colsum[by][N]: the GEMM epilogue
+// adds the partials, so no atomics and no zeroed buffer are needed.
+__global__ __launch_bounds__(256) void prep_kernel(const int32_t *__restrict__ A, const int32_t *__restrict__ B,
+                                                   int M, int N, int K, int Kp, uint8_t *__restrict__ Ap,
+                                                   uint8_t *__restrict__ Bp, size_t a_plane, size_t b_plane,
+                                                   uint16_t *__restrict__ Alo, uint16_t *__restrict__ Blo,
+                                                   unsigned long long *__restrict__ rowsum,
+                                                   unsigned long long *__restrict__ colsum, int na, int b_is_t,
+                                                   int nbx, int ktp) {
+    const int blk = blockIdx.x;
+    if (blk < na) {
+        prep_rows(A, M, K, Kp, Ap, a_plane, Alo, rowsum, blk);
+        return;
+    }
+    if (b_is_t) {
+        prep_rows(B, N, K, Kp, Bp, b_plane, Blo, colsum, blk - na);
+        return;
+    }
+    __shared__ int32_t tile[64][65];
+    const int t = blk - na, bx = t % nbx, by = t / nbx;
+    const int kt_end = min((by + 1) * ktp, Kp / 64);
+    long long sum = 0;
+    for (int kt = by * ktp; kt < kt_end; ++kt) prep_cols_tile(B, K, N, Kp, Bp, b_plane, Blo, tile, bx, kt * 64, sum);
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int n = bx * 64 + wave * 16 + (lane >> 2);
     sum += __shfl_xor(sum, 1);
     sum += __shfl_xor(sum, 2);
-    if (kq == 0 && n < N) atomicAdd(sums + n, (unsigned long long)sum);
+    if ((lane & 3) == 0 && n < N) colsum[(size_t)by * N + n] = (unsigned long long)sum;
 }
 
 // ------------------------------------------------------------------ main
@@ -212,7 +244,7 @@ constexpr int RP_STRIDE = 72;
 // traffic proceed beside it.
 __global__ __launch_bounds__(THREADS, 1) void q16x_kernel(
     const uint8_t *__restrict__ ws, Q16xWs L,
-    const unsigned long long *__restrict__ rowsum, const unsigned long long *__restrict__ colsum,
+    const unsigned long long *__restrict__ rowsum, const unsigned long long *__restrict__ colsum, int ncs,
     int32_t *__restrict__ C, int M, int N, int Kp, int tiles_m, int tiles_n, unsigned long long kc2) {
     __shared__ __attribute__((aligned(1024))) uint8_t smem[NST * STAGE];
 
@@ -233,6 +265,14 @@ __global__ __launch_bounds__(THREADS, 1) void q16x_kernel(
     if (wave < 4) {
         // ------------------------------------------------ limb waves
         const int qm = wave >> 1, qn = wave & 1;
+        // this lane's column-sum partials for the epilogue, loaded now and
+        // held in registers so their latency hides behind the K loop
+        unsigned long long cs_part[MAX_CS];
+        {
+            const int cc = min(n0 + qn * 32 + (lane & 31), N - 1);
+#pragma unroll
+            for (int i = 0; i < MAX_CS; ++i) cs_part[i] = colsum[(size_t)min(i, ncs - 1) * N + cc];
+        }
         // DMA: a stage is 48 blocks of 1 KiB (A planes 0..15, B planes
         // 16..31, A low halves 32..39, B low halves 40..47); limb wave w
         // issues blocks 12w .. 12w+11.  Lane i of a block fills LDS slot i,
@@ -304,7 +344,10 @@ __global__ __launch_bounds__(THREADS, 1) void q16x_kernel(
         const int col_l = qn * 32 + (lane & 31);
         const int col = n0 + col_l;
         const unsigned long long c = 0x808080ull;
-        const unsigned long long cb = col < N ? colsum[col] : 0ull;
+        // the ncs partial column sums [ncs][N] (loaded at the start)
+        unsigned long long cb = 0;
+#pragma unroll
+        for (int i = 0; i < MAX_CS; ++i) cb += i < ncs ? cs_part[i] : 0ull;
 #pragma unroll
         for (int r = 0; r < 16; ++r) {
             const int row_l = qm * 32 + 8 * (r >> 2) + 4 * fh + (r & 3);
@@ -387,9 +430,15 @@ bool q16x_eligible(int M, int N, int K) {
     return K >= 1 && K < 65536 && 6LL * ((long long)M + N) * Kp < (1LL << 31);
 }
 
-// Workspace layout (same size as limb_workspace_bytes(M, N, K, 4, true)):
-// A planes [4][M][Kp], B^T planes [4][N][Kp], A low halves [M][Kp] u16,
-// B low halves [N][Kp] u16, row sums [M] u64, column sums [N] u64.
+// Workspace layout: A planes [4][M][Kp], B^T planes [4][N][Kp], A low
+// halves [M][Kp] u16, B low halves [N][Kp] u16, row sums [M] u64, column-sum
+// partials [ncs][N] u64 (ncs <= MAX_CS).
+size_t q16x_workspace_bytes(int M, int N, int K) {
+    const size_t Kp = (size_t)((K + q16x::KP_ALIGN - 1) / q16x::KP_ALIGN) * q16x::KP_ALIGN;
+    const size_t b = 6 * ((size_t)M + N) * Kp + 8 * ((size_t)M + (size_t)q16x::q16_ncs((int)Kp) * N);
+    return (b + 255) & ~(size_t)255;
+}
+
 hipError_t launch_gemm_q16x(const int32_t *A, const int32_t *B, int32_t *C, int M, int N, int K, bool b_is_t,
                             void *ws, hipStream_t s) {
     using namespace q16x;
@@ -402,17 +451,11 @@ hipError_t launch_gemm_q16x(const int32_t *A, const int32_t *B, int32_t *C, int 
     unsigned long long *rowsum = (unsigned long long *)(Blo + b_plane);
     unsigned long long *colsum = rowsum + M;
 
-    if (b_is_t) {
-        hipLaunchKernelGGL(prep_rows_kernel, dim3((M + 3) / 4), dim3(256), 0, s, A, M, K, Kp, Ap, a_plane, Alo,
-                           rowsum, colsum, 0);
-        hipLaunchKernelGGL(prep_rows_kernel, dim3((N + 3) / 4), dim3(256), 0, s, B, N, K, Kp, Bp, b_plane, Blo,
-                           colsum, rowsum, 0);
-    } else {
-        hipLaunchKernelGGL(prep_rows_kernel, dim3((M + 3) / 4), dim3(256), 0, s, A, M, K, Kp, Ap, a_plane, Alo,
-                           rowsum, colsum, N);
-        hipLaunchKernelGGL(prep_cols_kernel, dim3((N + 63) / 64, Kp / 64), dim3(256), 0, s, B, K, N, Kp, Bp,
-                           b_plane, Blo, colsum);
-    }
+    const int na = (M + 3) / 4, nbx = (N + 63) / 64, ktp = q16_ktp(Kp);
+    const int ncs = b_is_t ? 1 : q16_ncs(Kp);
+    const int nb = b_is_t ? (N + 3) / 4 : nbx * ncs;
+    hipLaunchKernelGGL(prep_kernel, dim3(na + nb), dim3(256), 0, s, A, B, M, N, K, Kp, Ap, Bp, a_plane, b_plane,
+                       Alo, Blo, rowsum, colsum, na, (int)b_is_t, nbx, ktp);
     const int tiles_m = (M + BM - 1) / BM, tiles_n = (N + BN - 1) / BN;
     const unsigned long long kc2 = (unsigned long long)K * 0x808080ull * 0x808080ull;
     Q16xWs L;
@@ -422,8 +465,8 @@ hipError_t launch_gemm_q16x(const int32_t *A, const int32_t *B, int32_t *C, int 
     L.alo = (uint32_t)((uint8_t *)Alo - Ap);
     L.blo = (uint32_t)((uint8_t *)Blo - Ap);
     L.bytes = (uint32_t)((uint8_t *)(Blo + b_plane) - Ap);
-    hipLaunchKernelGGL(q16x_kernel, dim3(tiles_m * tiles_n), dim3(THREADS), 0, s, Ap, L, rowsum, colsum, C, M, N,
-                       Kp, tiles_m, tiles_n, kc2);
+    hipLaunchKernelGGL(q16x_kernel, dim3(tiles_m * tiles_n), dim3(THREADS), 0, s, Ap, L, rowsum, colsum, ncs, C,
+                       M, N, Kp, tiles_m, tiles_n, kc2);
     return hipGetLastError();
 }
 

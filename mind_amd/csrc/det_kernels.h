@@ -10,20 +10,28 @@
 
 namespace det {
 
+// The int16 and Q16 preps write column sums of B as at most MAX_CS exact
+// partials per column ([ncs][N], ncs <= MAX_CS); the GEMM epilogues add them.
+constexpr int MAX_CS = 16;
+
 // C[M,N] (i32) = A[M,K] (i8) * B[K,N] (i8)
 hipError_t launch_gemm_i8(const int8_t *A, const int8_t *B, int32_t *C, int M, int N, int K, hipStream_t s);
 
 // Workspace (device bytes) the limb GEMMs need: operand limb planes, low-16
 // halves (Q16) and exact row / column sums.
 size_t limb_workspace_bytes(int M, int N, int K, int np, bool q16);
-inline size_t q16_workspace_bytes(int M, int N, int K) { return limb_workspace_bytes(M, N, K, 4, true); }
+size_t q16x_workspace_bytes(int M, int N, int K);   // the second-generation Q16 kernel's layout
+inline size_t q16_workspace_bytes(int M, int N, int K) {
+    const size_t a = limb_workspace_bytes(M, N, K, 4, true), b = q16x_workspace_bytes(M, N, K);
+    return a > b ? a : b;
+}
 size_t i16_workspace_bytes(int M, int N, int K);   // covers both int16 paths below
 
 // Q16.16: B is [K][N], or [N][K] when b_is_t.
 hipError_t launch_gemm_q16(const int32_t *A, const int32_t *B, int32_t *C, int M, int N, int K, bool b_is_t,
                            void *ws, hipStream_t s);
 // Second-generation Q16 kernel (8 waves per tile, no flush): K <= 65536 and
-// 4 * max(M, N) * Kp < 2^31.  Same workspace as q16_workspace_bytes.
+// 4 * max(M, N) * Kp < 2^31.  Its workspace is covered by q16_workspace_bytes.
 bool q16x_eligible(int M, int N, int K);
 hipError_t launch_gemm_q16x(const int32_t *A, const int32_t *B, int32_t *C, int M, int N, int K, bool b_is_t,
                             void *ws, hipStream_t s);
