@@ -1,5 +1,5 @@
 // det_gemm_q16x.hip -- Q16.16 GEMM for K < 65536: limb-plane int8 MFMA for
-// the bilinear part, VALU residue for the per-term floor, 8 waves per tile.
+// the bilinear part, VALU residue for the per-term floor, 12 waves per tile.
 //
 // Semantics (reference src/mlir/lowering.rs:9300-9410, 7074-7676, oracle
 // benches/det_matmul_q16.rs:227-240):
@@ -14,22 +14,24 @@
 //    B^T), and transposing 64x64 tiles for row-major B.  Both write the limb
 //    planes [p][rows][Kp] (K-contiguous, biased bytes), the low-16 halves
 //    [rows][Kp] and exact int64 row sums / column-sum partials (no atomics).
-//  * Main kernel: 64x64 output tile per 512-thread workgroup, 48 KiB LDS
+//  * Main kernel: 64x64 output tile per 768-thread workgroup, 48 KiB LDS
 //    stages (limb planes + low halves of A and B for 64 k) filled by
 //    direct global->LDS DMA two steps ahead (3 stages).  The waves are
 //    specialised: on each SIMD one "limb wave" runs the 15 limb-pair
 //    v_mfma_i32_32x32x32_i8 of a 32x32 quadrant (six shift-set
-//    accumulators) and issues the DMA, and one "residue wave" computes R for
-//    the whole tile over a quarter of each K step with an 8x8 output
-//    micro-tile per lane (0.5 LDS bytes per residue term).  On gfx950 an
-//    MFMA and a VALU operation of another wave on the same SIMD do not
-//    execute concurrently (measured), so the kernel is bounded by MFMA time
-//    plus residue VALU time per SIMD; the specialisation keeps each wave's
-//    instruction stream dense and the residue LDS traffic low.
+//    accumulators) and issues the DMA, and two "residue waves" compute R
+//    for the whole tile, each over an eighth of each K step, with an 8x8
+//    output micro-tile per lane (0.5 LDS bytes per residue term).  On
+//    gfx950 an MFMA and a VALU operation of another wave on the same SIMD do
+//    not execute concurrently (measured), so the kernel is bounded by MFMA
+//    time plus residue VALU time per SIMD; the specialisation keeps each
+//    wave's instruction stream dense and the residue LDS traffic low, and two
+//    residue waves per SIMD issue VALU faster than one (a single wave waits
+//    between its own instructions: 9-10% fewer cycles per tile with two).
 //  * Exactness: the limb waves cover the whole K, so the shift-0 set is
 //    bounded by K 2^14 and the shift-1 set by K 2^15 (exact in int32 for
-//    K < 2^16); each residue wave's partial is below (K/4) 2^16 and the sum
-//    of the four below K 2^16 < 2^32.  Sets with shift >= 2 only need their
+//    K < 2^16); each residue wave's partial is below (K/8) 2^16 and the sum
+//    of the eight below K 2^16 < 2^32.  Sets with shift >= 2 only need their
 //    value mod 2^32.  The epilogue combines S, R and the bias terms in
 //    uint64 and keeps bits 16..47.
 #include "det_common.h"
@@ -39,7 +41,7 @@ namespace det {
 namespace q16x {
 
 constexpr int KP_ALIGN = 64;
-constexpr int BM = 64, BN = 64, BK = 64, THREADS = 512;
+constexpr int BM = 64, BN = 64, BK = 64, THREADS = 768;
 constexpr int PT = BM * BK;             // bytes per limb-plane tile
 constexpr int LT = BM * BK * 2;         // bytes per low-16 tile
 constexpr int STAGE = 8 * PT + 2 * LT;  // A and B: 4 planes + low halves
@@ -227,18 +229,20 @@ struct Q16xWs {
     uint32_t bytes;              // total bytes of the four regions
 };
 
-// Residue partials in the epilogue: [4 K quarters][64 lanes][RP_STRIDE] u32
-// (a lane's 8x8 block at i*8 + j; the stride makes both the dump and the
-// MFMA-layout gather conflict-light).
+// Residue partials in the epilogue: [4][64 lanes][RP_STRIDE] u32 (a lane's
+// 8x8 block at i*8 + j; the stride makes both the dump and the MFMA-layout
+// gather conflict-light).  Residue waves 4..7 write their partials, then
+// waves 8..11 add theirs into the same slots (wave w+4 onto wave w).
 constexpr int RP_STRIDE = 72;
 
-// Wave roles (one of each per SIMD; waves w and w+4 share SIMD w):
+// Wave roles (waves w, w+4 and w+8 share SIMD w % 4):
 //  * waves 0..3 ("limb waves"): 32x32 quadrant w of the tile over the whole
 //    K: the 15 limb-pair MFMAs (shift sets s = p+q in six accumulators) and
 //    all of the DMA (12 loads per stage each).
-//  * waves 4..7 ("residue waves"): the whole 64x64 tile over K quarter w-4
-//    of every step: an 8x8 micro-tile per lane (rows 8*ly+i, columns
-//    8*lx+j), 16 LDS reads of 8 bytes per 256 VALU operations.
+//  * waves 4..11 ("residue waves"): the whole 64x64 tile over K eighth w-4
+//    of every step (one 8-k chunk): an 8x8 micro-tile per lane (rows
+//    8*ly+i, columns 8*lx+j), 16 LDS reads of 8 bytes per 256 VALU
+//    operations.
 // The residue is VALU work that no MFMA can do; giving it whole waves lets
 // the SIMD issue it back to back while the limb wave's MFMAs and LDS
 // traffic proceed beside it.
@@ -265,14 +269,6 @@ __global__ __launch_bounds__(THREADS, 1) void q16x_kernel(
     if (wave < 4) {
         // ------------------------------------------------ limb waves
         const int qm = wave >> 1, qn = wave & 1;
-        // this lane's column-sum partials for the epilogue, loaded now and
-        // held in registers so their latency hides behind the K loop
-        unsigned long long cs_part[MAX_CS];
-        {
-            const int cc = min(n0 + qn * 32 + (lane & 31), N - 1);
-#pragma unroll
-            for (int i = 0; i < MAX_CS; ++i) cs_part[i] = colsum[(size_t)min(i, ncs - 1) * N + cc];
-        }
         // DMA: a stage is 48 blocks of 1 KiB (A planes 0..15, B planes
         // 16..31, A low halves 32..39, B low halves 40..47); limb wave w
         // issues blocks 12w .. 12w+11.  Lane i of a block fills LDS slot i,
@@ -337,8 +333,17 @@ __global__ __launch_bounds__(THREADS, 1) void q16x_kernel(
             __builtin_amdgcn_s_barrier();
         }
         DET_WAIT_VMCNT(0);     // no load past the end may still write LDS
+        // this lane's column-sum partials for the epilogue: loaded now, so
+        // their latency overlaps the residue waves' partial exchange
+        unsigned long long cs_part[MAX_CS];
+        {
+            const int cc = min(n0 + qn * 32 + (lane & 31), N - 1);
+#pragma unroll
+            for (int i = 0; i < MAX_CS; ++i) cs_part[i] = colsum[(size_t)min(i, ncs - 1) * N + cc];
+        }
         __syncthreads();       // stages free
-        __syncthreads();       // residue partials written
+        __syncthreads();       // residue partials of waves 4..7 written
+        __syncthreads();       // waves 8..11 added theirs
         // combine in the MFMA layout: lane l, element r -> row 8(r>>2) +
         // 4(l>>5) + (r&3), column l&31 of the quadrant
         const int col_l = qn * 32 + (lane & 31);
@@ -375,11 +380,10 @@ __global__ __launch_bounds__(THREADS, 1) void q16x_kernel(
         __builtin_amdgcn_s_barrier();   // step 0 landed
         for (int kt = 0; kt < nk; ++kt) {
             const uint8_t *sal = smem + (kt % NST) * STAGE + 8 * PT, *sbl = sal + LT;
-            // sub-chunk sc (4 k) of this wave's quarter: chunk 2*kq + (sc>>1),
-            // 8-byte half (sc & 1); reads run one sub-chunk ahead
+            // sub-chunk sc (4 k) of this wave's eighth: chunk kq, 8-byte half sc
             uint2 av[2][8], bv[2][8];
             auto rload = [&](int sc, uint2 (&a)[8], uint2 (&b)[8]) {
-                const int ch = 2 * kq + (sc >> 1), half = (sc & 1) * 8;
+                const int ch = kq, half = sc * 8;
 #pragma unroll
                 for (int i = 0; i < 8; ++i) {
                     a[i] = *(const uint2 *)(sal + swz_lo(8 * ly + i, ch) + half);
@@ -388,8 +392,8 @@ __global__ __launch_bounds__(THREADS, 1) void q16x_kernel(
             };
             rload(0, av[0], bv[0]);
 #pragma unroll
-            for (int sc = 0; sc < 4; ++sc) {
-                if (sc < 3) rload(sc + 1, av[(sc + 1) & 1], bv[(sc + 1) & 1]);
+            for (int sc = 0; sc < 2; ++sc) {
+                if (sc < 1) rload(sc + 1, av[(sc + 1) & 1], bv[(sc + 1) & 1]);
                 const uint2(&a)[8] = av[sc & 1];
                 const uint2(&b)[8] = bv[sc & 1];
 #pragma unroll
@@ -413,13 +417,26 @@ __global__ __launch_bounds__(THREADS, 1) void q16x_kernel(
             __builtin_amdgcn_s_barrier();
         }
         __syncthreads();       // stages free (matches the limb waves)
-        uint32_t *dst = sR + (kq * 64 + lane) * RP_STRIDE;
+        uint32_t *dst = sR + ((kq & 3) * 64 + lane) * RP_STRIDE;
+        if (kq < 4) {
 #pragma unroll
-        for (int i = 0; i < 8; ++i) {
-            *(uint4 *)(dst + i * 8) = make_uint4(racc[i][0], racc[i][1], racc[i][2], racc[i][3]);
-            *(uint4 *)(dst + i * 8 + 4) = make_uint4(racc[i][4], racc[i][5], racc[i][6], racc[i][7]);
+            for (int i = 0; i < 8; ++i) {
+                *(uint4 *)(dst + i * 8) = make_uint4(racc[i][0], racc[i][1], racc[i][2], racc[i][3]);
+                *(uint4 *)(dst + i * 8 + 4) = make_uint4(racc[i][4], racc[i][5], racc[i][6], racc[i][7]);
+            }
         }
-        __syncthreads();       // residue partials written
+        __syncthreads();       // partials of waves 4..7 written
+        if (kq >= 4) {
+#pragma unroll
+            for (int i = 0; i < 8; ++i)
+#pragma unroll
+                for (int h = 0; h < 2; ++h) {
+                    uint4 v = *(uint4 *)(dst + i * 8 + 4 * h);
+                    v.x += racc[i][4 * h]; v.y += racc[i][4 * h + 1]; v.z += racc[i][4 * h + 2]; v.w += racc[i][4 * h + 3];
+                    *(uint4 *)(dst + i * 8 + 4 * h) = v;
+                }
+        }
+        __syncthreads();       // waves 8..11 added theirs
     }
 }
 
