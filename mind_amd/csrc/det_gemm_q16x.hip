@@ -129,24 +129,32 @@ __device__ __forceinline__ void prep_cols_tile(const int32_t *__restrict__ src, 
                                                long long &sum) {
     const int n0 = bx * 64;
     const int tid = threadIdx.x;
-    const bool vec = ((N & 3) == 0) && ((((uintptr_t)src) & 15) == 0);
+    const int c = (tid & 15) * 4;
+    uint4 v[4];
+    if (((N & 3) == 0) && ((((uintptr_t)src) & 15) == 0) && n0 + 64 <= N && k0 + 64 <= K) {
+        // block-uniform: the whole tile inside B with 16-byte rows; the four
+        // loads of a thread are all in flight before any is used
+#pragma unroll
+        for (int pass = 0; pass < 4; ++pass)
+            v[pass] = *(const uint4 *)(src + (size_t)(k0 + (tid >> 4) + 16 * pass) * N + n0 + c);
+    } else {
+#pragma unroll
+        for (int pass = 0; pass < 4; ++pass) {
+            const int k = k0 + (tid >> 4) + 16 * pass, n = n0 + c;
+            const int32_t *p = src + (size_t)k * N + n;
+            uint32_t w[4];
+#pragma unroll
+            for (int e = 0; e < 4; ++e) w[e] = k < K && n + e < N ? (uint32_t)p[e] : 0u;
+            v[pass] = make_uint4(w[0], w[1], w[2], w[3]);
+        }
+    }
 #pragma unroll
     for (int pass = 0; pass < 4; ++pass) {
-        const int kr = (tid >> 4) + 16 * pass, c = (tid & 15) * 4;
-        const int k = k0 + kr, n = n0 + c;
-        uint32_t v[4] = {0, 0, 0, 0};
-        if (k < K) {
-            const int32_t *p = src + (size_t)k * N + n;
-            if (vec && n + 4 <= N) {
-                const uint4 q = *(const uint4 *)p;
-                v[0] = q.x, v[1] = q.y, v[2] = q.z, v[3] = q.w;
-            } else {
-#pragma unroll
-                for (int e = 0; e < 4; ++e) v[e] = n + e < N ? (uint32_t)p[e] : 0u;
-            }
-        }
-#pragma unroll
-        for (int e = 0; e < 4; ++e) tile[kr][c + e] = (int32_t)v[e];
+        const int kr = (tid >> 4) + 16 * pass;
+        tile[kr][c + 0] = (int32_t)v[pass].x;
+        tile[kr][c + 1] = (int32_t)v[pass].y;
+        tile[kr][c + 2] = (int32_t)v[pass].z;
+        tile[kr][c + 3] = (int32_t)v[pass].w;
     }
     __syncthreads();
     const int lane = tid & 63, wave = tid >> 6;
