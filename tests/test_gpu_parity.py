@@ -725,6 +725,33 @@ def test_dev_api_poisoned_outputs_and_run_to_run():
     s.destroy()
 
 
+@pytest.mark.parametrize("op,m,k,n", [("i16", 64, 5000, 96), ("i16", 300, 1000, 270), ("q16", 64, 3000, 100),
+                                      ("q16", 130, 4096, 70)])
+def test_ws_dev_exact_workspace_with_garbage(op, m, k, n):
+    # the exact reported workspace, refilled with garbage before every call:
+    # the preps write every column-sum partial they later read (several
+    # 64-row B tiles per partial at these K), nothing relies on zeroed memory
+    if op == "i16":
+        a, b = O.gen_i16(0x6A5 ^ k, m * k, k * n)
+        want, code, dt = O.gemm_i16(a, b, m, k, n), M.DET_OP_I16, np.int16
+    else:
+        a, b = O.gen_q16_sat(0x6A6 ^ k, m * k, k * n)
+        want, code, dt = O.gemm_q16(a, b, m, k, n), M.DET_OP_Q16, np.int32
+    ws_bytes = M.lib().det_workspace_bytes(code, m, k, n)
+    assert ws_bytes > 0
+    da, db = M.DeviceBuffer.from_array(a.astype(dt)), M.DeviceBuffer.from_array(b.astype(dt))
+    dc, ws = M.DeviceBuffer(m * n * 4), M.DeviceBuffer(ws_bytes)
+    s = M.Stream()
+    for rep, fill in enumerate((0xA5, 0x00, 0xFF)):
+        ws.fill(fill)
+        dc.fill(0x5A)
+        note(f"det_matmul_ws_dev {op} {m}x{k}x{n} rep={rep}")
+        M.check(M.lib().det_matmul_ws_dev(code, da.ptr, db.ptr, dc.ptr, m, k, n, ws.ptr, ws_bytes, s.ptr))
+        s.sync()
+        np.testing.assert_array_equal(dc.to_array(np.int32, (m, n)), want.reshape(m, n))
+    s.destroy()
+
+
 def test_invalid_shapes_are_rejected_before_launch():
     c = np.zeros(4, np.int32)
     a = np.zeros(4, np.int8)
