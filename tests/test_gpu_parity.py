@@ -840,3 +840,66 @@ def test_config_gemv_q16_16384(nb):
     else:
         rows = _sample_rows(m, 64)
         np.testing.assert_array_equal(Y[:, rows], O.gemv_q16_rows(W, X, m, k, nb, rows))
+
+
+# ------------------------------------------------------------------ operands beyond 2 GiB
+# The fast paths address operands through 32-bit buffer offsets and are
+# chosen only below 2^31 bytes; a larger operand must take the generic
+# (64-bit addressed) variant of the same computation.  One operand of each
+# of these calls is 2.5 GiB; outputs are checked on rows sampled across it.
+
+BIG_M = 40960           # x 16384 x 4 bytes = 2.5 GiB of Q16 W / f32 W
+
+
+def _rows_spread(m, count=12):
+    rows = _sample_rows(m, count)
+    return np.unique(np.r_[rows, m // 2, (1 << 31) // (4 * 16384) - 1, (1 << 31) // (4 * 16384)])
+
+
+def test_big_gemv_q16_batch1_and_8():
+    m, k = BIG_M, 16384
+    W, X = M.gen_q16(0xB16 ^ 1, m * k, 8 * k, 15)
+    assert W.nbytes > (1 << 31)
+    rows = _rows_spread(m)
+    for nb in (1, 8):
+        note(f"det_gemv_q16_dev {m}x{k} nb={nb} (W {W.nbytes >> 20} MiB)")
+        Y = _dev_run(lambda pw, px, py, s: M.lib().det_gemv_q16_dev(pw, px, py, m, k, nb, s), [W, X[:nb * k]],
+                     (nb, m), reps=1)
+        np.testing.assert_array_equal(Y[:, rows], O.gemv_q16_rows(W, X[:nb * k], m, k, nb, rows))
+
+
+def test_big_gemm_i8():
+    m, k, n = 65536, 40960, 48            # A = 2.5 GiB
+    A, B = M.gen_i8(0xB16 ^ 2, m * k, k * n)
+    assert A.nbytes > (1 << 31)
+    note(f"det_matmul_i8_dev {m}x{k}x{n} (A {A.nbytes >> 20} MiB)")
+    C = _dev_run(lambda pa, pb, pc, s: M.lib().det_matmul_i8_dev(pa, pb, pc, m, k, n, s), [A, B], (m, n), reps=1)
+    rows = np.unique(np.r_[_sample_rows(m, 12), (1 << 31) // k - 1, (1 << 31) // k])
+    np.testing.assert_array_equal(C[rows], O.gemm_i8_rows(A, B, m, k, n, rows))
+
+
+def test_big_gemm_q16_limb_path():
+    m, k, n = BIG_M, 16384, 64            # A = 2.5 GiB: beyond the second-generation kernel's limit
+    A, B = M.gen_q16(0xB16 ^ 3, m * k, k * n, 13)
+    assert A.nbytes > (1 << 31)
+    note(f"det_matmul_q16_dev {m}x{k}x{n} (A {A.nbytes >> 20} MiB)")
+    C = _dev_run(lambda pa, pb, pc, s: M.lib().det_matmul_q16_dev(pa, pb, pc, m, k, n, s), [A, B], (m, n), reps=1)
+    rows = _rows_spread(m)
+    np.testing.assert_array_equal(C[rows], O.gemm_q16_rows(A, B, m, k, n, rows))
+
+
+def test_big_matmul_rmajor_f32():
+    rows_n, cols = BIG_M, 16384           # W = 2.5 GiB
+    W, x = M.gen_f32_unit(0xB16 ^ 4, rows_n * cols, cols)
+    assert W.nbytes > (1 << 31)
+    note(f"det_matmul_rmajor_f32_dev {rows_n}x{cols} (W {W.nbytes >> 20} MiB)")
+    dW, dx, dy = M.DeviceBuffer.from_array(W), M.DeviceBuffer.from_array(x), M.DeviceBuffer(rows_n * 4)
+    s = M.Stream()
+    dy.fill(0xA5)
+    M.check(M.lib().det_matmul_rmajor_f32_dev(dW.ptr, dx.ptr, dy.ptr, rows_n, cols, s.ptr))
+    s.sync()
+    y = dy.to_array(np.float32, (rows_n,))
+    for r in _rows_spread(rows_n):
+        want = O.matmul_rmajor_f32(W[r * cols:(r + 1) * cols], x, 1, cols)[0]
+        assert y[r].view(np.uint32) == np.float32(want).view(np.uint32), r
+    s.destroy()
