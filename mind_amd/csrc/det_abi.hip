@@ -231,7 +231,11 @@ int64_t gemv_host(bool q16, int64_t w, int64_t x, int64_t y, int64_t m, int64_t 
         const int32_t *dW = (const int32_t *)io, *dX = (const int32_t *)(io + off_x);
         const size_t need = gemv_ws_need(dW, dX, m, k, nb);
         if ((rc = ensure(&ds.ws, &ds.ws_bytes, need))) return rc;
+        // the workspace arena is shared with the device-pointer entry points
+        // (other streams): start after its last user, then mark this stream
+        if (need) DET_HIP_CHECK(hipStreamWaitEvent(s, ds.ws_free, 0));
         DET_HIP_CHECK(gemv_q16_any(dW, dX, (int32_t *)(io + off_y), m, k, nb, need ? ds.ws : nullptr, s));
+        if (need) DET_HIP_CHECK(hipEventRecord(ds.ws_free, s));
     } else
         DET_HIP_CHECK(det::launch_gemv_i16((const int16_t *)io, (const int16_t *)(io + off_x),
                                            (int32_t *)(io + off_y), (int)m, (int)k, s));

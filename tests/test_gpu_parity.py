@@ -553,6 +553,33 @@ def test_device_arena_shared_by_two_streams():
         dA.free(); dB.free(); dC.free()
 
 
+def test_host_batched_gemv_orders_itself_after_device_arena_users():
+    # A device-pointer Q16 GEMM queued on a caller stream holds the workspace
+    # arena; a host-pointer batched GEMV called right after it (its MFMA path
+    # stages the query planes in the same arena) must wait for it: both
+    # results must equal the oracle's
+    L = M.lib()
+    m, k, n = 1024, 2048, 1024
+    a, b = O.gen_q16(0xA7E, m * k, k * n, shift=13)
+    rows = _sample_rows(m, 8)
+    want_c = O.gemm_q16_rows(a, b, m, k, n, rows)
+    gm, gk, nb = 4096, 4096, 8
+    W, X = O.gen_q16(0xA7F, gm * gk, nb * gk, shift=15)
+    want_y = O.gemv_q16_batched(W, X, gm, gk, nb)
+    dA, dB, dC = M.DeviceBuffer.from_array(a), M.DeviceBuffer.from_array(b), M.DeviceBuffer(m * n * 4)
+    s = M.Stream()
+    for rep in range(3):
+        dC.fill(0x33)
+        note(f"det_matmul_q16_dev {m}x{k}x{n} then host gemv nb={nb}, rep {rep}")
+        M.check(L.det_matmul_q16_dev(dA.ptr, dB.ptr, dC.ptr, m, k, n, s.ptr))
+        y = M.det_gemv_q16(W.reshape(gm, gk), X.reshape(nb, gk))
+        s.sync()
+        np.testing.assert_array_equal(dC.to_array(np.int32, (m, n))[rows], want_c)
+        np.testing.assert_array_equal(y, want_y)
+    s.destroy()
+    dA.free(); dB.free(); dC.free()
+
+
 # ------------------------------------------------------------------ int8 shapes
 
 I8_SHAPES = [(1, 1, 1), (1, 64, 1), (3, 5, 7), (16, 16, 16), (17, 33, 65), (64, 64, 64), (255, 257, 129),
