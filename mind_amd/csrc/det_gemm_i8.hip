@@ -246,17 +246,11 @@ __global__ __launch_bounds__(THREADS, 1) void gemm_i8_kernel(const int8_t *__res
 // OOB_OFFSET and land in LDS as zeros.  NSTAGE LDS stages; each wave issues
 // 2 A blocks + 2 B blocks (4 instructions) per stage.
 //
-// Per iteration kt (fragments p0 = first half of step kt already read):
-//   read p1 (second half of step kt);  MFMAs on p0;
-//   wait until this wave's loads of step kt+1 landed, then s_barrier
-//   (every wave's loads of step kt+1 are in LDS, and every wave finished
-//   iteration kt-1, so buffer (kt-1) % NSTAGE is free);
-//   issue step kt-1+NSTAGE into that buffer;
-//   read p0 of step kt+1;  MFMAs on p1.
-// The wait is explicit (s_waitcnt vmcnt) and the barrier is a bare
-// s_barrier: the loads of later steps stay in flight across it.  (This is
-// the schedule of the edge-tile path; full tiles use the ping-pong schedule
-// described at the FULL loop.)
+// Both the full-tile and the edge-tile loop use the ping-pong schedule
+// described at the full-tile loop: the two waves of each SIMD alternate an
+// MFMA phase and an LDS-read / DMA-issue phase, with explicit s_waitcnt
+// vmcnt waits and bare s_barrier so the loads of later steps stay in flight
+// across the barriers.
 constexpr int NSTAGE = 4;
 constexpr int DMA_PER_STAGE = 4;     // instructions per wave per stage
 
@@ -479,26 +473,53 @@ __global__ __launch_bounds__(THREADS, 1) void gemm_i8_dma_kernel(const int8_t *_
         // be writing LDS when the workgroup ends
         DET_WAIT_VMCNT(0);
     } else {
+    // The ping-pong schedule of the full-tile path (see there for the slot
+    // structure and why every stage reuse and wait is safe), with run-time
+    // stage indices, bounds-checked DMA and any number of K steps.
+    static_assert(NSTAGE == 4, "the schedule below assumes 4 stages");
 #pragma unroll
     for (int st = 0; st < NSTAGE - 1; ++st) issue(st, st * BK);
-    DET_WAIT_VMCNT(DMA_PER_STAGE * (NSTAGE - 2));   // step 0 landed
+    DET_WAIT_VMCNT(DMA_PER_STAGE * 2);   // step 0 landed
     __builtin_amdgcn_s_barrier();
-    Ops p0, p1;
-    read_ops(p0, 0, 0);
-    for (int kt = 0; kt < nk; ++kt) {
-        const int cur = kt % NSTAGE, nxt = (kt + 1) % NSTAGE;
-        read_ops(p1, cur, 1);
-        mma(p0);
-        // loads of steps kt+1 .. kt+NSTAGE-2 are outstanding; the oldest
-        // (kt+1) must have landed
-        DET_WAIT_VMCNT(DMA_PER_STAGE * (NSTAGE - 3));
-        __builtin_amdgcn_s_waitcnt(0xc07f & ~(15 << 8));   // lgkmcnt(0): this wave's reads done
+    Ops q0, q1;
+    auto mem = [&](int s) {
+        const int st = s % NSTAGE;
+        read_ops(q0, st, 0);
+        read_ops(q1, st, 1);
+        issue((s + 3) % NSTAGE, (s + 3) * BK);
+    };
+    auto lgkm0 = [&]() { __builtin_amdgcn_s_waitcnt(0xc07f & ~(15 << 8)); };
+    if (wave < 4) {
+        mem(0);
+        lgkm0();
         __builtin_amdgcn_s_barrier();
-        issue((kt + NSTAGE - 1) % NSTAGE, (kt + NSTAGE - 1) * BK);
-        __builtin_amdgcn_sched_barrier(0);
-        read_ops(p0, nxt, 0);
-        mma(p1);
-        __builtin_amdgcn_sched_barrier(0);
+        for (int kt = 0; kt < nk; ++kt) {
+            __builtin_amdgcn_sched_barrier(0);
+            mma(q0);
+            mma(q1);
+            __builtin_amdgcn_sched_barrier(0);
+            DET_WAIT_VMCNT(DMA_PER_STAGE * 2);
+            __builtin_amdgcn_s_barrier();
+            __builtin_amdgcn_sched_barrier(0);
+            if (kt + 1 < nk) mem(kt + 1);
+            lgkm0();
+            __builtin_amdgcn_sched_barrier(0);
+            __builtin_amdgcn_s_barrier();
+        }
+    } else {
+        __builtin_amdgcn_s_barrier();
+        for (int kt = 0; kt < nk; ++kt) {
+            __builtin_amdgcn_sched_barrier(0);
+            mem(kt);
+            DET_WAIT_VMCNT(DMA_PER_STAGE * 2);
+            lgkm0();
+            __builtin_amdgcn_s_barrier();
+            __builtin_amdgcn_sched_barrier(0);
+            mma(q0);
+            mma(q1);
+            __builtin_amdgcn_sched_barrier(0);
+            __builtin_amdgcn_s_barrier();
+        }
     }
     // the loads issued past the end of K are zero fills; none may still be
     // writing LDS when the workgroup ends
