@@ -645,7 +645,7 @@ int64_t det_device_info(int64_t *info, char *name, int64_t name_len) {
         info[5] = p.memoryBusWidth;
     }
     if (name && name_len > 0) {
-        std::string s = std::string(p.name) + " " + p.gcnArchName;
+        std::string s = p.name[0] ? std::string(p.name) + " " + p.gcnArchName : std::string(p.gcnArchName);
         size_t l = s.size() < (size_t)name_len - 1 ? s.size() : (size_t)name_len - 1;
         memcpy(name, s.data(), l);
         name[l] = 0;
