@@ -48,7 +48,7 @@ hipError_t launch_gemm_i16x(const int16_t *A, const int16_t *B, int32_t *C, int 
 // Y[nb][M] = Q16 GEMV of W[M][K] with each X[b][K].
 hipError_t launch_gemv_q16(const int32_t *W, const int32_t *X, int32_t *Y, int M, int K, int nb, hipStream_t s);
 // Several query vectors at once (nb <= 8) on the int8 MFMA + VALU residue:
-// eligible when M >= 16, K % 256 == 0, K <= 32768, W < 2^31 bytes, aligned.
+// eligible when M >= 16, K % 512 == 0, K <= 32768, W < 2^31 bytes, aligned.
 bool gemv8_eligible(const int32_t *W, const int32_t *X, int M, int K);
 size_t gemv8_workspace_bytes(int K);
 hipError_t launch_gemv_q16_mfma(const int32_t *W, const int32_t *X, int32_t *Y, int M, int K, int nb, void *ws,

@@ -915,6 +915,16 @@ def test_big_gemm_q16_limb_path():
     np.testing.assert_array_equal(C[rows], O.gemm_q16_rows(A, B, m, k, n, rows))
 
 
+def test_big_gemm_i16_limb_path():
+    m, k, n = BIG_M, 32768, 48            # A = 2.5 GiB: 2 * M * K >= 2^31 rules out the interleaved-limb kernel
+    assert 2 * m * k >= 1 << 31
+    A, B = M.gen_i16(0xB16 ^ 5, m * k, k * n)
+    note(f"det_matmul_i16_dev {m}x{k}x{n} (A {A.nbytes >> 20} MiB)")
+    C = _dev_run(lambda pa, pb, pc, s: M.lib().det_matmul_i16_dev(pa, pb, pc, m, k, n, s), [A, B], (m, n), reps=1)
+    rows = np.unique(np.r_[_sample_rows(m, 12), m // 2, (1 << 30) // k - 1, (1 << 30) // k])
+    np.testing.assert_array_equal(C[rows], O.gemm_i16_rows(A, B, m, k, n, rows))
+
+
 def test_big_matmul_rmajor_f32():
     rows_n, cols = BIG_M, 16384           # W = 2.5 GiB
     W, x = M.gen_f32_unit(0xB16 ^ 4, rows_n * cols, cols)
