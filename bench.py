@@ -13,12 +13,14 @@ are timed the same way and reported under "secondary".  --vendor-ref adds,
 for context only, the vendor int8 GEMM (torch._int_mm) on the headline shape.
 
 Timing: HIP events recorded on the stream the kernels are launched on,
-around exactly K steps after W warm-up steps, with a device synchronisation
-on both sides; ms_per_step is the host wall clock over the same region.
+around exactly K steps after W warm-up steps and --settle seconds (0.5) of
+back-to-back running (the clock controller's transient ends within that),
+with a device synchronisation on both sides; ms_per_step is the host wall
+clock over the same region.
 Every timed output is checked bit-exact against the CPU oracle (sampled rows
 at these sizes) before its number is reported.
 
-Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--only q16_1024,...] [--vendor-ref]
+Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--settle S] [--only q16_1024,...] [--vendor-ref]
 """
 from __future__ import annotations
 
@@ -45,11 +47,26 @@ def log(msg: str) -> None:
     print(f"[bench] {msg}", file=sys.stderr, flush=True)
 
 
+SETTLE_S = 0.5                   # back-to-back running before each timed region (--settle)
+
+
 def time_steps(launch, steps: int, warmup: int, stream) -> tuple[float, float]:
-    """Return (event ms per step, wall ms per step) over exactly `steps` launches."""
+    """Return (event ms per step, wall ms per step) over exactly `steps` launches.
+
+    After the `warmup` launches the workload keeps running back to back for
+    SETTLE_S seconds before the timed region: the GPU's clock controller
+    takes tens of milliseconds to settle after a burst starts (measured: the
+    batched GEMV's calls take ~200 us at first, up to ~260 us a few ms later
+    and 203 us from then on), so a short timed region right after a short
+    warm-up times that transient, not the sustained rate."""
     for _ in range(warmup):
         launch()
     M.check(M.lib().det_device_sync())
+    t_end = time.perf_counter() + SETTLE_S
+    while time.perf_counter() < t_end:
+        for _ in range(8):
+            launch()
+        M.check(M.lib().det_device_sync())
     e0, e1 = M.Event(), M.Event()
     t0 = time.perf_counter()
     e0.record(stream)
@@ -295,7 +312,7 @@ def host_abi_timings(reps: int = 3) -> dict:
     return res
 
 
-def vendor_int8_child(steps: int) -> None:
+def vendor_int8_child(steps: int, settle_s: float) -> None:
     """Child-process body of --vendor-ref: time the vendor int8 GEMM
     (torch._int_mm, which dispatches to hipBLASLt on ROCm) on the headline
     shape with torch's own events and print one JSON line.  B is passed
@@ -311,6 +328,11 @@ def vendor_int8_child(steps: int) -> None:
         for _ in range(5):
             torch._int_mm(a, bb)
         torch.cuda.synchronize()
+        t_end = time.perf_counter() + settle_s   # the same settle phase as time_steps
+        while time.perf_counter() < t_end:
+            for _ in range(8):
+                torch._int_mm(a, bb)
+            torch.cuda.synchronize()
         e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
         e0.record()
         for _ in range(steps):
@@ -322,12 +344,13 @@ def vendor_int8_child(steps: int) -> None:
     print(json.dumps(out), flush=True)
 
 
-def vendor_int8_reference(steps: int) -> dict:
+def vendor_int8_reference(steps: int, settle_s: float) -> dict:
     """Run vendor_int8_child in a child process.  Called before this process
     makes any HIP call, so the child starts from a process that has not
     touched the GPU."""
     import subprocess
-    p = subprocess.run([sys.executable, os.path.abspath(__file__), "--vendor-child", "--steps", str(steps)],
+    p = subprocess.run([sys.executable, os.path.abspath(__file__), "--vendor-child", "--steps", str(steps),
+                        "--settle", str(settle_s)],
                        capture_output=True, text=True, timeout=600)
     lines = [x for x in p.stdout.splitlines() if x.startswith("{")]
     if p.returncode != 0 or not lines:
@@ -442,9 +465,13 @@ def main() -> int:
     ap.add_argument("--vendor-child", action="store_true", help=argparse.SUPPRESS)
     ap.add_argument("--host-abi", action="store_true",
                     help="also time the reference-ABI host-pointer calls end to end (PCIe included)")
+    ap.add_argument("--settle", type=float, default=0.5,
+                    help="seconds of back-to-back running before each timed region (default %(default)s)")
     args = ap.parse_args()
+    global SETTLE_S
+    SETTLE_S = max(0.0, args.settle)
     if args.vendor_child:
-        vendor_int8_child(args.steps)
+        vendor_int8_child(args.steps, SETTLE_S)
         return 0
 
     world = int(os.environ.get("WORLD_SIZE", "1"))
@@ -454,7 +481,7 @@ def main() -> int:
               file=sys.stderr)
         return 2
     # the vendor leg runs first, in a child process, before any HIP call here
-    vendor = vendor_int8_reference(args.steps) if args.vendor_ref else None
+    vendor = vendor_int8_reference(args.steps, SETTLE_S) if args.vendor_ref else None
 
     L = M.lib()
     M.check(L.det_set_device(0))
@@ -487,6 +514,7 @@ def main() -> int:
         "n_gpus": 1,
         "steps": K,
         "warmup": W,
+        "settle_s": SETTLE_S,
         "ms_per_step": round(head["wall_ms"], 5),
         "higher_is_better": True,
         "scaling": "weak",
