@@ -85,3 +85,13 @@ def test_missing_library_fails_loudly(monkeypatch):
     monkeypatch.setattr(mind_amd, "LIB_PATH", "/nonexistent/libmind_det_hip.so")
     with pytest.raises(RuntimeError, match="no CPU fallback"):
         mind_amd.lib()
+
+
+def test_bench_refuses_more_than_one_gpu():
+    """bench.py's contract: --gpus N > 1 exits non-zero with a message before any GPU call."""
+    import subprocess
+    import sys
+    p = subprocess.run([sys.executable, os.path.join(ROOT, "bench.py"), "--gpus", "2"], capture_output=True,
+                       text=True, timeout=120)
+    assert p.returncode == 2
+    assert "one GPU" in p.stderr and p.stdout == ""
