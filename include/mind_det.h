@@ -84,7 +84,11 @@ int64_t __mind_blas_dot_i16_v(int64_t a, int64_t b, int64_t len);
 /* Replaces __mind_blas_dot_f32(a, b, len): strict-FP f32 dot (8 lanes of
  * unfused multiply-then-add, left-to-right lane fold, sequential tail); the
  * result's f32 bits are returned in the low 32 bits of the int64 (0 for
- * len <= 0 or NULL): runtime-support/mind_intrinsics.c:1190-1290. */
+ * len <= 0 or NULL): runtime-support/mind_intrinsics.c:1190-1290.
+ * The packed return has no room for an error code: a device failure also
+ * returns 0 (the bits of +0.0f).  These symbols (and dotf32) clear
+ * det_last_error() on entry, so a caller that must tell a failure from a
+ * zero dot checks that det_last_error()[0] == '\0' after the call. */
 int64_t __mind_blas_dot_f32(int64_t a, int64_t b, int64_t len);
 /* Replaces __mind_blas_dot_f32_v (vector-dialect twin, same schedule):
  * src/type_checker/mod.rs (dot_f32_v), src/mlir/lowering.rs:5528-5690. */
@@ -196,6 +200,13 @@ int64_t det_matmul_ws_dev(int64_t op, const void *a, const void *b, int32_t *c, 
                           void *ws, int64_t ws_bytes, void *stream);
 
 /* Runtime helpers (thin wrappers over HIP, so a caller needs no HIP headers). */
+/* Release the library's per-device state (its stream, event, host-call
+ * staging buffer and workspace arena) after waiting for the work queued on
+ * them; later calls recreate what they need.  The same teardown runs at
+ * dlclose and at process exit, as the reference joins its thread pool at
+ * unload (runtime-support/mind_intrinsics.c:2066-2080).  No other call of the
+ * library may be in flight. */
+int64_t det_shutdown(void);
 const char *det_last_error(void);
 const char *det_version(void);
 int64_t det_device_count(void);

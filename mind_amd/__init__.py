@@ -86,6 +86,7 @@ def _bind(L):
     L.det_matmul_ws_dev.argtypes = [_i64, _p, _p, _p, _i64, _i64, _i64, _p, _i64, _p]
     L.det_matmul_ws_dev.restype = _i64
     L.det_last_error.argtypes = []; L.det_last_error.restype = ctypes.c_char_p
+    L.det_shutdown.argtypes = []; L.det_shutdown.restype = _i64
     L.det_version.argtypes = []; L.det_version.restype = ctypes.c_char_p
     L.det_device_count.argtypes = []; L.det_device_count.restype = _i64
     L.det_set_device.argtypes = [_i64]; L.det_set_device.restype = _i64

@@ -3,7 +3,9 @@
 Every .hip file under csrc/ is compiled to an object with hipcc (device code
 for gfx950 only), the host-only .cpp files with the same compiler driver, and
 everything is linked into ``mind_amd/lib/libmind_det_hip.so``.  Objects go to
-``mind_amd/_build/`` (not committed).
+``mind_amd/_build/`` (not committed).  ``shim/gemmq_kn.c`` becomes
+``mind_amd/lib/libmind_det_gemmq_kn.so``: the Q16 benches' ``gemmq`` (B
+un-transposed), forwarding into the main library.
 
 Run ``python -m mind_amd.build`` (or ``__graft_entry__.build()``).
 """
@@ -20,6 +22,7 @@ CSRC = os.path.join(HERE, "csrc")
 BUILD = os.path.join(HERE, "_build")
 LIBDIR = os.path.join(HERE, "lib")
 LIB = os.path.join(LIBDIR, "libmind_det_hip.so")
+SHIM_LIB = os.path.join(LIBDIR, "libmind_det_gemmq_kn.so")
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 ARCH = "gfx950"
 
@@ -57,8 +60,17 @@ def build(verbose: bool = True) -> str:
     if r.returncode != 0:
         raise RuntimeError(f"link failed: {' '.join(cmd)}\n{r.stdout}\n{r.stderr}")
     os.replace(tmp, LIB)
+    # the bench form of `gemmq` (B un-transposed), a separate small library
+    # that forwards into libmind_det_hip.so
+    tmp = SHIM_LIB + ".tmp"
+    cmd = ["gcc", "-O2", "-Wall", "-Werror", "-shared", "-fPIC", os.path.join(HERE, "shim", "gemmq_kn.c"),
+           "-L", LIBDIR, "-lmind_det_hip", "-Wl,-rpath,$ORIGIN", "-o", tmp]
+    r = subprocess.run(cmd, capture_output=True, text=True)
+    if r.returncode != 0:
+        raise RuntimeError(f"shim link failed: {' '.join(cmd)}\n{r.stdout}\n{r.stderr}")
+    os.replace(tmp, SHIM_LIB)
     if verbose:
-        print(f"built {LIB}")
+        print(f"built {LIB} and {SHIM_LIB}")
     return LIB
 
 

@@ -20,6 +20,8 @@
 // reference's mind_last_error (src/ffi/mod.rs:173).  A NULL pointer or a
 // non-positive size with nothing to compute follows the reference's Track A
 // convention and returns 0 (runtime-support/mind_intrinsics.c:1537-1539).
+#include <cstdio>
+#include <cstdlib>
 #include <cstring>
 #include <mutex>
 #include <string>
@@ -30,7 +32,15 @@
 
 namespace {
 
-thread_local std::string g_err;
+// Last error text of this thread.  A plain buffer, not a std::string: a
+// thread_local object with a destructor would keep the library loaded at
+// dlclose (the C runtime holds a DSO while it has pending thread-local
+// destructors), and the unload teardown below would never run.
+thread_local char g_err[512];
+
+void put_err(const char *a, const char *b = nullptr) {
+    snprintf(g_err, sizeof g_err, "%s%s%s", a, b ? ": " : "", b ? b : "");
+}
 
 constexpr int MAX_DEV = 64;
 constexpr int64_t DIM_MAX = 0x7fffffff;
@@ -49,8 +59,8 @@ struct DevState {
 };
 DevState g_dev[MAX_DEV];
 
-int64_t set_err(int64_t code, const std::string &msg) {
-    g_err = msg;
+int64_t set_err(int64_t code, const char *msg) {
+    put_err(msg);
     return code;
 }
 
@@ -83,11 +93,62 @@ int64_t ensure(void **buf, size_t *have, size_t need) {
     return 0;
 }
 
+void teardown_at_unload();
+
 int64_t ensure_stream(DevState &d) {
+    // The first resource the library creates registers the teardown.  It is
+    // registered after the HIP runtime has initialised (this call is past a
+    // HIP call), so at process exit it runs before the runtime's own exit
+    // handlers; atexit from a shared object also runs at its dlclose.
+    static std::once_flag registered;
+    std::call_once(registered, [] { atexit(teardown_at_unload); });
     if (!d.stream) DET_HIP_CHECK(hipStreamCreateWithFlags(&d.stream, hipStreamNonBlocking));
     if (!d.ws_free) DET_HIP_CHECK(hipEventCreateWithFlags(&d.ws_free, hipEventDisableTiming));
     return 0;
 }
+
+// Release device d's state: wait until the library stream and the last
+// workspace user are done, then free the staging buffer and the arena and
+// destroy the stream and the event.  Caller holds ds.mu and has made d the
+// current device.  Returns the first failure, but releases what it can.
+int64_t release_device(DevState &ds) {
+    int64_t rc = 0;
+    auto step = [&](hipError_t e, const char *what) {
+        if (e != hipSuccess && rc == 0) rc = det_fail_hip(e, what);
+    };
+    if (ds.stream) step(hipStreamSynchronize(ds.stream), "hipStreamSynchronize");
+    if (ds.ws_free) step(hipEventSynchronize(ds.ws_free), "hipEventSynchronize");
+    if (ds.io) step(hipFree(ds.io), "hipFree(staging)");
+    if (ds.ws) step(hipFree(ds.ws), "hipFree(workspace)");
+    if (ds.ws_free) step(hipEventDestroy(ds.ws_free), "hipEventDestroy");
+    if (ds.stream) step(hipStreamDestroy(ds.stream), "hipStreamDestroy");
+    ds.io = ds.ws = nullptr;
+    ds.io_bytes = ds.ws_bytes = 0;
+    ds.ws_free = nullptr;
+    ds.stream = nullptr;
+    return rc;
+}
+
+int64_t release_all() {
+    int64_t rc = 0;
+    int prev = -1;
+    if (hipGetDevice(&prev) != hipSuccess) prev = -1;
+    for (int d = 0; d < MAX_DEV; ++d) {
+        DevState &ds = g_dev[d];
+        std::lock_guard<std::mutex> lock(ds.mu);
+        if (!ds.stream && !ds.ws_free && !ds.io && !ds.ws) continue;
+        hipError_t e = hipSetDevice(d);
+        int64_t r = e == hipSuccess ? release_device(ds) : det_fail_hip(e, "hipSetDevice");
+        if (r && rc == 0) rc = r;
+    }
+    if (prev >= 0) (void)hipSetDevice(prev);
+    return rc;
+}
+
+// Library teardown at dlclose / exit (the reference joins its thread pool at
+// unload the same way, runtime-support/mind_intrinsics.c:2066-2080).  Runs
+// single-threaded: no call of this library may be in flight.
+void teardown_at_unload() { (void)release_all(); }
 
 bool bad_dims(int64_t m, int64_t k, int64_t n) {
     return m < 0 || k < 0 || n < 0 || m > DIM_MAX || k > DIM_MAX || n > DIM_MAX;
@@ -299,7 +360,11 @@ int64_t pack_f32(float v) {
     return (int64_t)(uint64_t)b;
 }
 
+// The packed f32 return cannot carry an error code (a failure returns the
+// bits of +0.0f), so the error text is cleared on entry: after the call an
+// empty det_last_error() means success.
 int64_t dot_f32_host(int64_t a, int64_t b, int64_t len) {
+    g_err[0] = 0;
     if (len <= 0 || !a || !b) return pack_f32(0.0f);
     float out = 0.0f;
     if (f32_rows_host((const float *)(intptr_t)a, (const float *)(intptr_t)b, &out, 1, len) != 0) return 0;
@@ -379,7 +444,7 @@ int64_t fft_host(int64_t re, int64_t im, int64_t tw, int64_t logn, int64_t n, in
 }  // namespace
 
 extern "C" int64_t det_fail_hip(hipError_t e, const char *what) {
-    g_err = std::string(what) + ": " + hipGetErrorString(e);
+    put_err(what, hipGetErrorString(e));
     return DET_ERR_HIP;
 }
 
@@ -617,7 +682,8 @@ int64_t det_dot_dev(int64_t op, const void *a, const void *b, int64_t len, int32
 }
 
 // ---------------------------------------------------------------- runtime
-const char *det_last_error(void) { return g_err.c_str(); }
+int64_t det_shutdown(void) { return release_all(); }
+const char *det_last_error(void) { return g_err; }
 const char *det_version(void) { return "mind-det-mi355x 0.1 (gfx950)"; }
 
 int64_t det_device_count(void) {

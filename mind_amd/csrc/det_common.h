@@ -118,7 +118,10 @@ __device__ __forceinline__ void dma16(v4i32 rsrc, uint32_t lds, int voff) {
                  : "memory", "m0");
 }
 // The same with a uniform byte offset added from an SGPR (soffset), so a
-// loop can advance every lane's address without a vector add.
+// loop can advance every lane's address without a vector add.  The range
+// check covers voffset only: soffset is added after it, so voff + soff must
+// itself stay inside the buffer (an out-of-range soffset is a real access,
+// not a zero fill).
 __device__ __forceinline__ void dma16s(v4i32 rsrc, uint32_t lds, int voff, uint32_t soff) {
     asm volatile("s_mov_b32 m0, %0\n\tbuffer_load_dwordx4 %1, %2, %3 offen lds" ::"s"(lds), "v"(voff), "s"(rsrc),
                  "s"(soff)

@@ -372,16 +372,20 @@ __global__ __launch_bounds__(THREADS, 1) void gemm_i8_dma_kernel(const int8_t *_
 
     const int nk = (K + BK - 1) / BK;
     if constexpr (FULL) {
-        // lane offsets without k; steps past the end point beyond the buffer
-        // (soffset = its size), which the DMA turns into zero fills
-        const uint32_t lim_a = (uint32_t)M * (uint32_t)K, lim_b = (uint32_t)K * (uint32_t)N;
+        // Lane offsets without k; the K step enters through soffset.  The
+        // buffer unit's range check covers voffset only (soffset is added
+        // after it), so a step past the end of K must not be expressed as an
+        // out-of-range soffset: it re-loads the last step instead (K >= BK on
+        // this path).  Those loads land in a stage whose data is never read
+        // again (see the schedule below) and hit in L2.
+        const uint32_t last_a = (uint32_t)(K - BK), last_b = (uint32_t)(K - BK) * (uint32_t)N;
         // LDS destinations by scalar arithmetic from one base
         const uint32_t lds_w = lds_addr(smem) + (uint32_t)(2 * wave) * 1024u;
         auto issue_f = [&](auto st_c, int k0) {
             constexpr int st = decltype(st_c)::value;
             const bool in = k0 < K;
-            const uint32_t sa = in ? (uint32_t)k0 : lim_a;
-            const uint32_t sb = in ? (uint32_t)k0 * (uint32_t)N : lim_b;
+            const uint32_t sa = in ? (uint32_t)k0 : last_a;
+            const uint32_t sb = in ? (uint32_t)k0 * (uint32_t)N : last_b;
 #pragma unroll
             for (int j = 0; j < 2; ++j) {
                 dma16s(ra, lds_w + (uint32_t)((2 * st + 0) * TILE_BYTES + j * 1024), (int)a_off[j], sa);
@@ -469,8 +473,8 @@ __global__ __launch_bounds__(THREADS, 1) void gemm_i8_dma_kernel(const int8_t *_
                 step1(S3{}, kt + 3);
             }
         }
-        // the loads issued past the end of K are zero fills; none may still
-        // be writing LDS when the workgroup ends
+        // the re-loads issued past the end of K must not still be writing
+        // LDS when the workgroup ends
         DET_WAIT_VMCNT(0);
     } else {
     // The ping-pong schedule of the full-tile path (see there for the slot
@@ -611,7 +615,7 @@ hipError_t launch_gemm_i8(const int8_t *A, const int8_t *B, int32_t *C, int M, i
     const dim3 grid(tiles_m * tiles_n), block(THREADS);
     const bool fast = (K % 16 == 0) && (N % 16 == 0) && (((uintptr_t)A & 15) == 0) && (((uintptr_t)B & 15) == 0) &&
                       (size_t)M * K < 0x80000000ull && (size_t)K * N < 0x80000000ull;
-    const bool full = fast && M % BM == 0 && N % BN == 0 && K % (BK * NSTAGE) == 0;
+    const bool full = fast && K > 0 && M % BM == 0 && N % BN == 0 && K % (BK * NSTAGE) == 0;
     if (full)
         hipLaunchKernelGGL((gemm_i8_dma_kernel<EPI_I8, true>), grid, block, 0, s, A, B, C, M, N, K, tiles_m, tiles_n,
                            I16Epi{});
@@ -632,7 +636,7 @@ hipError_t launch_gemm_i8_i16epi(const int8_t *A2, const int8_t *B2, int M2, int
     using namespace i8g;
     const int tiles_m = (M2 + BM - 1) / BM, tiles_n = (N2 + BN - 1) / BN;
     I16Epi e{rowsum, colsum, C, M16, N16, ncs, 0x80u, (uint32_t)((uint64_t)(uint32_t)K16 * 0x4000u)};
-    const bool full = M2 % BM == 0 && N2 % BN == 0 && Kp % (BK * NSTAGE) == 0;
+    const bool full = Kp > 0 && M2 % BM == 0 && N2 % BN == 0 && Kp % (BK * NSTAGE) == 0;
     if (full)
         hipLaunchKernelGGL((gemm_i8_dma_kernel<EPI_I16, true>), dim3(tiles_m * tiles_n), dim3(THREADS), 0, s, A2, B2,
                            (int32_t *)nullptr, M2, N2, Kp, tiles_m, tiles_n, e);

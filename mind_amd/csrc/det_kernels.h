@@ -30,8 +30,10 @@ size_t i16_workspace_bytes(int M, int N, int K);   // covers both int16 paths be
 // Q16.16: B is [K][N], or [N][K] when b_is_t.
 hipError_t launch_gemm_q16(const int32_t *A, const int32_t *B, int32_t *C, int M, int N, int K, bool b_is_t,
                            void *ws, hipStream_t s);
-// Second-generation Q16 kernel (8 waves per tile, no flush): K <= 65536 and
-// 4 * max(M, N) * Kp < 2^31.  Its workspace is covered by q16_workspace_bytes.
+// Second-generation Q16 kernel (12 waves per 64x64 tile, no flush): eligible
+// for 1 <= K < 65536 (the shift-0/1 limb sets stay exact in int32 only below
+// 2^16 terms) and 6 * (M + N) * Kp < 2^31 (Kp = K rounded up to 64).  Its
+// workspace is covered by q16_workspace_bytes.
 bool q16x_eligible(int M, int N, int K);
 hipError_t launch_gemm_q16x(const int32_t *A, const int32_t *B, int32_t *C, int M, int N, int K, bool b_is_t,
                             void *ws, hipStream_t s);

@@ -97,6 +97,17 @@ def lib():
     return _lib
 
 
+def ref_built() -> bool:
+    """Whether oracle/_ref holds the reference's runtime-support library
+    (checked without loading it, so test collection maps nothing)."""
+    return os.path.exists(REF_PATH)
+
+
+def fft_ref_built() -> bool:
+    """Whether oracle/_ref holds the reference's C FFT (not loaded here)."""
+    return os.path.exists(FFT_REF_PATH)
+
+
 def ref_lib():
     """The reference's own runtime-support library, or None if not built."""
     global _ref

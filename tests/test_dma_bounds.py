@@ -1,0 +1,105 @@
+"""CPU model of the int8 DMA kernel's buffer addressing (no GPU needed).
+
+gemm_i8_dma_kernel (mind_amd/csrc/det_gemm_i8.hip) moves operand chunks
+global -> LDS with buffer_load_dwordx4 ... lds.  The buffer unit's range check
+covers the per-lane voffset only; the full-tile loop advances K through the
+SGPR soffset, so every (voffset + soffset) it issues, including the steps it
+issues past the end of K, must lie inside the operand.  The edge-tile loop
+expresses out-of-range chunks as voffset = OOB_OFFSET (range-checked, a zero
+fill) and must keep every other chunk inside.  This test restates the lane ->
+chunk assignment and the issue schedule of both loops and checks every
+address they can form, for the shapes the library routes to each loop.
+"""
+import numpy as np
+import pytest
+
+BM = BN = 256
+BK = 64
+NSTAGE = 4
+OOB = 0x80000000
+
+
+def _lane_chunks():
+    """Per (wave, j, lane): A row / k-chunk and B k-row / n-chunk of the
+    wave's DMA share (the inverse of the LDS swizzles)."""
+    wave = np.arange(8)[:, None, None]
+    j = np.arange(2)[None, :, None]
+    lane = np.arange(64)[None, None, :]
+    slot = 64 * (2 * wave + j) + lane
+    ar = slot >> 2
+    ac = (slot & 3) ^ ((ar >> 2) & 3)
+    br = slot >> 4
+    bc = (slot & 15) ^ ((br & 7) << 1)
+    return ar.ravel(), 16 * ac.ravel(), br.ravel(), 16 * bc.ravel()
+
+
+def _issued_steps(K):
+    nk = (K + BK - 1) // BK
+    # prologue: steps 0..2; MEM(s) for s = 0..nk-1 issues step s + 3
+    return np.arange(0, nk + NSTAGE - 1) * BK
+
+
+def _full_addresses(M, N, K):
+    ar, akc, br, bnc = _lane_chunks()
+    lim_a, lim_b = M * K, K * N
+    lo_a = hi_a = lo_b = hi_b = None
+    for m0 in range(0, M, BM):
+        a_off = (m0 + ar) * K + akc
+        for n0 in range(0, N, BN):
+            b_off = br * N + n0 + bnc
+            for k0 in _issued_steps(K):
+                sa = k0 if k0 < K else K - BK
+                sb = k0 * N if k0 < K else (K - BK) * N
+                va, vb = a_off + sa, b_off + sb
+                lo_a = va.min() if lo_a is None else min(lo_a, va.min())
+                hi_a = va.max() if hi_a is None else max(hi_a, va.max())
+                lo_b = vb.min() if lo_b is None else min(lo_b, vb.min())
+                hi_b = vb.max() if hi_b is None else max(hi_b, vb.max())
+    return (lo_a, hi_a + 16, lim_a), (lo_b, hi_b + 16, lim_b)
+
+
+def _edge_addresses(M, N, K):
+    ar, akc, br, bnc = _lane_chunks()
+    worst = []
+    for m0 in range(0, M, BM):
+        for n0 in range(0, N, BN):
+            a_ok = m0 + ar < M
+            b_ok = n0 + bnc < N
+            for k0 in _issued_steps(K):
+                oka = a_ok & (k0 + akc < K)
+                okb = b_ok & (k0 + br < K)
+                va = np.where(oka, (m0 + ar) * K + akc + k0, OOB)
+                vb = np.where(okb, (br + k0) * N + n0 + bnc, OOB)
+                for v, ok, lim in ((va, oka, M * K), (vb, okb, K * N)):
+                    inside = v[ok]
+                    if inside.size:
+                        worst.append(inside.max() + 16 - lim)
+                    # every chunk flagged outside must be the range-checked OOB offset
+                    assert np.all(v[~ok] == OOB)
+    return max(worst) if worst else -1
+
+
+@pytest.mark.parametrize("M,N,K", [(256, 256, 256), (512, 256, 1024), (256, 768, 512), (1024, 1024, 2048),
+                                   (4096, 4096, 4096), (256, 256, 8192)])
+def test_full_tile_dma_stays_inside_operands(M, N, K):
+    assert M % BM == 0 and N % BN == 0 and K % (BK * NSTAGE) == 0 and K > 0
+    (lo_a, end_a, lim_a), (lo_b, end_b, lim_b) = _full_addresses(M, N, K)
+    assert lo_a >= 0 and end_a <= lim_a, (end_a, lim_a)
+    assert lo_b >= 0 and end_b <= lim_b, (end_b, lim_b)
+
+
+def test_full_tile_model_catches_the_old_past_end_offset():
+    """The model is load-bearing: expressing a past-end step as soffset =
+    operand size (the form the kernel used before) reads past A and B."""
+    ar, akc, br, bnc = _lane_chunks()
+    M = N = K = 256
+    k0 = _issued_steps(K)[-1]
+    assert k0 >= K
+    assert ((ar * K + akc) + M * K).max() + 16 > M * K
+    assert ((br * N + bnc) + K * N).max() + 16 > K * N
+
+
+@pytest.mark.parametrize("M,N,K", [(1, 16, 16), (100, 48, 80), (257, 272, 320), (300, 1008, 48), (256, 256, 64)])
+def test_edge_tile_dma_stays_inside_operands(M, N, K):
+    assert K % 16 == 0 and N % 16 == 0
+    assert _edge_addresses(M, N, K) <= 0

@@ -839,6 +839,58 @@ def test_config_int8_mlp_4096x4096x11008():
     np.testing.assert_array_equal(C[rows], O.gemm_i8_rows(x, w, m, k, n, rows))
 
 
+def test_config_int8_8192_cubed():
+    """The square 8192^3 peak-probe config: sampled rows and columns against
+    the oracle, output poisoned before each of two runs."""
+    m = k = n = 8192
+    a, b = M.gen_i8(0xDEADBEEF ^ 0x8192, m * k, k * n)
+    note("det_matmul_i8_dev 8192^3")
+    C = _dev_run(lambda pa, pb, pc, s: M.lib().det_matmul_i8_dev(pa, pb, pc, m, k, n, s), [a, b], (m, n))
+    rows = _sample_rows(m, 4)
+    np.testing.assert_array_equal(C[rows], O.gemm_i8_rows(a, b, m, k, n, rows))
+    cols = _sample_rows(n, 4)
+    Bc = np.ascontiguousarray(b.reshape(k, n)[:, cols]).ravel()
+    np.testing.assert_array_equal(C[:, cols], O.gemm_i8(a, Bc, m, k, len(cols)))
+
+
+def test_config_q16_4096_cubed():
+    """Q16 at 4096^3 (the metric's Q16 shape), saturating generator: sampled
+    rows against the oracle, two poisoned runs."""
+    m = k = n = 4096
+    a, b = M.gen_q16_sat(0xDEADBEEF ^ 0x4016, m * k, k * n, 13)
+    note("det_matmul_q16_dev 4096^3 (saturating config)")
+    C = _dev_run(lambda pa, pb, pc, s: M.lib().det_matmul_q16_dev(pa, pb, pc, m, k, n, s), [a, b], (m, n))
+    rows = _sample_rows(m, 5)
+    np.testing.assert_array_equal(C[rows], O.gemm_q16_rows(a, b, m, k, n, rows))
+
+
+def test_determinism_256_runs(canaries):
+    """The reference's stability gate (benches/det_gemv_q16_mt.rs:71,
+    det_matmul_q16_mt.rs:88: 256 recomputations, one hash): the 64^3 int8 and
+    Q16 canaries and the 11922x384 routing-shape GEMV, each computed 256
+    times through the reference ABI into fresh poisoned buffers."""
+    runs = 256
+    w = canaries["workloads"]
+    a8, b8 = O.gen_i8(w["gemm-i8-64x64x64"]["seed"], 64 * 64, 64 * 64)
+    aq, bq = O.gen_q16(w["gemm-q16-fused-64x64x64"]["seed"], 64 * 64, 64 * 64)
+    m, k = 11922, 384
+    W, x = O.gen_q16(0xDEADBEEF_00000000 ^ ((m << 20) ^ k), m * k, k)
+    want_gemv = h32(O.gemv_q16(W, x, m, k))
+    cases = (("gemmi8", a8, b8, 6, w["gemm-i8-64x64x64"]["avx2"]),
+             ("gemmqmm", aq, bq, 6, w["gemm-q16-fused-64x64x64"]["avx2"]),
+             ("gemvq", W, x, 5, want_gemv))
+    for sym, a, b, arity, want in cases:
+        note(f"{sym} x{runs} into fresh poisoned buffers")
+        fn = getattr(M.lib(), sym)
+        hashes = set()
+        for rep in range(runs):
+            out = np.full(64 * 64 if arity == 6 else m, 0x5A5A5A5A ^ rep, np.int32)
+            rc = fn(addr(a), addr(b), addr(out), 64, 64, 64) if arity == 6 else fn(addr(a), addr(b), addr(out), m, k)
+            assert rc == 0, (rc, M.last_error())
+            hashes.add(h32(out))
+        assert hashes == {want}, (sym, len(hashes))
+
+
 def test_config_q16_1024_cubed():
     m = k = n = 1024
     a, b = M.gen_q16_sat(0xDEADBEEF ^ 0x1016, m * k, k * n, 13)

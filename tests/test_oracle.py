@@ -139,7 +139,7 @@ def test_f32_strict_schedule_is_load_bearing(canaries):
     assert not ok(lambda a: np.float32(np.dot(a.astype(np.float64), x.astype(np.float64))))
 
 
-@pytest.mark.skipif(O.ref_lib() is None, reason="oracle/_ref not built (reference tree absent)")
+@pytest.mark.skipif(not O.ref_built(), reason="oracle/_ref not built (reference tree absent)")
 def test_f32_strict_matches_reference_live():
     R = O.ref_lib()
     prev = R.__mind_blas_set_use_avx2(0)
@@ -175,7 +175,7 @@ def test_dot_l1_q16_brute_force_and_extremes():
         assert O.dot_l1_q16(a, a) == 0
 
 
-@pytest.mark.skipif(O.ref_lib() is None, reason="oracle/_ref not built (reference tree absent)")
+@pytest.mark.skipif(not O.ref_built(), reason="oracle/_ref not built (reference tree absent)")
 def test_dot_l1_q16_matches_reference_live():
     """The reference's scalar L1 (mind_intrinsics.c:1551-1562, the contract the
     vector-dialect emitter lowering.rs:6035-6060 matches byte for byte) on every
@@ -232,7 +232,7 @@ def test_dot_q16_matches_reference_fixture():
         assert got == c["scalar"] == c["avx2"], c
 
 
-@pytest.mark.skipif(O.ref_lib() is None, reason="oracle/_ref not built (reference tree absent)")
+@pytest.mark.skipif(not O.ref_built(), reason="oracle/_ref not built (reference tree absent)")
 def test_gemv_rows_match_reference_dot_live():
     R = O.ref_lib()
     m, k = 96, 1031
@@ -476,7 +476,7 @@ def test_fft_python_restatement_and_planted_mistakes(canaries):
         assert np.array_equal(got[0], want[0]) and np.array_equal(got[1], want[1]), logn
 
 
-@pytest.mark.skipif(O.fft_ref_lib() is None, reason="oracle/_ref not built (reference tree absent)")
+@pytest.mark.skipif(not O.fft_ref_built(), reason="oracle/_ref not built (reference tree absent)")
 @pytest.mark.parametrize("logn", list(range(1, 14)))
 def test_fft_matches_reference_c_live(logn):
     # bench/fft/fft_ref.c (span-2 stage unpeeled) equals the peeled kernel
@@ -515,7 +515,7 @@ def test_fft_close_to_the_float_dft():
         assert np.max(np.abs(X)) > 100 * bound
 
 
-@pytest.mark.skipif(O.fft_ref_lib() is None, reason="oracle/_ref not built (reference tree absent)")
+@pytest.mark.skipif(not O.fft_ref_built(), reason="oracle/_ref not built (reference tree absent)")
 def test_fft_peeled_stage_differs_from_the_c_file_when_tw0_is_not_one():
     # The kernel this build follows (examples/fft_q16.mind) peels the span-2
     # stage as a plain add / subtract; bench/fft/fft_ref.c multiplies by tw[0].
