@@ -199,6 +199,18 @@ int64_t det_workspace_bytes(int64_t op, int64_t m, int64_t k, int64_t n);
 int64_t det_matmul_ws_dev(int64_t op, const void *a, const void *b, int32_t *c, int64_t m, int64_t k, int64_t n,
                           void *ws, int64_t ws_bytes, void *stream);
 
+/* No counterpart in the reference.  For callers that cannot allocate device
+ * memory (code under HIP graph capture, tight serving loops, harnesses that
+ * forbid hipMalloc): det_matmul_ws_dev with the workspace taken from a fixed
+ * per-device array of DET_SCRATCH_BYTES compiled into the library, so the
+ * call allocates nothing.  A shape whose det_workspace_bytes exceeds it
+ * returns DET_ERR_ARG (32 MiB covers Q16 up to 1024^3 and int16 up to
+ * 2048^3).  Every call on one GPU shares that GPU's array: calls that
+ * overlap on one GPU (two streams, two host threads) race; order them. */
+#define DET_SCRATCH_BYTES (32LL << 20)
+int64_t det_matmul_scratch_dev(int64_t op, const void *a, const void *b, int32_t *c, int64_t m, int64_t k, int64_t n,
+                               void *stream);
+
 /* Runtime helpers (thin wrappers over HIP, so a caller needs no HIP headers). */
 /* Release the library's per-device state (its stream, event, host-call
  * staging buffer and workspace arena) after waiting for the work queued on

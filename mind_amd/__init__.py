@@ -85,6 +85,8 @@ def _bind(L):
     L.det_workspace_bytes.argtypes = [_i64] * 4; L.det_workspace_bytes.restype = _i64
     L.det_matmul_ws_dev.argtypes = [_i64, _p, _p, _p, _i64, _i64, _i64, _p, _i64, _p]
     L.det_matmul_ws_dev.restype = _i64
+    L.det_matmul_scratch_dev.argtypes = [_i64, _p, _p, _p, _i64, _i64, _i64, _p]
+    L.det_matmul_scratch_dev.restype = _i64
     L.det_last_error.argtypes = []; L.det_last_error.restype = ctypes.c_char_p
     L.det_shutdown.argtypes = []; L.det_shutdown.restype = _i64
     L.det_version.argtypes = []; L.det_version.restype = ctypes.c_char_p
