@@ -607,7 +607,220 @@ __global__ __launch_bounds__(THREADS, 1) void gemm_i8_dma_kernel(const int8_t *_
         else epilogue(std::true_type{});
     }
 }
+// ------------------------------------------------------- 128 x 256 tiles
+// The same ping-pong schedule on a 128 x 256 C tile, for grids whose
+// 256 x 256 tiles would fill at most one round of the chip.  With one
+// 256 x 256 tile per CU every CU writes its 256 KiB of C at the same moment
+// at the end (64 MiB at 4096^3: ~9 us at HBM write speed, nothing left to
+// overlap it with); with 128-row tiles each CU runs two tiles in turn and
+// the first tile's stores drain while the second computes, and small grids
+// (2048^3: 64 tiles of 256^2) use twice as many CUs.  The price is a smaller
+// wave tile (64 x 64: 2 x 2 blocks of 32x32x32), a third more LDS bytes per
+// MFMA, so grids of several rounds stay on the 256 x 256 kernel.
+// A stage holds K = 128 as two 64-wide sub-stages, each laid out like a
+// stage of the 256 x 256 kernel (A [128][64] with swz_a, B [64][256] with
+// swz_b), so every barrier slot again carries 16 MFMAs per wave; 3 stages
+// (144 KiB) with the DMA two steps ahead.  Full shapes only: M % 128 == 0,
+// N % 256 == 0, K % 128 == 0, K > 0, operands below 2^31 bytes, aligned.
+namespace h128 {
+constexpr int BM = 128, WM = 64, MI = 2, SUB = 2, NST = 3, KS = BK * SUB;
+constexpr int A_BYTES = BM * BK, B_BYTES = BK * BN, SS = A_BYTES + B_BYTES, ST = SUB * SS;
+constexpr int DPS = SUB * 3;   // DMA instructions per wave per stage: 1 A + 2 B per sub-stage
+
+__global__ __launch_bounds__(THREADS, 1) void gemm_i8_h128_kernel(const int8_t *__restrict__ A,
+                                                                  const int8_t *__restrict__ B,
+                                                                  int32_t *__restrict__ C, int M, int N, int K,
+                                                                  int tiles_m, int tiles_n) {
+    __shared__ __attribute__((aligned(1024))) int8_t smem[NST * ST];
+
+    const int ntiles = tiles_m * tiles_n;
+    const int pid = xcd_remap(blockIdx.x, ntiles);
+    const int in_group = GROUP_M * tiles_n;
+    const int first_m = (pid / in_group) * GROUP_M;
+    const int gsize = min(tiles_m - first_m, GROUP_M);
+    const int tm = first_m + (pid % in_group) % gsize;
+    const int tn = (pid % in_group) / gsize;
+    const int m0 = tm * BM, n0 = tn * BN;
+
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int wm = (wave >> 2) * WM, wn = (wave & 3) * WN;
+    const int l32 = lane & 31, lh = lane >> 5;
+    const int tg = lane >> 4, ti = lane & 15;
+    const int tr_row = 16 * (tg >> 1) + (ti >> 1);
+    const int tr_col = 16 * (tg & 1) + 8 * (ti & 1);
+
+    const v4i32 ra = rsrc_words(A, (uint32_t)M * (uint32_t)K);
+    const v4i32 rb = rsrc_words(B, (uint32_t)K * (uint32_t)N);
+    // this lane's chunk of the wave's A block (1 KiB = 16 rows) and of its two
+    // B blocks (1 KiB = 4 k-rows each) of a sub-stage: the inverse swizzles
+    uint32_t a_off, b_off[2];
+    {
+        const int slot = 64 * wave + lane;
+        const int ar = slot >> 2, ac = (slot & 3) ^ ((ar >> 2) & 3);
+        a_off = (uint32_t)(m0 + ar) * (uint32_t)K + (uint32_t)(16 * ac);
+    }
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+        const int slot = 64 * (2 * wave + j) + lane;
+        const int br = slot >> 4, bc = (slot & 15) ^ ((br & 7) << 1);
+        b_off[j] = (uint32_t)br * (uint32_t)N + (uint32_t)(n0 + 16 * bc);
+    }
+
+    v16i32 acc[MI][2];
+#pragma unroll
+    for (int i = 0; i < MI; ++i)
+#pragma unroll
+        for (int j = 0; j < 2; ++j) acc[i][j] = (v16i32){0};
+
+    struct Ops {
+        v2i64 a[MI], b[2];
+    };
+    auto read_ops = [&](Ops &o, int stage, int sub, int h) {
+        const int8_t *sA = smem + stage * ST + sub * SS;
+        const int8_t *sB = sA + A_BYTES;
+#pragma unroll
+        for (int j = 0; j < 2; ++j) {
+            const int r = 32 * h + tr_row, cb = (wn + 32 * j + tr_col) >> 4, sub8 = tr_col & 8;
+            const v2i32 lo = read_tr8(sB + swz_b(r, cb) + sub8);
+            const v2i32 hi = read_tr8(sB + swz_b(r + 8, cb) + sub8);
+            o.b[j] = __builtin_bit_cast(v2i64, (v4i32){lo.x, lo.y, hi.x, hi.y});
+        }
+#pragma unroll
+        for (int i = 0; i < MI; ++i) o.a[i] = *(const v2i64 *)(sA + swz_a(wm + i * 32 + l32, 2 * h + lh));
+    };
+    auto mma = [&](const Ops &o) {
+#pragma unroll
+        for (int i = 0; i < MI; ++i)
+#pragma unroll
+            for (int j = 0; j < 2; ++j) acc[i][j] = mfma32x32x32(o.a[i], o.b[j], acc[i][j]);
+    };
+
+    const int nk = K / KS;
+    // K advances through soffset, which the range check does not cover: a
+    // step past the end re-loads the last step (into a stage never read again)
+    const uint32_t last_a = (uint32_t)(K - KS), last_b = (uint32_t)(K - KS) * (uint32_t)N;
+    const uint32_t base = lds_addr(smem);
+    auto issue_f = [&](auto st_c, int k0) {
+        constexpr int st = decltype(st_c)::value;
+        const bool in = k0 < K;
+        const uint32_t sa = in ? (uint32_t)k0 : last_a;
+        const uint32_t sb = in ? (uint32_t)k0 * (uint32_t)N : last_b;
+#pragma unroll
+        for (int u = 0; u < SUB; ++u) {
+            dma16s(ra, base + (uint32_t)(st * ST + u * SS) + (uint32_t)wave * 1024u, (int)a_off,
+                   sa + (uint32_t)(u * BK));
+#pragma unroll
+            for (int j = 0; j < 2; ++j)
+                dma16s(rb, base + (uint32_t)(st * ST + u * SS + A_BYTES) + (uint32_t)(2 * wave + j) * 1024u,
+                       (int)b_off[j], sb + (uint32_t)(u * BK) * (uint32_t)N);
+        }
+    };
+    using S0 = std::integral_constant<int, 0>;
+    using S1 = std::integral_constant<int, 1>;
+    using S2 = std::integral_constant<int, 2>;
+    static_assert(NST == 3, "the unrolled loop below assumes 3 stages");
+    // Ping-pong schedule as in gemm_i8_dma_kernel (slots A_j = {group 0:
+    // MFMA(j), group 1: MEM(j)}, B_j = {group 0: MEM(j+1), group 1: MFMA(j)}),
+    // with the DMA two steps ahead: MEM(s) reads step s (stage s % 3) and
+    // refills stage (s + 2) % 3 with step s + 2.  That stage held step s - 1,
+    // read in B_{s-2} and A_{s-1}; MEM(s) runs in B_{s-1} (group 0) or A_s
+    // (group 1), after both.  Before the barrier closing A_j each wave waits
+    // for its share of step j + 1 (vmcnt(DPS): step j + 2 stays in flight).
+    issue_f(S0{}, 0);
+    issue_f(S1{}, KS);
+    DET_WAIT_VMCNT(DPS);   // step 0 landed
+    __builtin_amdgcn_s_barrier();
+    Ops q0, q1, q2, q3;
+    auto mem = [&](auto st_c, int s) {
+        constexpr int st = decltype(st_c)::value;
+        read_ops(q0, st, 0, 0);
+        read_ops(q1, st, 0, 1);
+        read_ops(q2, st, 1, 0);
+        read_ops(q3, st, 1, 1);
+        issue_f(std::integral_constant<int, (st + 2) % NST>{}, (s + 2) * KS);
+    };
+    auto mma_all = [&]() {
+        mma(q0);
+        mma(q1);
+        mma(q2);
+        mma(q3);
+    };
+    if (wave < 4) {
+        mem(S0{}, 0);
+        DET_WAIT_LGKM0();
+        __builtin_amdgcn_s_barrier();
+        auto step0 = [&](auto cur_c, int kt) {
+            constexpr int nxt = (decltype(cur_c)::value + 1) % NST;
+            __builtin_amdgcn_sched_barrier(0);
+            mma_all();
+            __builtin_amdgcn_sched_barrier(0);
+            DET_WAIT_VMCNT(DPS);
+            __builtin_amdgcn_s_barrier();
+            __builtin_amdgcn_sched_barrier(0);
+            if (kt + 1 < nk) mem(std::integral_constant<int, nxt>{}, kt + 1);
+            DET_WAIT_LGKM0();
+            __builtin_amdgcn_sched_barrier(0);
+            __builtin_amdgcn_s_barrier();
+        };
+        int kt = 0;
+        for (; kt + NST <= nk; kt += NST) {
+            step0(S0{}, kt);
+            step0(S1{}, kt + 1);
+            step0(S2{}, kt + 2);
+        }
+        if (kt < nk) step0(S0{}, kt);
+        if (kt + 1 < nk) step0(S1{}, kt + 1);
+    } else {
+        __builtin_amdgcn_s_barrier();
+        auto step1 = [&](auto cur_c, int kt) {
+            __builtin_amdgcn_sched_barrier(0);
+            mem(cur_c, kt);
+            DET_WAIT_VMCNT(DPS);
+            DET_WAIT_LGKM0();
+            __builtin_amdgcn_s_barrier();
+            __builtin_amdgcn_sched_barrier(0);
+            mma_all();
+            __builtin_amdgcn_sched_barrier(0);
+            __builtin_amdgcn_s_barrier();
+        };
+        int kt = 0;
+        for (; kt + NST <= nk; kt += NST) {
+            step1(S0{}, kt);
+            step1(S1{}, kt + 1);
+            step1(S2{}, kt + 2);
+        }
+        if (kt < nk) step1(S0{}, kt);
+        if (kt + 1 < nk) step1(S1{}, kt + 1);
+    }
+    // the re-loads issued past the end of K must not still be writing LDS
+    DET_WAIT_VMCNT(0);
+
+#pragma unroll
+    for (int i = 0; i < MI; ++i)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+            const int row = m0 + wm + i * 32 + 8 * (r >> 2) + 4 * lh + (r & 3);
+            int32_t *crow = C + (size_t)row * N + n0 + wn + l32;
+#pragma unroll
+            for (int j = 0; j < 2; ++j) __builtin_nontemporal_store(acc[i][j][r], crow + j * 32);
+        }
+}
+}  // namespace h128
 }  // namespace i8g
+
+// Compute units of the current device (cached per device).
+static int cu_count() {
+    static int cached[64];
+    int d = 0;
+    if (hipGetDevice(&d) != hipSuccess || d < 0 || d >= 64) return 256;
+    if (cached[d] == 0) {
+        int n = 0;
+        if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, d) != hipSuccess || n <= 0) n = 256;
+        cached[d] = n;
+    }
+    return cached[d];
+}
 
 hipError_t launch_gemm_i8(const int8_t *A, const int8_t *B, int32_t *C, int M, int N, int K, hipStream_t s) {
     using namespace i8g;
@@ -616,7 +829,14 @@ hipError_t launch_gemm_i8(const int8_t *A, const int8_t *B, int32_t *C, int M, i
     const bool fast = (K % 16 == 0) && (N % 16 == 0) && (((uintptr_t)A & 15) == 0) && (((uintptr_t)B & 15) == 0) &&
                       (size_t)M * K < 0x80000000ull && (size_t)K * N < 0x80000000ull;
     const bool full = fast && K > 0 && M % BM == 0 && N % BN == 0 && K % (BK * NSTAGE) == 0;
-    if (full)
+    const bool full128 = fast && K > 0 && M % h128::BM == 0 && N % BN == 0 && K % h128::KS == 0;
+    // 128-row tiles when 256 x 256 tiles would not fill more than one round
+    // of the chip (or do not fit the shape)
+    if (full128 && (!full || tiles_m * tiles_n <= cu_count())) {
+        const int tm128 = M / h128::BM;
+        hipLaunchKernelGGL(h128::gemm_i8_h128_kernel, dim3(tm128 * tiles_n), block, 0, s, A, B, C, M, N, K, tm128,
+                           tiles_n);
+    } else if (full)
         hipLaunchKernelGGL((gemm_i8_dma_kernel<EPI_I8, true>), grid, block, 0, s, A, B, C, M, N, K, tiles_m, tiles_n,
                            I16Epi{});
     else if (fast)

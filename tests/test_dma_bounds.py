@@ -1,8 +1,9 @@
 """CPU model of the int8 DMA kernel's buffer addressing (no GPU needed).
 
-gemm_i8_dma_kernel (mind_amd/csrc/det_gemm_i8.hip) moves operand chunks
-global -> LDS with buffer_load_dwordx4 ... lds.  The buffer unit's range check
-covers the per-lane voffset only; the full-tile loop advances K through the
+gemm_i8_dma_kernel and gemm_i8_h128_kernel (mind_amd/csrc/det_gemm_i8.hip)
+move operand chunks
+global -> LDS with buffer_load_dwordx4 ... lds.  The buffer unit's range
+check covers the per-lane voffset only; the full-tile loops advance K through the
 SGPR soffset, so every (voffset + soffset) it issues, including the steps it
 issues past the end of K, must lie inside the operand.  The edge-tile loop
 expresses out-of-range chunks as voffset = OOB_OFFSET (range-checked, a zero
@@ -97,6 +98,44 @@ def test_full_tile_model_catches_the_old_past_end_offset():
     assert k0 >= K
     assert ((ar * K + akc) + M * K).max() + 16 > M * K
     assert ((br * N + bnc) + K * N).max() + 16 > K * N
+
+
+def _h128_addresses(M, N, K):
+    """gemm_i8_h128_kernel: 128-row tiles, K steps of 128 as two 64-wide
+    sub-stages, each wave one A block and two B blocks per sub-stage, DMA two
+    steps ahead (prologue steps 0 and 1, MEM(s) issues step s + 2)."""
+    KS = 2 * BK
+    wave = np.arange(8)[:, None]
+    lane = np.arange(64)[None, :]
+    slot = (64 * wave + lane).ravel()
+    ar = slot >> 2
+    akc = 16 * ((slot & 3) ^ ((ar >> 2) & 3))
+    _, _, br, bnc = _lane_chunks()
+    assert ar.max() < 128
+    nk = K // KS
+    lo = [None, None]
+    hi = [None, None]
+    for m0 in range(0, M, 128):
+        a_off = (m0 + ar) * K + akc
+        for n0 in range(0, N, BN):
+            b_off = br * N + n0 + bnc
+            for step in range(0, nk + 2):
+                k0 = step * KS
+                sa = k0 if k0 < K else K - KS
+                sb = k0 * N if k0 < K else (K - KS) * N
+                for u in range(2):
+                    for i, v in enumerate((a_off + sa + u * BK, b_off + sb + u * BK * N)):
+                        lo[i] = v.min() if lo[i] is None else min(lo[i], v.min())
+                        hi[i] = v.max() if hi[i] is None else max(hi[i], v.max())
+    return (lo[0], hi[0] + 16, M * K), (lo[1], hi[1] + 16, K * N)
+
+
+@pytest.mark.parametrize("M,N,K", [(128, 256, 128), (4096, 4096, 4096), (384, 512, 384), (2048, 2048, 2048),
+                                   (128, 768, 1152)])
+def test_h128_tile_dma_stays_inside_operands(M, N, K):
+    assert M % 128 == 0 and N % BN == 0 and K % 128 == 0 and K > 0
+    for lo, end, lim in _h128_addresses(M, N, K):
+        assert lo >= 0 and end <= lim, (end, lim)
 
 
 @pytest.mark.parametrize("M,N,K", [(1, 16, 16), (100, 48, 80), (257, 272, 320), (300, 1008, 48), (256, 256, 64)])

@@ -594,6 +594,42 @@ def test_gemm_i8_shapes(m, k, n):
     np.testing.assert_array_equal(got, O.gemm_i8(a, b, m, k, n))
 
 
+# Shapes that route to the 128 x 256-tile kernel (M % 128, N % 256, K % 128
+# all zero, and at most one round of 256 x 256 tiles or K % 256 != 0): one
+# and two tiles, K of 1, 2, 3 and 128 steps of 128 (the 3-stage loop's
+# remainders), K not a multiple of 256.
+H128_SHAPES = [(128, 128, 256), (128, 256, 256), (256, 256, 256), (384, 384, 512), (1152, 640, 768),
+               (128, 16384, 256), (640, 1280, 1536), (2048, 2048, 2048)]
+
+
+@pytest.mark.parametrize("m,k,n", H128_SHAPES, ids=[f"{m}x{k}x{n}" for m, k, n in H128_SHAPES])
+def test_gemm_i8_h128_tile_shapes(m, k, n):
+    a, b = O.gen_i8(0x128128 ^ (m * 1000003 + k * 1009 + n), m * k, k * n)
+    note(f"det_matmul_i8_dev (128x256 tiles) {m}x{k}x{n}")
+    C = _dev_run(lambda pa, pb, pc, s: M.lib().det_matmul_i8_dev(pa, pb, pc, m, k, n, s), [a, b], (m, n))
+    if m * n * k <= 1 << 30:
+        np.testing.assert_array_equal(C, O.gemm_i8(a, b, m, k, n).reshape(m, n))
+    else:
+        rows = np.unique(np.r_[_sample_rows(m, 8), 127, 128, m - 128])
+        np.testing.assert_array_equal(C[rows], O.gemm_i8_rows(a, b, m, k, n, rows))
+        cols = _sample_rows(n, 4)
+        Bc = np.ascontiguousarray(b.reshape(k, n)[:, cols]).ravel()
+        np.testing.assert_array_equal(C[:, cols], O.gemm_i8(a, Bc, m, k, len(cols)))
+
+
+def test_gemm_i8_h128_wraps_mod_2_32():
+    m, k, n = 128, 131200, 256                   # 1025 steps of 128; k * 128 * 128 > 2^31
+    a = np.full((m, k), -128, np.int8)
+    b = np.full((k, n), -128, np.int8)
+    a[5, :] = 127
+    b[:, 7] = 3
+    note(f"det_matmul_i8 wrap (128x256 tiles) {m}x{k}x{n}")
+    got = M.det_matmul_i8(a, b)
+    rows = np.array([0, 5, 127])
+    np.testing.assert_array_equal(got[rows], O.gemm_i8_rows(a.ravel(), b.ravel(), m, k, n, rows))
+    assert got[0, 0] == np.int32(np.uint32((k * 16384) % (1 << 32)).astype(np.int32))
+
+
 def test_gemm_i8_k_zero_and_empty():
     note("det_matmul_i8 k=0")
     np.testing.assert_array_equal(M.det_matmul_i8(np.zeros((5, 0), np.int8), np.zeros((0, 7), np.int8)),
