@@ -146,7 +146,8 @@ def gemm_workload(kind: str, m: int, k: int, n: int, steps: int, warmup: int, st
     return out
 
 
-def gemv_workload(m: int, k: int, nb: int, steps: int, warmup: int, stream, seed_tag: int):
+def gemv_workload(m: int, k: int, nb: int, steps: int, warmup: int, stream, seed_tag: int,
+                  keep_output: bool = False):
     L = M.lib()
     W, X = M.gen_q16(SEED ^ seed_tag, m * k, nb * k, 15)
     dw, dx = M.DeviceBuffer.from_array(W), M.DeviceBuffer.from_array(X)
@@ -169,7 +170,10 @@ def gemv_workload(m: int, k: int, nb: int, steps: int, warmup: int, stream, seed
     for buf in (dw, dx, dy):
         buf.free()
     nbytes = 4.0 * m * k + 4.0 * k * nb + 4.0 * m * nb
-    return {"ms": ev, "wall_ms": wall, "bytes": nbytes, "verify": verify, "checked_rows": len(rows)}
+    out = {"ms": ev, "wall_ms": wall, "bytes": nbytes, "verify": verify, "checked_rows": len(rows)}
+    if keep_output:
+        out["W"], out["X"], out["Y"] = W, X, Y
+    return out
 
 
 def f32_rows_workload(rows: int, cols: int, steps: int, warmup: int, stream, seed_tag: int):
@@ -452,6 +456,82 @@ def cpu_baseline_int8(A: np.ndarray, B: np.ndarray, C_gpu: np.ndarray, m: int, k
             "host_cpus": os.cpu_count(), "cpu_model": _cpu_model()}
 
 
+def _time_median(fn, reps: int) -> float:
+    times = []
+    for _ in range(reps):
+        t0 = time.perf_counter()
+        fn()
+        times.append(time.perf_counter() - t0)
+    return sorted(times)[len(times) // 2]
+
+
+def cpu_baseline_q16(A: np.ndarray, B: np.ndarray, C_gpu: np.ndarray, m: int, k: int, n: int) -> dict:
+    """The MT CPU restatement of the reference's Q16 path (BLIS 4x8 i64
+    microkernel) on the whole Q16 workload; output equal to the GPU's."""
+    import oracle as O
+
+    L = O.lib()
+    c = np.empty(m * n, np.int32)
+    run = lambda: L.det_cpu_gemm_q16(A.ctypes.data, B.ctypes.data, c.ctypes.data, m, k, n)
+    run()
+    if not np.array_equal(c.reshape(m, n), C_gpu):
+        raise SystemExit("Q16 CPU baseline output differs from the GPU output")
+    t = _time_median(run, 5)
+    return {"value": 2.0 * m * n * k / t / 1e12, "unit": "Q16 TOP/s (2*MNK/t)", "gmac_per_s": m * n * k / t / 1e9,
+            "cores": int(L.det_cpu_threads_for(m)), "kind": "port",
+            "sample": f"the whole {m}x{k}x{n} Q16 GEMM (median of 5, {t * 1e3:.1f} ms each); oracle/det_cpu_mt.c "
+                      f"restatement of the reference MT Q16 path, output equal to the GPU output",
+            "cpu_model": _cpu_model()}
+
+
+def cpu_baseline_gemv(W: np.ndarray, x: np.ndarray, y_gpu: np.ndarray, m: int, k: int) -> dict:
+    """The MT CPU restatement of the reference's Q16 GEMV row bands on the
+    whole batch-1 workload; output equal to the GPU's."""
+    import oracle as O
+
+    L = O.lib()
+    y = np.empty(m, np.int32)
+    run = lambda: L.det_cpu_gemv_q16(W.ctypes.data, x.ctypes.data, y.ctypes.data, m, k)
+    run()
+    if not np.array_equal(y, y_gpu.ravel()):
+        raise SystemExit("GEMV CPU baseline output differs from the GPU output")
+    t = _time_median(run, 7)
+    nbytes = 4.0 * m * k + 4.0 * k + 4.0 * m
+    return {"value": nbytes / t / 1e9, "unit": "GB/s", "ms": t * 1e3, "cores": int(L.det_cpu_threads_for(m)),
+            "kind": "port",
+            "sample": f"the whole {m}x{k} batch-1 Q16 GEMV (median of 7); oracle/det_cpu_mt.c restatement of "
+                      f"__mind_blas_gemv_q16_mt's row bands, output equal to the GPU output",
+            "cpu_model": _cpu_model()}
+
+
+def cpu_config_i8_256() -> dict:
+    """BASELINE config 1 (the reference's CPU bench shape, int8 256^3 from the
+    bench LCG, seed 0xDEADBEEF00000000 ^ 256, benches/det_matmul_i8.rs), on ONE
+    thread of the MT restatement (the AVX2 vpmaddwd 4x16 microkernel), beside
+    the reference's published single-thread figure."""
+    import oracle as O
+
+    L = O.lib()
+    n = 256
+    a, b = O.gen_i8(0xDEADBEEF00000000 ^ n, n * n, n * n)
+    c = np.empty(n * n, np.int32)
+    L.det_cpu_set_threads(1)
+    try:
+        run = lambda: L.det_cpu_gemm_i8(a.ctypes.data, b.ctypes.data, c.ctypes.data, n, n, n)
+        run()
+        exact = bool(np.array_equal(c, O.gemm_i8(a, b, n, n, n).ravel()))
+        t = _time_median(run, 101)
+    finally:
+        L.det_cpu_set_threads(0)
+    if not exact:
+        raise SystemExit("int8 256^3 CPU baseline output differs from the oracle")
+    return {"value": n ** 3 / t / 1e9, "unit": "GMAC/s", "us": t * 1e6, "cores": 1, "kind": "port",
+            "sample": "int8 256^3 (median of 101 calls), one thread, output equal to the oracle",
+            "published_reference": {"value": 12.56, "unit": "GMAC/s", "host": "Intel i7-5930K 3.5 GHz AVX2, 1 core",
+                                    "source": "docs/benchmarks/RESULTS-mind-vs-rust-2026-06-09.md:45"},
+            "cpu_model": _cpu_model()}
+
+
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -552,7 +632,7 @@ def main() -> int:
     sec = {}
     if want("q16_1024"):
         log("q16_1024: det_matmul_q16 1024^3 (saturating config)")
-        r = runs["q16_1024"] = gemm_workload("q16", 1024, 1024, 1024, K, W, stream, 0x1016)
+        r = runs["q16_1024"] = gemm_workload("q16", 1024, 1024, 1024, K, W, stream, 0x1016, keep_output=True)
         t = r["ops"] / (r["ms"] * 1e-3) / 1e12
         sec["q16_1024"] = {"ms": round(r["ms"], 5), "value": round(t, 3), "unit": "Q16 TOP/s (2*MNK/t)",
                            "gmac_per_s": round(t * 500.0, 1),
@@ -584,7 +664,7 @@ def main() -> int:
         name = f"gemv_q16_16384_b{nb}"
         if want(name):
             log(f"{name}: det_gemv_q16 16384x16384 batch {nb}")
-            r = runs[name] = gemv_workload(16384, 16384, nb, K, W, stream, 0x6E3F ^ nb)
+            r = runs[name] = gemv_workload(16384, 16384, nb, K, W, stream, 0x6E3F ^ nb, keep_output=(nb == 1))
             gbs = r["bytes"] / (r["ms"] * 1e-3) / 1e9
             sec[name] = {"ms": round(r["ms"], 5), "value": round(gbs, 1), "unit": "GB/s",
                          "roofline": {"bound": "hbm", "achieved": round(gbs, 1), "peak": PEAK_HBM_GBS,
@@ -661,6 +741,19 @@ def main() -> int:
         log("cpu_baseline: MT CPU restatement on a row band of the same workload")
         result["cpu_baseline"] = cpu_baseline_int8(head["A"], head["B"], head["C"], m, k, n)
         log(f"cpu_baseline: {result['cpu_baseline']['value']:.3f} TOP/s on {result['cpu_baseline']['cores']} threads")
+        extra = {"i8_256_one_thread": cpu_config_i8_256()}
+        log(f"cpu_baseline i8 256^3, 1 thread: {extra['i8_256_one_thread']['value']:.2f} GMAC/s")
+        if "q16_1024" in runs and "A" in runs["q16_1024"]:
+            r = runs["q16_1024"]
+            extra["q16_1024"] = cpu_baseline_q16(r["A"], r["B"], r["C"], 1024, 1024, 1024)
+            log(f"cpu_baseline q16 1024^3: {extra['q16_1024']['gmac_per_s']:.1f} GMAC/s "
+                f"on {extra['q16_1024']['cores']} threads")
+        if "gemv_q16_16384_b1" in runs and "W" in runs["gemv_q16_16384_b1"]:
+            r = runs["gemv_q16_16384_b1"]
+            extra["gemv_q16_16384_b1"] = cpu_baseline_gemv(r["W"], r["X"], r["Y"], 16384, 16384)
+            log(f"cpu_baseline gemv 16384^2: {extra['gemv_q16_16384_b1']['value']:.1f} GB/s "
+                f"on {extra['gemv_q16_16384_b1']['cores']} threads")
+        result["cpu_baselines"] = extra
     else:
         result["exact_vs_oracle"] = None
         result["cpu_baseline"] = None

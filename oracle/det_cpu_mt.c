@@ -13,17 +13,28 @@
  *   - a persistent worker pool created lazily once, a dispatch lock that
  *     serialises callers, condvar wake / join
  *                                   (runtime-support/mind_intrinsics.c:1935-2082)
- *   - per band, the BLIS loop nest jc -> pc -> ic -> jr -> ir with packed A/B
- *     panels and an i64 C-scratch, truncated to i32 once at the store
+ *   - per band, the BLIS loop nest jc -> ic -> pc -> jr -> ir with packed
+ *     A/B panels and a C-scratch truncated to i32 once at the store
  *                                   (src/mlir/lowering.rs:7074-7676, 8371-9265)
  *   - tile constants                (src/mlir/gemm_tuning.rs:61-159)
  *       int8: MC/KC/NC = 1024/512/128, MR x NR = 4 x 16
  *       Q16 : MC/KC/NC =   64/256/128, MR x NR = 4 x 8
- *   - GEMV: one row band per worker, per-row K-ordered Q16 dot
- *                                   (src/mlir/lowering.rs:9822-9997)
+ *   - the AVX2 microkernels, written with intrinsics in the shape the
+ *     reference emits them:
+ *       int8 (lowering.rs:7798-8052): panels packed to i16 K-pairs; per K
+ *       pair the NR/8 = 2 B vectors are loaded once, each row's A pair is
+ *       broadcast as one i32 and contracted with both by vpmaddwd into i32
+ *       accumulators (vpaddd), 4 x 2 ymm accumulators, an i32 C-scratch;
+ *       Q16 (lowering.rs:7470-7540): per k the 8 B values are sign-extended
+ *       to i64, each row's A value broadcast, multiplied (vpmuldq), shifted
+ *       arithmetically by 16 and added into 4 x 2 ymm i64 accumulators;
+ *   - GEMV: one row band per worker, per-row Q16 dot 8 lanes wide in i64
+ *     (vpmuldq + shift + add), a scalar K % 8 tail, lane sums folded at the
+ *     end                           (src/mlir/lowering.rs:9822-9997)
  * Built with -O3 -march=x86-64-v3 -ffp-contract=off -pthread, the flags the
  * reference passes to clang (src/eval/mlir_build.rs:685-760).
  */
+#include <immintrin.h>
 #include <pthread.h>
 #include <stdint.h>
 #include <stdlib.h>
@@ -145,66 +156,80 @@ static long make_bands(band_args *args, const void *a, const void *b, void *c, i
 #define I8_MR 4
 #define I8_NR 16
 
+/* 4 x 16 int8 microkernel over kp K pairs: acc[r][g] holds columns 8g..8g+7
+ * of row r.  bq: [kp][16 columns][2] i16, aq: [kp][4 rows][2] i16. */
+static inline void i8_micro(const int16_t *aq, const int16_t *bq, int64_t kp, int32_t *cs, int64_t ldc) {
+    __m256i acc[I8_MR][2];
+    for (int r = 0; r < I8_MR; ++r) acc[r][0] = acc[r][1] = _mm256_setzero_si256();
+    for (int64_t q = 0; q < kp; ++q) {
+        const __m256i b0 = _mm256_load_si256((const __m256i *)(bq + q * 2 * I8_NR));
+        const __m256i b1 = _mm256_load_si256((const __m256i *)(bq + q * 2 * I8_NR + 16));
+        const int16_t *a = aq + q * 2 * I8_MR;
+        for (int r = 0; r < I8_MR; ++r) {
+            int32_t pair;
+            memcpy(&pair, a + 2 * r, 4);
+            const __m256i av = _mm256_set1_epi32(pair);   /* [a0, a1] in every 32-bit lane */
+            acc[r][0] = _mm256_add_epi32(acc[r][0], _mm256_madd_epi16(av, b0));
+            acc[r][1] = _mm256_add_epi32(acc[r][1], _mm256_madd_epi16(av, b1));
+        }
+    }
+    for (int r = 0; r < I8_MR; ++r)
+        for (int g = 0; g < 2; ++g) {
+            __m256i *c = (__m256i *)(cs + r * ldc + 8 * g);
+            _mm256_storeu_si256(c, _mm256_add_epi32(_mm256_loadu_si256(c), acc[r][g]));
+        }
+}
+
 static void i8_band(void *p) {
     band_args *ba = (band_args *)p;
     const int8_t *A = (const int8_t *)ba->a, *B = (const int8_t *)ba->b;
     int32_t *C = (int32_t *)ba->c;
     const int64_t k = ba->k, n = ba->n;
     /* packed panels are i16 (sign-extended once at pack time), K-pair
-     * interleaved like the vpmaddwd microkernel consumes them */
-    int16_t *bp = (int16_t *)aligned_alloc(64, sizeof(int16_t) * (I8_KC + 1) * I8_NC);
-    int16_t *ap = (int16_t *)aligned_alloc(64, sizeof(int16_t) * (I8_KC + 1) * I8_MC);
-    int64_t *cs = (int64_t *)aligned_alloc(64, sizeof(int64_t) * I8_MC * I8_NC);
+     * interleaved like the vpmaddwd microkernel consumes them; the C-scratch
+     * is i32 (the AVX2 rung's: i32 partials end to end, wrapped like the
+     * final truncation) */
+    int16_t *bp = (int16_t *)aligned_alloc(64, sizeof(int16_t) * (I8_KC + 2) * I8_NC);
+    int16_t *ap = (int16_t *)aligned_alloc(64, sizeof(int16_t) * (I8_KC + 2) * I8_MC);
+    int32_t *cs = (int32_t *)aligned_alloc(64, sizeof(int32_t) * I8_MC * I8_NC);
     for (int64_t jc = 0; jc < n; jc += I8_NC) {
         const int64_t nc = n - jc < I8_NC ? n - jc : I8_NC;
         const int64_t ncp = (nc + I8_NR - 1) / I8_NR * I8_NR;
         for (int64_t ic = ba->r0; ic < ba->r1; ic += I8_MC) {
             const int64_t mc = ba->r1 - ic < I8_MC ? ba->r1 - ic : I8_MC;
             const int64_t mcp = (mc + I8_MR - 1) / I8_MR * I8_MR;
-            memset(cs, 0, sizeof(int64_t) * mcp * ncp);
+            memset(cs, 0, sizeof(int32_t) * mcp * ncp);
             for (int64_t pc = 0; pc < k; pc += I8_KC) {
                 const int64_t kc = k - pc < I8_KC ? k - pc : I8_KC;
                 const int64_t kp = (kc + 1) / 2; /* K pairs, zero padded */
                 /* pack B: [jr block][kpair][NR][2] */
-                for (int64_t jr = 0; jr < ncp; jr += I8_NR)
-                    for (int64_t q = 0; q < kp; ++q)
-                        for (int64_t c = 0; c < I8_NR; ++c)
-                            for (int e = 0; e < 2; ++e) {
-                                int64_t kk = 2 * q + e, j = jr + c;
-                                bp[((jr / I8_NR) * kp + q) * 2 * I8_NR + 2 * c + e] =
-                                    (kk < kc && j < nc) ? B[(pc + kk) * n + jc + j] : 0;
-                            }
-                /* pack A: [ir block][kpair][MR][2] */
-                for (int64_t ir = 0; ir < mcp; ir += I8_MR)
-                    for (int64_t q = 0; q < kp; ++q)
-                        for (int64_t r = 0; r < I8_MR; ++r)
-                            for (int e = 0; e < 2; ++e) {
-                                int64_t kk = 2 * q + e, i = ir + r;
-                                ap[((ir / I8_MR) * kp + q) * 2 * I8_MR + 2 * r + e] =
-                                    (kk < kc && i < mc) ? A[(ic + i) * k + pc + kk] : 0;
-                            }
                 for (int64_t jr = 0; jr < ncp; jr += I8_NR) {
-                    const int16_t *bb = bp + (jr / I8_NR) * kp * 2 * I8_NR;
-                    for (int64_t ir = 0; ir < mcp; ir += I8_MR) {
-                        const int16_t *aa = ap + (ir / I8_MR) * kp * 2 * I8_MR;
-                        int32_t acc[I8_MR][I8_NR];
-                        memset(acc, 0, sizeof acc);
-                        for (int64_t q = 0; q < kp; ++q) {
-                            const int16_t *bq = bb + q * 2 * I8_NR;
-                            const int16_t *aq = aa + q * 2 * I8_MR;
-                            for (int r = 0; r < I8_MR; ++r) {
-                                const int32_t a0 = aq[2 * r], a1 = aq[2 * r + 1];
-                                for (int c = 0; c < I8_NR; ++c)
-                                    acc[r][c] += a0 * (int32_t)bq[2 * c] + a1 * (int32_t)bq[2 * c + 1];
-                            }
+                    int16_t *d = bp + (jr / I8_NR) * kp * 2 * I8_NR;
+                    for (int64_t q = 0; q < kp; ++q)
+                        for (int e = 0; e < 2; ++e) {
+                            const int64_t kk = 2 * q + e;
+                            const int8_t *src = B + (pc + kk) * n + jc + jr;
+                            for (int64_t c = 0; c < I8_NR; ++c)
+                                d[q * 2 * I8_NR + 2 * c + e] = (kk < kc && jr + c < nc) ? src[c] : 0;
                         }
-                        for (int r = 0; r < I8_MR; ++r)
-                            for (int c = 0; c < I8_NR; ++c) cs[(ir + r) * ncp + jr + c] += acc[r][c];
+                }
+                /* pack A: [ir block][kpair][MR][2] */
+                for (int64_t ir = 0; ir < mcp; ir += I8_MR) {
+                    int16_t *d = ap + (ir / I8_MR) * kp * 2 * I8_MR;
+                    for (int64_t r = 0; r < I8_MR; ++r) {
+                        const int8_t *src = A + (ic + ir + r) * k + pc;
+                        const int ok = ir + r < mc;
+                        for (int64_t kk = 0; kk < 2 * kp; ++kk)
+                            d[(kk >> 1) * 2 * I8_MR + 2 * r + (kk & 1)] = (ok && kk < kc) ? src[kk] : 0;
                     }
                 }
+                for (int64_t jr = 0; jr < ncp; jr += I8_NR) {
+                    const int16_t *bb = bp + (jr / I8_NR) * kp * 2 * I8_NR;
+                    for (int64_t ir = 0; ir < mcp; ir += I8_MR)
+                        i8_micro(ap + (ir / I8_MR) * kp * 2 * I8_MR, bb, kp, cs + ir * ncp + jr, ncp);
+                }
             }
-            for (int64_t i = 0; i < mc; ++i)
-                for (int64_t j = 0; j < nc; ++j) C[(ic + i) * n + jc + j] = (int32_t)cs[i * ncp + j];
+            for (int64_t i = 0; i < mc; ++i) memcpy(C + (ic + i) * n + jc, cs + i * ncp, sizeof(int32_t) * nc);
         }
     }
     free(bp);
@@ -220,37 +245,73 @@ static void i8_band(void *p) {
 #define Q_MR 4
 #define Q_NR 8
 
+/* Arithmetic shift right by 16 of four i64 lanes (AVX2 has no vpsraq):
+ * offset by 2^63, shift logically, remove the shifted offset. */
+static inline __m256i sra16_epi64(__m256i x) {
+    const __m256i bias = _mm256_set1_epi64x((long long)0x8000000000000000ull);
+    return _mm256_sub_epi64(_mm256_srli_epi64(_mm256_xor_si256(x, bias), 16), _mm256_srli_epi64(bias, 16));
+}
+
+/* 4 x 8 Q16 microkernel over kc k: acc[r][h] holds columns 4h..4h+3 of row r
+ * as i64.  bq: [kc][8] i32, aq: [kc][4] i32. */
+static inline void q16_micro(const int32_t *aq, const int32_t *bq, int64_t kc, int64_t *cs, int64_t ldc) {
+    __m256i acc[Q_MR][2];
+    for (int r = 0; r < Q_MR; ++r) acc[r][0] = acc[r][1] = _mm256_setzero_si256();
+    for (int64_t kk = 0; kk < kc; ++kk) {
+        const __m256i bv = _mm256_load_si256((const __m256i *)(bq + kk * Q_NR));
+        const __m256i b0 = _mm256_cvtepi32_epi64(_mm256_castsi256_si128(bv));
+        const __m256i b1 = _mm256_cvtepi32_epi64(_mm256_extracti128_si256(bv, 1));
+        for (int r = 0; r < Q_MR; ++r) {
+            const __m256i av = _mm256_set1_epi64x((long long)aq[kk * Q_MR + r]);
+            acc[r][0] = _mm256_add_epi64(acc[r][0], sra16_epi64(_mm256_mul_epi32(av, b0)));
+            acc[r][1] = _mm256_add_epi64(acc[r][1], sra16_epi64(_mm256_mul_epi32(av, b1)));
+        }
+    }
+    for (int r = 0; r < Q_MR; ++r)
+        for (int h = 0; h < 2; ++h) {
+            __m256i *c = (__m256i *)(cs + r * ldc + 4 * h);
+            _mm256_storeu_si256(c, _mm256_add_epi64(_mm256_loadu_si256(c), acc[r][h]));
+        }
+}
+
 static void q16_band(void *p) {
     band_args *ba = (band_args *)p;
     const int32_t *A = (const int32_t *)ba->a, *B = (const int32_t *)ba->b;
     int32_t *C = (int32_t *)ba->c;
     const int64_t k = ba->k, n = ba->n;
-    int32_t bp[Q_KC * Q_NC], ap[Q_MC * Q_KC];
-    int64_t cs[Q_MC * Q_NC];
+    /* packed panels (B: [jr block][kk][NR], A: [ir block][kk][MR]) and the
+     * i64 C-scratch: the reference keeps them on the stack (alloca) */
+    int32_t bp[Q_KC * Q_NC] __attribute__((aligned(64)));
+    int32_t ap[Q_MC * Q_KC] __attribute__((aligned(64)));
+    int64_t cs[Q_MC * Q_NC] __attribute__((aligned(64)));
     for (int64_t jc = 0; jc < n; jc += Q_NC) {
         const int64_t nc = n - jc < Q_NC ? n - jc : Q_NC;
+        const int64_t ncp = (nc + Q_NR - 1) / Q_NR * Q_NR;
         for (int64_t ic = ba->r0; ic < ba->r1; ic += Q_MC) {
             const int64_t mc = ba->r1 - ic < Q_MC ? ba->r1 - ic : Q_MC;
+            const int64_t mcp = (mc + Q_MR - 1) / Q_MR * Q_MR;
             memset(cs, 0, sizeof cs);
             for (int64_t pc = 0; pc < k; pc += Q_KC) {
                 const int64_t kc = k - pc < Q_KC ? k - pc : Q_KC;
-                for (int64_t kk = 0; kk < kc; ++kk)
-                    for (int64_t j = 0; j < Q_NC; ++j) bp[kk * Q_NC + j] = j < nc ? B[(pc + kk) * n + jc + j] : 0;
-                for (int64_t i = 0; i < Q_MC; ++i)
-                    for (int64_t kk = 0; kk < kc; ++kk) ap[i * Q_KC + kk] = i < mc ? A[(ic + i) * k + pc + kk] : 0;
-                for (int64_t jr = 0; jr < nc; jr += Q_NR)
-                    for (int64_t ir = 0; ir < mc; ir += Q_MR) {
-                        int64_t acc[Q_MR][Q_NR];
-                        memset(acc, 0, sizeof acc);
-                        for (int64_t kk = 0; kk < kc; ++kk)
-                            for (int r = 0; r < Q_MR; ++r) {
-                                const int64_t a = ap[(ir + r) * Q_KC + kk];
-                                for (int c = 0; c < Q_NR; ++c)
-                                    acc[r][c] += (a * (int64_t)bp[kk * Q_NC + jr + c]) >> 16;
-                            }
-                        for (int r = 0; r < Q_MR; ++r)
-                            for (int c = 0; c < Q_NR; ++c) cs[(ir + r) * Q_NC + jr + c] += acc[r][c];
+                for (int64_t jr = 0; jr < ncp; jr += Q_NR) {
+                    int32_t *d = bp + (jr / Q_NR) * kc * Q_NR;
+                    for (int64_t kk = 0; kk < kc; ++kk) {
+                        const int32_t *src = B + (pc + kk) * n + jc + jr;
+                        for (int64_t c = 0; c < Q_NR; ++c) d[kk * Q_NR + c] = jr + c < nc ? src[c] : 0;
                     }
+                }
+                for (int64_t ir = 0; ir < mcp; ir += Q_MR) {
+                    int32_t *d = ap + (ir / Q_MR) * kc * Q_MR;
+                    for (int64_t r = 0; r < Q_MR; ++r) {
+                        const int32_t *src = A + (ic + ir + r) * k + pc;
+                        const int ok = ir + r < mc;
+                        for (int64_t kk = 0; kk < kc; ++kk) d[kk * Q_MR + r] = ok ? src[kk] : 0;
+                    }
+                }
+                for (int64_t jr = 0; jr < ncp; jr += Q_NR)
+                    for (int64_t ir = 0; ir < mcp; ir += Q_MR)
+                        q16_micro(ap + (ir / Q_MR) * kc * Q_MR, bp + (jr / Q_NR) * kc * Q_NR, kc,
+                                  cs + ir * Q_NC + jr, Q_NC);
             }
             for (int64_t i = 0; i < mc; ++i)
                 for (int64_t j = 0; j < nc; ++j) C[(ic + i) * n + jc + j] = (int32_t)cs[i * Q_NC + j];
@@ -284,11 +345,26 @@ static void gemv_q16_band(void *p) {
     band_args *ba = (band_args *)p;
     const int32_t *W = (const int32_t *)ba->a, *x = (const int32_t *)ba->b;
     int32_t *y = (int32_t *)ba->c;
-    const int64_t k = ba->k;
+    const int64_t k = ba->k, kmain = k / 8 * 8;
     for (int64_t i = ba->r0; i < ba->r1; ++i) {
         const int32_t *w = W + i * k;
+        __m256i acc0 = _mm256_setzero_si256(), acc1 = _mm256_setzero_si256();
+        for (int64_t kk = 0; kk < kmain; kk += 8) {
+            const __m256i wv = _mm256_loadu_si256((const __m256i *)(w + kk));
+            const __m256i xv = _mm256_loadu_si256((const __m256i *)(x + kk));
+            const __m256i w0 = _mm256_cvtepi32_epi64(_mm256_castsi256_si128(wv));
+            const __m256i w1 = _mm256_cvtepi32_epi64(_mm256_extracti128_si256(wv, 1));
+            const __m256i x0 = _mm256_cvtepi32_epi64(_mm256_castsi256_si128(xv));
+            const __m256i x1 = _mm256_cvtepi32_epi64(_mm256_extracti128_si256(xv, 1));
+            acc0 = _mm256_add_epi64(acc0, sra16_epi64(_mm256_mul_epi32(w0, x0)));
+            acc1 = _mm256_add_epi64(acc1, sra16_epi64(_mm256_mul_epi32(w1, x1)));
+        }
+        int64_t lanes[8];
+        _mm256_storeu_si256((__m256i *)lanes, acc0);
+        _mm256_storeu_si256((__m256i *)(lanes + 4), acc1);
         int64_t acc = 0;
-        for (int64_t kk = 0; kk < k; ++kk) acc += ((int64_t)w[kk] * (int64_t)x[kk]) >> 16;
+        for (int l = 0; l < 8; ++l) acc += lanes[l];
+        for (int64_t kk = kmain; kk < k; ++kk) acc += ((int64_t)w[kk] * (int64_t)x[kk]) >> 16;
         y[i] = (int32_t)acc;
     }
 }

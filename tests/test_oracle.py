@@ -369,7 +369,7 @@ def test_cpu_mt_baseline_matches_oracle(threads):
     L = O.lib()
     L.det_cpu_set_threads(threads)
     try:
-        for (m, k, n) in [(1, 1, 1), (13, 77, 19), (70, 600, 150), (130, 1100, 40)]:
+        for (m, k, n) in [(1, 1, 1), (13, 77, 19), (70, 600, 150), (130, 1100, 40), (256, 256, 256), (67, 1030, 129)]:
             A, B = O.gen_i8(m * 31 + k, m * k, k * n)
             C = np.empty(m * n, np.int32)
             L.det_cpu_gemm_i8(A.ctypes.data, B.ctypes.data, C.ctypes.data, m, k, n)
