@@ -711,6 +711,18 @@ def main() -> int:
                           "gmac_per_s": round(t * 500.0, 1),
                           "frac": round(t / PEAK_INT8_TOPS, 4)}
         log(f"i8_8192: {r['ms'] * 1e3:.1f} us  {t:.1f} TOP/s")
+    # int8 off the headline shape: the reference's own sweep sizes (256, 512),
+    # a grid smaller than the chip (2048^3) and a ragged cube (4095^3, K and
+    # N off the 16-byte grid: operands repacked into padded panels)
+    for nn in (256, 512, 2048, 4095):
+        name = f"i8_{nn}"
+        if want(name):
+            log(f"{name}: det_matmul_i8 {nn}^3")
+            r = runs[name] = gemm_workload("i8", nn, nn, nn, K, W, stream, nn, check_rows=2)
+            t = r["ops"] / (r["ms"] * 1e-3) / 1e12
+            sec[name] = {"ms": round(r["ms"], 5), "value": round(t, 2), "unit": "TOP/s",
+                         "gmac_per_s": round(t * 500.0, 1), "frac": round(t / PEAK_INT8_TOPS, 4)}
+            log(f"{name}: {r['ms'] * 1e3:.1f} us  {t:.1f} TOP/s")
     result["secondary"] = sec
     stream.destroy()
     if args.host_abi:

@@ -194,7 +194,13 @@ int64_t det_fft_q16_dev(int64_t *re, int64_t *im, const int64_t *tw, int64_t log
 int64_t det_fft_q16_oop_dev(const int64_t *in_re, const int64_t *in_im, int64_t *out_re, int64_t *out_im,
                             const int64_t *tw, int64_t logn, int64_t n, int64_t batch, void *stream);
 int64_t det_fft_workspace_bytes(int64_t logn, int64_t batch);
-/* Workspace bytes op (DET_OP_*) needs at this shape (0 for int8). */
+/* Workspace bytes op (DET_OP_*) needs at this shape.  int8 needs one only
+ * when K or N is not a multiple of 16: its operands are then repacked into
+ * aligned zero-padded panels of Mp*Kp + Kp*Np bytes (M, K, N rounded up to
+ * 256).  int8 operands that are not 16-byte aligned are repacked the same
+ * way when the workspace given holds that size.  For int8 the workspace is
+ * optional: without it such operands run a slower byte-load kernel;
+ * det_matmul_ws_dev rejects a short workspace only for int16 / Q16. */
 int64_t det_workspace_bytes(int64_t op, int64_t m, int64_t k, int64_t n);
 int64_t det_matmul_ws_dev(int64_t op, const void *a, const void *b, int32_t *c, int64_t m, int64_t k, int64_t n,
                           void *ws, int64_t ws_bytes, void *stream);

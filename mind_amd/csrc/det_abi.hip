@@ -178,7 +178,7 @@ int64_t gemm_dev(Op op, const void *A, const void *B, void *C, int64_t m, int64_
     const int M = (int)m, N = (int)n, K = (int)k;
     if (K == 0) DET_HIP_CHECK(zero_i32((int32_t *)C, (size_t)m * n, s));
     else if (op == Op::I8)
-        DET_HIP_CHECK(det::launch_gemm_i8((const int8_t *)A, (const int8_t *)B, (int32_t *)C, M, N, K, s));
+        DET_HIP_CHECK(det::launch_gemm_i8((const int8_t *)A, (const int8_t *)B, (int32_t *)C, M, N, K, ws, s));
     else if (op == Op::I16)
         DET_HIP_CHECK(det::launch_gemm_i16((const int16_t *)A, (const int16_t *)B, (int32_t *)C, M, N, K, ws, s));
     else
@@ -187,8 +187,14 @@ int64_t gemm_dev(Op op, const void *A, const void *B, void *C, int64_t m, int64_
     return 0;
 }
 
-size_t ws_need(Op op, int64_t m, int64_t k, int64_t n) {
-    if (op == Op::I8 || k == 0) return 0;
+bool aligned16(const void *a, const void *b) { return (((uintptr_t)a | (uintptr_t)b) & 15) == 0; }
+
+// Workspace bytes of one GEMM.  int8 needs one only for operands off the
+// 16-byte grid (repacked into padded panels), which depends on the operand
+// addresses; NULL operands are taken as aligned.
+size_t ws_need(Op op, int64_t m, int64_t k, int64_t n, const void *A = nullptr, const void *B = nullptr) {
+    if (k == 0) return 0;
+    if (op == Op::I8) return det::i8_workspace_bytes((int)m, (int)n, (int)k, aligned16(A, B));
     return op == Op::I16 ? det::i16_workspace_bytes((int)m, (int)n, (int)k)
                          : det::q16_workspace_bytes((int)m, (int)n, (int)k);
 }
@@ -200,7 +206,7 @@ int64_t gemm_dev_arena(Op op, const void *A, const void *B, void *C, int64_t m, 
     if (bad_dims(m, k, n)) return set_err(DET_ERR_ARG, "dimension out of range [0, 2^31)");
     if (m == 0 || n == 0) return 0;
     if (!A || !B || !C) return set_err(DET_ERR_ARG, "null device pointer");
-    const size_t need = ws_need(op, m, k, n);
+    const size_t need = ws_need(op, m, k, n, A, B);
     if (need == 0) return gemm_dev(op, A, B, C, m, k, n, nullptr, s);
     int64_t rc = 0;
     const int d = cur_device(&rc);
@@ -581,6 +587,7 @@ int64_t det_matmul_q16_dev(const int32_t *a, const int32_t *b, int32_t *c, int64
 
 int64_t det_workspace_bytes(int64_t op, int64_t m, int64_t k, int64_t n) {
     if (bad_dims(m, k, n) || m == 0 || n == 0) return 0;
+    if (op == DET_OP_I8) return (int64_t)ws_need(Op::I8, m, k, n);
     if (op == DET_OP_I16) return (int64_t)ws_need(Op::I16, m, k, n);
     if (op == DET_OP_Q16) return (int64_t)ws_need(Op::Q16, m, k, n);
     return 0;
@@ -596,9 +603,12 @@ int64_t det_matmul_ws_dev(int64_t op, const void *a, const void *b, int32_t *c, 
     else if (op == DET_OP_I16) o = Op::I16;
     else if (op == DET_OP_Q16) o = Op::Q16;
     else return set_err(DET_ERR_ARG, "unknown op");
-    if (ws_bytes < 0 || (size_t)ws_bytes < ws_need(o, m, k, n) || (ws_need(o, m, k, n) && !ws))
-        return set_err(DET_ERR_ARG, "workspace too small (see det_workspace_bytes)");
-    return gemm_dev(o, a, b, c, m, k, n, ws, (hipStream_t)stream);
+    const size_t need = ws_need(o, m, k, n, a, b);
+    const bool enough = ws_bytes >= 0 && (size_t)ws_bytes >= need && (need == 0 || ws);
+    // int8 runs without a workspace too (operands off the 16-byte grid then
+    // take the byte-load kernel); the limb GEMMs cannot
+    if (!enough && o != Op::I8) return set_err(DET_ERR_ARG, "workspace too small (see det_workspace_bytes)");
+    return gemm_dev(o, a, b, c, m, k, n, enough ? ws : nullptr, (hipStream_t)stream);
 }
 
 int64_t det_gemv_q16_dev(const int32_t *w, const int32_t *x, int32_t *y, int64_t m, int64_t k, int64_t nb,

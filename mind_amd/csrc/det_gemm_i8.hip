@@ -275,11 +275,16 @@ struct I16Epi {
 // compile-time offset and the DMA advances through its SGPR soffset: the
 // loop issues almost no VALU besides the MFMAs (VALU and MFMA work of one
 // SIMD do not overlap on gfx950).
-template <int EPI, bool FULL>
+// EPI_I8 stores C[row][col] at C + row * ldc + col for row < mst, col < nst
+// (ldc = nst = N, mst = M, except for operands repacked into padded panels:
+// see launch_gemm_i8); MASK = false: every row and column of the tile is
+// stored (full tiles of an unpadded problem).
+template <int EPI, bool FULL, bool MASK = !FULL>
 __global__ __launch_bounds__(THREADS, 1) void gemm_i8_dma_kernel(const int8_t *__restrict__ A,
                                                                  const int8_t *__restrict__ B,
                                                                  int32_t *__restrict__ C, int M, int N, int K,
-                                                                 int tiles_m, int tiles_n, I16Epi e16) {
+                                                                 int tiles_m, int tiles_n, int ldc, int mst, int nst,
+                                                                 I16Epi e16) {
     __shared__ __attribute__((aligned(1024))) int8_t smem[NSTAGE][2][TILE_BYTES];
 
     const int ntiles = tiles_m * tiles_n;
@@ -538,12 +543,12 @@ __global__ __launch_bounds__(THREADS, 1) void gemm_i8_dma_kernel(const int8_t *_
 #pragma unroll
             for (int r = 0; r < 16; ++r) {
                 const int row = m0 + wm + i * 32 + 8 * (r >> 2) + 4 * lh + (r & 3);
-                if (!FULL && row >= M) continue;   // full tiles: always inside
-                int32_t *crow = C + (size_t)row * N;
+                if (MASK && row >= mst) continue;
+                int32_t *crow = C + (size_t)row * ldc;
 #pragma unroll
                 for (int j = 0; j < 2; ++j) {
                     const int col = n0 + wn + j * 32 + l32;
-                    if (FULL || col < N) __builtin_nontemporal_store(acc[i][j][r], crow + col);
+                    if (!MASK || col < nst) __builtin_nontemporal_store(acc[i][j][r], crow + col);
                 }
             }
         }
@@ -622,15 +627,18 @@ __global__ __launch_bounds__(THREADS, 1) void gemm_i8_dma_kernel(const int8_t *_
 // swz_b), so every barrier slot again carries 16 MFMAs per wave; 3 stages
 // (144 KiB) with the DMA two steps ahead.  Full shapes only: M % 128 == 0,
 // N % 256 == 0, K % 128 == 0, K > 0, operands below 2^31 bytes, aligned.
+// C: row stride ldc, rows below mst and columns below nst stored.
 namespace h128 {
 constexpr int BM = 128, WM = 64, MI = 2, SUB = 2, NST = 3, KS = BK * SUB;
 constexpr int A_BYTES = BM * BK, B_BYTES = BK * BN, SS = A_BYTES + B_BYTES, ST = SUB * SS;
 constexpr int DPS = SUB * 3;   // DMA instructions per wave per stage: 1 A + 2 B per sub-stage
 
+template <bool MASK>
 __global__ __launch_bounds__(THREADS, 1) void gemm_i8_h128_kernel(const int8_t *__restrict__ A,
                                                                   const int8_t *__restrict__ B,
                                                                   int32_t *__restrict__ C, int M, int N, int K,
-                                                                  int tiles_m, int tiles_n) {
+                                                                  int tiles_m, int tiles_n, int ldc, int mst,
+                                                                  int nst) {
     __shared__ __attribute__((aligned(1024))) int8_t smem[NST * ST];
 
     const int ntiles = tiles_m * tiles_n;
@@ -801,9 +809,12 @@ __global__ __launch_bounds__(THREADS, 1) void gemm_i8_h128_kernel(const int8_t *
 #pragma unroll
         for (int r = 0; r < 16; ++r) {
             const int row = m0 + wm + i * 32 + 8 * (r >> 2) + 4 * lh + (r & 3);
-            int32_t *crow = C + (size_t)row * N + n0 + wn + l32;
+            if (MASK && row >= mst) continue;
+            const int col = n0 + wn + l32;
+            int32_t *crow = C + (size_t)row * ldc + col;
 #pragma unroll
-            for (int j = 0; j < 2; ++j) __builtin_nontemporal_store(acc[i][j][r], crow + j * 32);
+            for (int j = 0; j < 2; ++j)
+                if (!MASK || col + j * 32 < nst) __builtin_nontemporal_store(acc[i][j][r], crow + j * 32);
         }
 }
 }  // namespace h128
@@ -822,28 +833,121 @@ static int cu_count() {
     return cached[d];
 }
 
-hipError_t launch_gemm_i8(const int8_t *A, const int8_t *B, int32_t *C, int M, int N, int K, hipStream_t s) {
+// ------------------------------------------------------- ragged operands
+// Shapes off the 16-byte grid (K or N not a multiple of 16) and operands
+// not 16-byte aligned cannot be moved by whole 16-byte chunks: rows start at
+// unaligned offsets, and a chunk that runs past the end of a buffer cannot be
+// range-checked byte by byte.  Such operands are repacked once into
+// zero-padded, aligned panels A' [Mp][Kp] and B' [Kp][Np] (M, K, N rounded
+// up to 256) in the workspace, and the full-tile kernels run on those with
+// C's own row stride and row / column bounds.  The padding is zero on both sides of
+// every product, so C is unchanged.  One launch for both operands
+// (blockIdx.z); each thread writes 16 bytes of a panel row.  Where the 20
+// dword-aligned bytes covering its 16 source bytes lie inside the source
+// buffer it reads those (one 16-byte and one 4-byte load) and funnel-shifts
+// them (v_alignbyte); at the two ends of the buffer it reads single bytes,
+// so no load leaves the source buffer.
+__global__ __launch_bounds__(256) void pad_i8_kernel(const int8_t *__restrict__ A, const int8_t *__restrict__ B,
+                                                     int M, int N, int K, int Mp, int Kp, int Np,
+                                                     uint4 *__restrict__ Ap, uint4 *__restrict__ Bp) {
+    const bool is_b = blockIdx.z != 0;
+    const int8_t *src = is_b ? B : A;
+    uint4 *dst = is_b ? Bp : Ap;
+    const int rows = is_b ? K : M, rows_out = is_b ? Kp : Mp, cols = is_b ? N : K, dcols = is_b ? Np : Kp;
+    const long long total = (long long)rows * cols;
+    const int c0 = (blockIdx.x * 256 + threadIdx.x) * 16;
+    if (c0 >= dcols) return;
+    for (int row = blockIdx.y; row < rows_out; row += gridDim.y) {
+        uint32_t w[4] = {0, 0, 0, 0};
+        if (row < rows && c0 < cols) {
+            const long long p = (long long)row * cols + c0;
+            const uintptr_t base = (uintptr_t)src, at = base + (uintptr_t)p, a = at & ~(uintptr_t)3;
+            if (c0 + 16 <= cols && a >= base && a + 20 <= base + (uintptr_t)total) {
+                // one 16-byte load (dword-aligned) and the dword after it
+                const uint4 q = *(const uint4 *)a;
+                const uint32_t v[5] = {q.x, q.y, q.z, q.w, *(const uint32_t *)(a + 16)};
+                const uint32_t sh = (uint32_t)(at & 3);
+#pragma unroll
+                for (int i = 0; i < 4; ++i) w[i] = __builtin_amdgcn_alignbyte(v[i + 1], v[i], sh);
+            } else {
+                const int nv = min(16, cols - c0);
+                for (int e = 0; e < nv; ++e) w[e >> 2] |= (uint32_t)(uint8_t)src[p + e] << (8 * (e & 3));
+            }
+        }
+        dst[((long long)row * dcols + c0) >> 4] = make_uint4(w[0], w[1], w[2], w[3]);
+    }
+}
+
+static bool i8_fast(const int8_t *A, const int8_t *B, int M, int N, int K) {
+    return (K % 16 == 0) && (N % 16 == 0) && (((uintptr_t)A & 15) == 0) && (((uintptr_t)B & 15) == 0) &&
+           (size_t)M * K < 0x80000000ull && (size_t)K * N < 0x80000000ull;
+}
+
+// Workspace of the repack path: 0 when the operands go to the kernels as
+// they are (16-byte grid, or panels beyond the buffer fast paths' 2 GiB).
+static inline size_t round256(size_t x) { return (x + 255) / 256 * 256; }
+size_t i8_workspace_bytes(int M, int N, int K, bool aligned) {
+    const size_t Mp = round256(M), Kp = round256(K), Np = round256(N);
+    const bool grid16 = K % 16 == 0 && N % 16 == 0 && aligned;
+    if (grid16 || K == 0 || Mp * Kp >= 0x80000000ull || Kp * Np >= 0x80000000ull) return 0;
+    return Mp * Kp + Kp * Np;
+}
+
+// Operands on the 16-byte grid: pick the kernel; C has row stride ldc and
+// rows < mst, columns < nst are stored (masked only when that is not the
+// whole M x N).
+static void launch_i8_on_grid(const int8_t *A, const int8_t *B, int32_t *C, int M, int N, int K, int ldc, int mst,
+                              int nst, hipStream_t s) {
+    const bool mask = mst != M || nst != N || ldc != N;
     using namespace i8g;
     const int tiles_m = (M + BM - 1) / BM, tiles_n = (N + BN - 1) / BN;
     const dim3 grid(tiles_m * tiles_n), block(THREADS);
-    const bool fast = (K % 16 == 0) && (N % 16 == 0) && (((uintptr_t)A & 15) == 0) && (((uintptr_t)B & 15) == 0) &&
-                      (size_t)M * K < 0x80000000ull && (size_t)K * N < 0x80000000ull;
-    const bool full = fast && K > 0 && M % BM == 0 && N % BN == 0 && K % (BK * NSTAGE) == 0;
-    const bool full128 = fast && K > 0 && M % h128::BM == 0 && N % BN == 0 && K % h128::KS == 0;
+    const bool full = K > 0 && M % BM == 0 && N % BN == 0 && K % (BK * NSTAGE) == 0;
+    const bool full128 = K > 0 && M % h128::BM == 0 && N % BN == 0 && K % h128::KS == 0;
     // 128-row tiles when 256 x 256 tiles would not fill more than one round
     // of the chip (or do not fit the shape)
     if (full128 && (!full || tiles_m * tiles_n <= cu_count())) {
         const int tm128 = M / h128::BM;
-        hipLaunchKernelGGL(h128::gemm_i8_h128_kernel, dim3(tm128 * tiles_n), block, 0, s, A, B, C, M, N, K, tm128,
-                           tiles_n);
-    } else if (full)
-        hipLaunchKernelGGL((gemm_i8_dma_kernel<EPI_I8, true>), grid, block, 0, s, A, B, C, M, N, K, tiles_m, tiles_n,
-                           I16Epi{});
-    else if (fast)
+        if (mask)
+            hipLaunchKernelGGL(h128::gemm_i8_h128_kernel<true>, dim3(tm128 * tiles_n), block, 0, s, A, B, C, M, N, K,
+                               tm128, tiles_n, ldc, mst, nst);
+        else
+            hipLaunchKernelGGL(h128::gemm_i8_h128_kernel<false>, dim3(tm128 * tiles_n), block, 0, s, A, B, C, M, N, K,
+                               tm128, tiles_n, ldc, mst, nst);
+    } else if (full) {
+        if (mask)
+            hipLaunchKernelGGL((gemm_i8_dma_kernel<EPI_I8, true, true>), grid, block, 0, s, A, B, C, M, N, K, tiles_m,
+                               tiles_n, ldc, mst, nst, I16Epi{});
+        else
+            hipLaunchKernelGGL((gemm_i8_dma_kernel<EPI_I8, true, false>), grid, block, 0, s, A, B, C, M, N, K, tiles_m,
+                               tiles_n, ldc, mst, nst, I16Epi{});
+    } else {
         hipLaunchKernelGGL((gemm_i8_dma_kernel<EPI_I8, false>), grid, block, 0, s, A, B, C, M, N, K, tiles_m, tiles_n,
-                           I16Epi{});
-    else
-        hipLaunchKernelGGL(gemm_i8_kernel<false>, grid, block, 0, s, A, B, C, M, N, K, tiles_m, tiles_n);
+                           ldc, mst, nst, I16Epi{});
+    }
+}
+
+hipError_t launch_gemm_i8(const int8_t *A, const int8_t *B, int32_t *C, int M, int N, int K, void *ws,
+                          hipStream_t s) {
+    using namespace i8g;
+    const bool aligned = (((uintptr_t)A & 15) == 0) && (((uintptr_t)B & 15) == 0);
+    const size_t pad = i8_workspace_bytes(M, N, K, aligned);
+    if (i8_fast(A, B, M, N, K)) {
+        launch_i8_on_grid(A, B, C, M, N, K, N, M, N, s);
+    } else if (pad && ws) {
+        const int Mp = (int)round256(M), Kp = (int)round256(K), Np = (int)round256(N);
+        int8_t *Ap = (int8_t *)ws;
+        int8_t *Bp = Ap + (size_t)Mp * Kp;
+        const int wide = Kp > Np ? Kp : Np, tall = Mp > Kp ? Mp : Kp;
+        const dim3 pgrid((unsigned)((wide / 16 + 255) / 256), (unsigned)(tall < 65535 ? tall : 65535), 2);
+        hipLaunchKernelGGL(pad_i8_kernel, pgrid, dim3(256), 0, s, A, B, M, N, K, Mp, Kp, Np, (uint4 *)Ap,
+                           (uint4 *)Bp);
+        launch_i8_on_grid(Ap, Bp, C, Mp, Np, Kp, N, M, N, s);
+    } else {
+        const int tiles_m = (M + BM - 1) / BM, tiles_n = (N + BN - 1) / BN;
+        hipLaunchKernelGGL(gemm_i8_kernel<false>, dim3(tiles_m * tiles_n), dim3(THREADS), 0, s, A, B, C, M, N, K,
+                           tiles_m, tiles_n);
+    }
     return hipGetLastError();
 }
 
@@ -859,10 +963,10 @@ hipError_t launch_gemm_i8_i16epi(const int8_t *A2, const int8_t *B2, int M2, int
     const bool full = Kp > 0 && M2 % BM == 0 && N2 % BN == 0 && Kp % (BK * NSTAGE) == 0;
     if (full)
         hipLaunchKernelGGL((gemm_i8_dma_kernel<EPI_I16, true>), dim3(tiles_m * tiles_n), dim3(THREADS), 0, s, A2, B2,
-                           (int32_t *)nullptr, M2, N2, Kp, tiles_m, tiles_n, e);
+                           (int32_t *)nullptr, M2, N2, Kp, tiles_m, tiles_n, N2, M2, N2, e);
     else
         hipLaunchKernelGGL((gemm_i8_dma_kernel<EPI_I16, false>), dim3(tiles_m * tiles_n), dim3(THREADS), 0, s, A2, B2,
-                           (int32_t *)nullptr, M2, N2, Kp, tiles_m, tiles_n, e);
+                           (int32_t *)nullptr, M2, N2, Kp, tiles_m, tiles_n, N2, M2, N2, e);
     return hipGetLastError();
 }
 

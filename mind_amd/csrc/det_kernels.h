@@ -14,8 +14,14 @@ namespace det {
 // partials per column ([ncs][N], ncs <= MAX_CS); the GEMM epilogues add them.
 constexpr int MAX_CS = 16;
 
-// C[M,N] (i32) = A[M,K] (i8) * B[K,N] (i8)
-hipError_t launch_gemm_i8(const int8_t *A, const int8_t *B, int32_t *C, int M, int N, int K, hipStream_t s);
+// C[M,N] (i32) = A[M,K] (i8) * B[K,N] (i8).  Shapes off the 16-byte grid (K
+// or N not a multiple of 16, operands not 16-byte aligned) repack the
+// operands into `ws`, which must then hold i8_workspace_bytes(M, N, K,
+// aligned) bytes (0 on the grid; with ws == NULL they take the byte-load
+// kernel instead).
+size_t i8_workspace_bytes(int M, int N, int K, bool aligned);
+hipError_t launch_gemm_i8(const int8_t *A, const int8_t *B, int32_t *C, int M, int N, int K, void *ws,
+                          hipStream_t s);
 
 // Workspace (device bytes) the limb GEMMs need: operand limb planes, low-16
 // halves (Q16) and exact row / column sums.

@@ -69,7 +69,17 @@ extern "C" int64_t det_matmul_scratch_dev(int64_t op, const void *a, const void 
         return 0;
     }
     if (op == DET_OP_I8) {
-        DET_HIP_CHECK(det::launch_gemm_i8((const int8_t *)a, (const int8_t *)b, c, M, N, K, s));
+        // int8 uses the scratch only for operands off the 16-byte grid (the
+        // repack into padded panels); beyond the scratch it takes the
+        // byte-load kernel, which needs no workspace
+        const bool aligned = (((uintptr_t)a | (uintptr_t)b) & 15) == 0;
+        const size_t need8 = det::i8_workspace_bytes(M, N, K, aligned);
+        void *ws8 = nullptr;
+        if (need8 && need8 <= (size_t)DET_SCRATCH_BYTES) {
+            const int64_t rc = scratch_on_current_device(&ws8);
+            if (rc) return rc;
+        }
+        DET_HIP_CHECK(det::launch_gemm_i8((const int8_t *)a, (const int8_t *)b, c, M, N, K, ws8, s));
         return 0;
     }
     const size_t need = op == DET_OP_I16 ? det::i16_workspace_bytes(M, N, K) : det::q16_workspace_bytes(M, N, K);

@@ -142,3 +142,43 @@ def test_h128_tile_dma_stays_inside_operands(M, N, K):
 def test_edge_tile_dma_stays_inside_operands(M, N, K):
     assert K % 16 == 0 and N % 16 == 0
     assert _edge_addresses(M, N, K) <= 0
+
+
+def _pad_row_chunks(src, base, rows, cols, dcols):
+    """pad_i8_kernel's reads for one operand, restated: returns the padded
+    panel it writes and checks every load stays inside the source buffer.
+    `src` is the buffer's bytes, `base` its address modulo 4."""
+    total = rows * cols
+    out = np.zeros((rows, dcols), np.uint8)
+    for row in range(rows):
+        for c0 in range(0, dcols, 16):
+            if c0 >= cols:
+                continue
+            p = row * cols + c0
+            at = base + p
+            a = at & ~3
+            if c0 + 16 <= cols and a >= base and a + 20 <= base + total:
+                lo = a - base
+                assert 0 <= lo and lo + 20 <= total
+                v = src[lo:lo + 20].view("<u4").astype(np.uint64)
+                sh = at & 3
+                w = [int((((v[i + 1] << np.uint64(32)) | v[i]) >> np.uint64(8 * sh)) & np.uint64(0xFFFFFFFF))
+                     for i in range(4)]
+                out[row, c0:c0 + 16] = np.array(w, "<u4").view(np.uint8)
+            else:
+                nv = min(16, cols - c0)
+                assert 0 <= p and p + nv <= total
+                out[row, c0:c0 + nv] = src[p:p + nv]
+    return out
+
+
+@pytest.mark.parametrize("rows,cols", [(1, 1), (3, 17), (5, 33), (7, 4095), (2, 64), (4, 20)])
+@pytest.mark.parametrize("base", [0, 1, 2, 3])
+def test_pad_kernel_reads_stay_inside_and_assemble_the_rows(rows, cols, base):
+    rng = np.random.default_rng(rows * 131 + cols + base)
+    src = rng.integers(0, 256, rows * cols, dtype=np.uint8)
+    dcols = (cols + 15) // 16 * 16
+    got = _pad_row_chunks(src, base, rows, cols, dcols)
+    want = np.zeros((rows, dcols), np.uint8)
+    want[:, :cols] = src.reshape(rows, cols)
+    np.testing.assert_array_equal(got, want)

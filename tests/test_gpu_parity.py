@@ -630,6 +630,50 @@ def test_gemm_i8_h128_wraps_mod_2_32():
     assert got[0, 0] == np.int32(np.uint32((k * 16384) % (1 << 32)).astype(np.int32))
 
 
+# Operands off the 16-byte grid (K or N not a multiple of 16) or not 16-byte
+# aligned: repacked into padded panels in the workspace (arena, caller
+# workspace or scratch), or, without a workspace, the byte-load kernel.
+RAGGED_I8 = [(1, 17, 1), (37, 100, 53), (300, 1000, 77), (256, 4095, 256), (1000, 1000, 1000), (257, 4100, 1003),
+             (64, 64, 64), (256, 256, 256)]
+
+
+def _offset_buffer(a, off):
+    """A device buffer holding `a` at byte offset `off` (a misaligned operand)."""
+    buf = M.DeviceBuffer(a.nbytes + 64)
+    M.check(M.lib().det_memcpy_htod(buf.ptr + off, a.ctypes.data, a.nbytes))
+    return buf
+
+
+@pytest.mark.parametrize("m,k,n", RAGGED_I8, ids=[f"{m}x{k}x{n}" for m, k, n in RAGGED_I8])
+@pytest.mark.parametrize("offs", [(0, 0), (1, 3), (8, 4)], ids=["aligned", "off1_3", "off8_4"])
+def test_gemm_i8_ragged_and_misaligned_device_operands(m, k, n, offs):
+    a, b = O.gen_i8(0xA11 ^ (m * 7 + k * 3 + n), m * k, k * n)
+    want = O.gemm_i8(a, b, m, k, n).reshape(m, n)
+    da, db = _offset_buffer(a, offs[0]), _offset_buffer(b, offs[1])
+    pa, pb = da.ptr + offs[0], db.ptr + offs[1]
+    dc = M.DeviceBuffer(m * n * 4)
+    s = M.Stream()
+    L = M.lib()
+    # the library arena (sized for these addresses), a caller workspace of the
+    # reported size (enough only for aligned operands), and none at all
+    ws_bytes = L.det_workspace_bytes(M.DET_OP_I8, m, k, n)
+    ws = M.DeviceBuffer(max(ws_bytes, 256))
+    for how in ("arena", "ws", "no_ws"):
+        dc.fill(0xA5)
+        note(f"int8 {m}x{k}x{n} offsets {offs} via {how} (reported ws {ws_bytes})")
+        if how == "arena":
+            M.check(L.det_matmul_i8_dev(pa, pb, dc.ptr, m, k, n, s.ptr))
+        elif how == "ws":
+            M.check(L.det_matmul_ws_dev(M.DET_OP_I8, pa, pb, dc.ptr, m, k, n, ws.ptr, ws_bytes, s.ptr))
+        else:
+            M.check(L.det_matmul_ws_dev(M.DET_OP_I8, pa, pb, dc.ptr, m, k, n, None, 0, s.ptr))
+        s.sync()
+        np.testing.assert_array_equal(dc.to_array(np.int32, (m, n)), want)
+    s.destroy()
+    for buf in (da, db, dc, ws):
+        buf.free()
+
+
 def test_gemm_i8_k_zero_and_empty():
     note("det_matmul_i8 k=0")
     np.testing.assert_array_equal(M.det_matmul_i8(np.zeros((5, 0), np.int8), np.zeros((0, 7), np.int8)),
