@@ -220,10 +220,12 @@ int64_t det_matmul_scratch_dev(int64_t op, const void *a, const void *b, int32_t
 /* Runtime helpers (thin wrappers over HIP, so a caller needs no HIP headers). */
 /* Release the library's per-device state (its stream, event, host-call
  * staging buffer and workspace arena) after waiting for the work queued on
- * them; later calls recreate what they need.  The same teardown runs at
- * dlclose and at process exit, as the reference joins its thread pool at
- * unload (runtime-support/mind_intrinsics.c:2066-2080).  No other call of the
- * library may be in flight. */
+ * them; later calls recreate what they need.  The reference joins its thread
+ * pool at unload (runtime-support/mind_intrinsics.c:2066-2080); here the
+ * release is explicit: a caller that unloads the library calls det_shutdown()
+ * before dlclose (an exit hook would run HIP calls during process exit, which
+ * abort under tools that intercept HIP).  No other call of the library may be
+ * in flight. */
 int64_t det_shutdown(void);
 const char *det_last_error(void);
 const char *det_version(void);

@@ -33,9 +33,9 @@
 namespace {
 
 // Last error text of this thread.  A plain buffer, not a std::string: a
-// thread_local object with a destructor would keep the library loaded at
+// thread_local object with a destructor keeps the library loaded after
 // dlclose (the C runtime holds a DSO while it has pending thread-local
-// destructors), and the unload teardown below would never run.
+// destructors), so its code object and device globals would stay resident.
 thread_local char g_err[512];
 
 void put_err(const char *a, const char *b = nullptr) {
@@ -93,15 +93,7 @@ int64_t ensure(void **buf, size_t *have, size_t need) {
     return 0;
 }
 
-void teardown_at_unload();
-
 int64_t ensure_stream(DevState &d) {
-    // The first resource the library creates registers the teardown.  It is
-    // registered after the HIP runtime has initialised (this call is past a
-    // HIP call), so at process exit it runs before the runtime's own exit
-    // handlers; atexit from a shared object also runs at its dlclose.
-    static std::once_flag registered;
-    std::call_once(registered, [] { atexit(teardown_at_unload); });
     if (!d.stream) DET_HIP_CHECK(hipStreamCreateWithFlags(&d.stream, hipStreamNonBlocking));
     if (!d.ws_free) DET_HIP_CHECK(hipEventCreateWithFlags(&d.ws_free, hipEventDisableTiming));
     return 0;
@@ -145,10 +137,6 @@ int64_t release_all() {
     return rc;
 }
 
-// Library teardown at dlclose / exit (the reference joins its thread pool at
-// unload the same way, runtime-support/mind_intrinsics.c:2066-2080).  Runs
-// single-threaded: no call of this library may be in flight.
-void teardown_at_unload() { (void)release_all(); }
 
 bool bad_dims(int64_t m, int64_t k, int64_t n) {
     return m < 0 || k < 0 || n < 0 || m > DIM_MAX || k > DIM_MAX || n > DIM_MAX;
@@ -692,6 +680,12 @@ int64_t det_dot_dev(int64_t op, const void *a, const void *b, int64_t len, int32
 }
 
 // ---------------------------------------------------------------- runtime
+// Teardown (the reference joins its thread pool at unload,
+// runtime-support/mind_intrinsics.c:2066-2080).  Explicit, not an exit or
+// unload hook: a handler that an atexit from this library registers runs at
+// process exit as well as at dlclose, and HIP calls made during process exit
+// abort under tools that intercept HIP (a profiler's per-thread state is
+// gone by then).  Callers that unload the library call it before dlclose.
 int64_t det_shutdown(void) { return release_all(); }
 const char *det_last_error(void) { return g_err; }
 const char *det_version(void) { return "mind-det-mi355x 0.1 (gfx950)"; }

@@ -630,6 +630,9 @@ __global__ __launch_bounds__(THREADS, 1) void gemm_i8_dma_kernel(const int8_t *_
 // C: row stride ldc, rows below mst and columns below nst stored.
 namespace h128 {
 constexpr int BM = 128, WM = 64, MI = 2, SUB = 2, NST = 3, KS = BK * SUB;
+// groups of 8 row tiles (1024 rows, as the 256-row kernel's groups of 4):
+// each XCD's share of a 4096^3 grid then reads 4 MiB of A and 8 MiB of B
+constexpr int GROUP_M = 8;
 constexpr int A_BYTES = BM * BK, B_BYTES = BK * BN, SS = A_BYTES + B_BYTES, ST = SUB * SS;
 constexpr int DPS = SUB * 3;   // DMA instructions per wave per stage: 1 A + 2 B per sub-stage
 

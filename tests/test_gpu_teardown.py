@@ -2,15 +2,15 @@
 dlclose, runtime-support/mind_intrinsics.c:2066-2080).
 
 A fresh child process loads libmind_det_hip.so, makes a host-pointer call
-that grows the library's staging buffer (and its stream / event), and
-unloads it again, 20 times, reading the device's free memory (hipMemGetInfo,
-through the HIP runtime directly) with the library loaded after the call and
-again after dlclose.  The library must be gone from the process after every
-dlclose, each dlclose must give the 128+ MiB staging buffer back, and the
-level after dlclose must stay flat from round to round: without the teardown
-each round would leave its staging buffer behind.  (The first kernel launch
-in a process costs the HIP runtime a one-time ~150 MiB of its own, which the
-first round's figure includes.)
+that grows the library's staging buffer (and its stream / event), releases
+the library's state with det_shutdown() and unloads it, 20 times, reading the
+device's free memory (hipMemGetInfo, through the HIP runtime directly) with
+the library loaded after the call and again after det_shutdown + dlclose.
+The library must be gone from the process after every dlclose, each round
+must give the 128+ MiB staging buffer back, and the level must stay flat from
+round to round: without the teardown each round would leave its staging
+buffer behind.  (The first kernel launch in a process costs the HIP runtime a
+one-time ~150 MiB of its own, which the first round's figure includes.)
 """
 import os
 import subprocess
@@ -47,6 +47,8 @@ for it in range(20):
         first = y.copy()
     assert (y == first).all()
     held = free_mem()
+    L.det_shutdown.restype = ctypes.c_int64
+    assert L.det_shutdown() == 0
     handle = L._handle
     del f, L
     _ctypes.dlclose(handle)
@@ -60,7 +62,7 @@ for it in range(20):
 
 @pytest.mark.gpu
 def test_unload_releases_device_memory():
-    print("[teardown] 20x load / det_gemv_q16 2048x16384 / dlclose in a child", flush=True)
+    print("[teardown] 20x load / det_gemv_q16 2048x16384 / det_shutdown / dlclose in a child", flush=True)
     r = subprocess.run([sys.executable, "-c", CHILD, mind_amd.LIB_PATH], capture_output=True, text=True,
                        timeout=240)
     print(r.stdout[-3000:], r.stderr[-3000:], flush=True)
@@ -71,7 +73,7 @@ def test_unload_releases_device_memory():
             held.append(int(line.split("loaded ")[1].split(" MiB")[0]))
             after.append(int(line.split("after dlclose ")[1].split(" MiB")[0]))
     assert len(after) == 20
-    # each dlclose returns the 128 MiB staging buffer (and more)
+    # each det_shutdown + dlclose returns the 128 MiB staging buffer (and more)
     assert all(h - a >= 128 for h, a in zip(held, after)), list(zip(held, after))
     # and nothing accumulates: a leaked staging buffer would add 128 MiB a round
     assert max(after) - min(after) < 32, after
