@@ -438,19 +438,23 @@ def cpu_baseline_int8(A: np.ndarray, B: np.ndarray, C_gpu: np.ndarray, m: int, k
     t, _ = run(probe)
     rows = int(min(m, max(probe, (budget_s / 3) / max(t, 1e-6) * probe)))
     rows = max(probe, rows // 64 * 64)
+    # the whole workload may take well under the budget on a wide host:
+    # repeat it until the budget is spent (at least 3 calls) and take the median
     times = []
     c = None
-    for _ in range(3):
+    t_start = time.perf_counter()
+    while len(times) < 3 or (time.perf_counter() - t_start < budget_s and len(times) < 1000):
         dt, c = run(rows)
         times.append(dt)
     exact = bool(np.array_equal(c, C_gpu[:rows])) and bool(
         np.array_equal(c[[0, rows - 1]], O.gemm_i8_rows(A, B, m, k, n, [0, rows - 1])))
     if not exact:
         raise SystemExit("CPU baseline output differs from the GPU/oracle output")
-    med = sorted(times)[1]
+    med = sorted(times)[len(times) // 2]
     return {"value": 2.0 * rows * n * k / med / 1e12, "unit": "TOP/s", "cores": int(L.det_cpu_threads_for(rows)),
             "kind": "port",
-            "sample": f"rows 0..{rows - 1} of the 4096x4096x4096 int8 GEMM (median of 3, {med:.2f} s each); "
+            "sample": f"rows 0..{rows - 1} of the 4096x4096x4096 int8 GEMM (median of {len(times)} calls, "
+                      f"{med:.3f} s each, {sum(times):.1f} s in all); "
                       f"oracle/det_cpu_mt.c restatement of the reference MT BLIS int8 path, "
                       f"-O3 -march=x86-64-v3, output equal to the GPU rows",
             "host_cpus": os.cpu_count(), "cpu_model": _cpu_model()}
