@@ -614,20 +614,23 @@ __global__ __launch_bounds__(THREADS, 1) void gemm_i8_dma_kernel(const int8_t *_
 }
 // ------------------------------------------------------- 128 x 256 tiles
 // The same ping-pong schedule on a 128 x 256 C tile, for grids whose
-// 256 x 256 tiles would fill at most one round of the chip.  With one
-// 256 x 256 tile per CU every CU writes its 256 KiB of C at the same moment
-// at the end (64 MiB at 4096^3: ~9 us at HBM write speed, nothing left to
-// overlap it with); with 128-row tiles each CU runs two tiles in turn and
-// the first tile's stores drain while the second computes, and small grids
-// (2048^3: 64 tiles of 256^2) use twice as many CUs.  The price is a smaller
-// wave tile (64 x 64: 2 x 2 blocks of 32x32x32), a third more LDS bytes per
-// MFMA, so grids of several rounds stay on the 256 x 256 kernel.
+// 256 x 256 tiles would fill at most one round of the chip.  Small grids
+// (2048^3: 64 tiles of 256^2) use twice as many CUs, and at 4096^3 each CU
+// owns two tiles.  The price is a smaller wave tile (64 x 64: 2 x 2 blocks of
+// 32x32x32), a third more LDS bytes per MFMA, so grids of several rounds
+// stay on the 256 x 256 kernel.
 // A stage holds K = 128 as two 64-wide sub-stages, each laid out like a
 // stage of the 256 x 256 kernel (A [128][64] with swz_a, B [64][256] with
 // swz_b), so every barrier slot again carries 16 MFMAs per wave; 3 stages
 // (144 KiB) with the DMA two steps ahead.  Full shapes only: M % 128 == 0,
 // N % 256 == 0, K % 128 == 0, K > 0, operands below 2^31 bytes, aligned.
 // C: row stride ldc, rows below mst and columns below nst stored.
+//
+// Persistent: a workgroup walks tiles blockIdx.x, blockIdx.x + gridDim.x, ...
+// (gridDim.x a multiple of 8, so every tile of a workgroup stays on its XCD).
+// A finished tile's accumulators move to a second register set and its
+// stores are spread over the first HEAD K steps of the next tile, after each
+// step's DMA; only the last tile's stores are left exposed at the end.
 namespace h128 {
 constexpr int BM = 128, WM = 64, MI = 2, SUB = 2, NST = 3, KS = BK * SUB;
 // groups of 8 row tiles (1024 rows, as the 256-row kernel's groups of 4):
@@ -635,8 +638,32 @@ constexpr int BM = 128, WM = 64, MI = 2, SUB = 2, NST = 3, KS = BK * SUB;
 constexpr int GROUP_M = 8;
 constexpr int A_BYTES = BM * BK, B_BYTES = BK * BN, SS = A_BYTES + B_BYTES, ST = SUB * SS;
 constexpr int DPS = SUB * 3;   // DMA instructions per wave per stage: 1 A + 2 B per sub-stage
+constexpr int NSTORE = MI * 16 * 2;                // store instructions per wave per tile
+constexpr int HEAD = 6;                            // K steps that carry the previous tile's stores
+constexpr int SPS = (NSTORE + HEAD - 1) / HEAD;    // stores per head step
+static_assert(HEAD % NST == 0 && HEAD >= NST, "the head must end on a stage-0 step");
+static_assert(DPS + SPS < 64, "vmcnt holds at most 63");
 
-template <bool MASK>
+// f(integral_constant<int, I>) for I = I0 .. N-1, in order
+template <int I, int N>
+struct unroll_ic {
+    template <class F>
+    __device__ __forceinline__ static void run(F &&f) {
+        if constexpr (I < N) {
+            f(std::integral_constant<int, I>{});
+            unroll_ic<I + 1, N>::run(f);
+        }
+    }
+};
+
+// stores carried by head step c (none outside the head)
+__host__ __device__ constexpr int chunk_size(int c) {
+    return (c < 0 || c >= HEAD) ? 0 : (NSTORE - c * SPS < SPS ? NSTORE - c * SPS : SPS);
+}
+
+// MULTI: tiles may outnumber the workgroups (several rounds); otherwise each
+// workgroup computes exactly one tile and stores it at the end.
+template <bool MASK, bool MULTI>
 __global__ __launch_bounds__(THREADS, 1) void gemm_i8_h128_kernel(const int8_t *__restrict__ A,
                                                                   const int8_t *__restrict__ B,
                                                                   int32_t *__restrict__ C, int M, int N, int K,
@@ -645,14 +672,6 @@ __global__ __launch_bounds__(THREADS, 1) void gemm_i8_h128_kernel(const int8_t *
     __shared__ __attribute__((aligned(1024))) int8_t smem[NST * ST];
 
     const int ntiles = tiles_m * tiles_n;
-    const int pid = xcd_remap(blockIdx.x, ntiles);
-    const int in_group = GROUP_M * tiles_n;
-    const int first_m = (pid / in_group) * GROUP_M;
-    const int gsize = min(tiles_m - first_m, GROUP_M);
-    const int tm = first_m + (pid % in_group) % gsize;
-    const int tn = (pid % in_group) / gsize;
-    const int m0 = tm * BM, n0 = tn * BN;
-
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int wm = (wave >> 2) * WM, wn = (wave & 3) * WN;
@@ -664,161 +683,235 @@ __global__ __launch_bounds__(THREADS, 1) void gemm_i8_h128_kernel(const int8_t *
     const v4i32 ra = rsrc_words(A, (uint32_t)M * (uint32_t)K);
     const v4i32 rb = rsrc_words(B, (uint32_t)K * (uint32_t)N);
     // this lane's chunk of the wave's A block (1 KiB = 16 rows) and of its two
-    // B blocks (1 KiB = 4 k-rows each) of a sub-stage: the inverse swizzles
-    uint32_t a_off, b_off[2];
+    // B blocks (1 KiB = 4 k-rows each) of a sub-stage, relative to the tile
+    // origin: the inverse swizzles
+    uint32_t a_rel, b_rel[2];
     {
         const int slot = 64 * wave + lane;
         const int ar = slot >> 2, ac = (slot & 3) ^ ((ar >> 2) & 3);
-        a_off = (uint32_t)(m0 + ar) * (uint32_t)K + (uint32_t)(16 * ac);
+        a_rel = (uint32_t)ar * (uint32_t)K + (uint32_t)(16 * ac);
     }
 #pragma unroll
     for (int j = 0; j < 2; ++j) {
         const int slot = 64 * (2 * wave + j) + lane;
         const int br = slot >> 4, bc = (slot & 15) ^ ((br & 7) << 1);
-        b_off[j] = (uint32_t)br * (uint32_t)N + (uint32_t)(n0 + 16 * bc);
+        b_rel[j] = (uint32_t)br * (uint32_t)N + (uint32_t)(16 * bc);
     }
 
-    v16i32 acc[MI][2];
-#pragma unroll
-    for (int i = 0; i < MI; ++i)
-#pragma unroll
-        for (int j = 0; j < 2; ++j) acc[i][j] = (v16i32){0};
+    v16i32 acc[MI][2], prv[MI][2];
+    int pm0 = 0, pn0 = 0;   // origin of the tile held in prv
+    bool have_prev = false;
 
-    struct Ops {
-        v2i64 a[MI], b[2];
+    // store e of tile (tm0, tn0) from v: e = (i * 16 + r) * 2 + j.  The address
+    // is a wave-uniform row pointer plus this lane's byte offset (4 lh rows and
+    // l32 columns, below 2^32 since ldc < 2^24)
+    const uint32_t lane_b = (uint32_t)(4 * lh) * (uint32_t)ldc * 4u + (uint32_t)l32 * 4u;
+    auto store_c = [&](const v16i32 (&v)[MI][2], int tm0, int tn0, int e) __attribute__((always_inline)) {
+        const int i = e >> 5, r = (e >> 1) & 15, j = e & 1;
+        const int rowu = tm0 + wm + i * 32 + 8 * (r >> 2) + (r & 3);   // wave-uniform part
+        const int colu = tn0 + wn + 32 * j;
+        int32_t *dst = (int32_t *)((char *)(C + (size_t)rowu * ldc + colu) + lane_b);
+        if (!MASK || (rowu + 4 * lh < mst && colu + l32 < nst)) __builtin_nontemporal_store(v[i][j][r], dst);
     };
-    auto read_ops = [&](Ops &o, int stage, int sub, int h) {
-        const int8_t *sA = smem + stage * ST + sub * SS;
-        const int8_t *sB = sA + A_BYTES;
-#pragma unroll
-        for (int j = 0; j < 2; ++j) {
-            const int r = 32 * h + tr_row, cb = (wn + 32 * j + tr_col) >> 4, sub8 = tr_col & 8;
-            const v2i32 lo = read_tr8(sB + swz_b(r, cb) + sub8);
-            const v2i32 hi = read_tr8(sB + swz_b(r + 8, cb) + sub8);
-            o.b[j] = __builtin_bit_cast(v2i64, (v4i32){lo.x, lo.y, hi.x, hi.y});
-        }
-#pragma unroll
-        for (int i = 0; i < MI; ++i) o.a[i] = *(const v2i64 *)(sA + swz_a(wm + i * 32 + l32, 2 * h + lh));
-    };
-    auto mma = [&](const Ops &o) {
-#pragma unroll
-        for (int i = 0; i < MI; ++i)
-#pragma unroll
-            for (int j = 0; j < 2; ++j) acc[i][j] = mfma32x32x32(o.a[i], o.b[j], acc[i][j]);
-    };
+    auto store_prev = [&](int e) __attribute__((always_inline)) { store_c(prv, pm0, pn0, e); };
 
     const int nk = K / KS;
     // K advances through soffset, which the range check does not cover: a
     // step past the end re-loads the last step (into a stage never read again)
     const uint32_t last_a = (uint32_t)(K - KS), last_b = (uint32_t)(K - KS) * (uint32_t)N;
     const uint32_t base = lds_addr(smem);
-    auto issue_f = [&](auto st_c, int k0) {
-        constexpr int st = decltype(st_c)::value;
-        const bool in = k0 < K;
-        const uint32_t sa = in ? (uint32_t)k0 : last_a;
-        const uint32_t sb = in ? (uint32_t)k0 * (uint32_t)N : last_b;
+
+    for (int t = blockIdx.x; t < ntiles; t += MULTI ? gridDim.x : ntiles) {
+        const int pid = xcd_remap(t, ntiles);
+        const int in_group = GROUP_M * tiles_n;
+        const int first_m = (pid / in_group) * GROUP_M;
+        const int gsize = min(tiles_m - first_m, GROUP_M);
+        const int tm = first_m + (pid % in_group) % gsize;
+        const int tn = (pid % in_group) / gsize;
+        const int m0 = tm * BM, n0 = tn * BN;
+        const uint32_t a_off = (uint32_t)m0 * (uint32_t)K + a_rel;
+        uint32_t b_off[2];
 #pragma unroll
-        for (int u = 0; u < SUB; ++u) {
-            dma16s(ra, base + (uint32_t)(st * ST + u * SS) + (uint32_t)wave * 1024u, (int)a_off,
-                   sa + (uint32_t)(u * BK));
-#pragma unroll
-            for (int j = 0; j < 2; ++j)
-                dma16s(rb, base + (uint32_t)(st * ST + u * SS + A_BYTES) + (uint32_t)(2 * wave + j) * 1024u,
-                       (int)b_off[j], sb + (uint32_t)(u * BK) * (uint32_t)N);
-        }
-    };
-    using S0 = std::integral_constant<int, 0>;
-    using S1 = std::integral_constant<int, 1>;
-    using S2 = std::integral_constant<int, 2>;
-    static_assert(NST == 3, "the unrolled loop below assumes 3 stages");
-    // Ping-pong schedule as in gemm_i8_dma_kernel (slots A_j = {group 0:
-    // MFMA(j), group 1: MEM(j)}, B_j = {group 0: MEM(j+1), group 1: MFMA(j)}),
-    // with the DMA two steps ahead: MEM(s) reads step s (stage s % 3) and
-    // refills stage (s + 2) % 3 with step s + 2.  That stage held step s - 1,
-    // read in B_{s-2} and A_{s-1}; MEM(s) runs in B_{s-1} (group 0) or A_s
-    // (group 1), after both.  Before the barrier closing A_j each wave waits
-    // for its share of step j + 1 (vmcnt(DPS): step j + 2 stays in flight).
-    issue_f(S0{}, 0);
-    issue_f(S1{}, KS);
-    DET_WAIT_VMCNT(DPS);   // step 0 landed
-    __builtin_amdgcn_s_barrier();
-    Ops q0, q1, q2, q3;
-    auto mem = [&](auto st_c, int s) {
-        constexpr int st = decltype(st_c)::value;
-        read_ops(q0, st, 0, 0);
-        read_ops(q1, st, 0, 1);
-        read_ops(q2, st, 1, 0);
-        read_ops(q3, st, 1, 1);
-        issue_f(std::integral_constant<int, (st + 2) % NST>{}, (s + 2) * KS);
-    };
-    auto mma_all = [&]() {
-        mma(q0);
-        mma(q1);
-        mma(q2);
-        mma(q3);
-    };
-    if (wave < 4) {
-        mem(S0{}, 0);
-        DET_WAIT_LGKM0();
-        __builtin_amdgcn_s_barrier();
-        auto step0 = [&](auto cur_c, int kt) {
-            constexpr int nxt = (decltype(cur_c)::value + 1) % NST;
-            __builtin_amdgcn_sched_barrier(0);
-            mma_all();
-            __builtin_amdgcn_sched_barrier(0);
-            DET_WAIT_VMCNT(DPS);
-            __builtin_amdgcn_s_barrier();
-            __builtin_amdgcn_sched_barrier(0);
-            if (kt + 1 < nk) mem(std::integral_constant<int, nxt>{}, kt + 1);
-            DET_WAIT_LGKM0();
-            __builtin_amdgcn_sched_barrier(0);
-            __builtin_amdgcn_s_barrier();
-        };
-        int kt = 0;
-        for (; kt + NST <= nk; kt += NST) {
-            step0(S0{}, kt);
-            step0(S1{}, kt + 1);
-            step0(S2{}, kt + 2);
-        }
-        if (kt < nk) step0(S0{}, kt);
-        if (kt + 1 < nk) step0(S1{}, kt + 1);
-    } else {
-        __builtin_amdgcn_s_barrier();
-        auto step1 = [&](auto cur_c, int kt) {
-            __builtin_amdgcn_sched_barrier(0);
-            mem(cur_c, kt);
-            DET_WAIT_VMCNT(DPS);
-            DET_WAIT_LGKM0();
-            __builtin_amdgcn_s_barrier();
-            __builtin_amdgcn_sched_barrier(0);
-            mma_all();
-            __builtin_amdgcn_sched_barrier(0);
-            __builtin_amdgcn_s_barrier();
-        };
-        int kt = 0;
-        for (; kt + NST <= nk; kt += NST) {
-            step1(S0{}, kt);
-            step1(S1{}, kt + 1);
-            step1(S2{}, kt + 2);
-        }
-        if (kt < nk) step1(S0{}, kt);
-        if (kt + 1 < nk) step1(S1{}, kt + 1);
-    }
-    // the re-loads issued past the end of K must not still be writing LDS
-    DET_WAIT_VMCNT(0);
+        for (int j = 0; j < 2; ++j) b_off[j] = b_rel[j] + (uint32_t)n0;
 
 #pragma unroll
-    for (int i = 0; i < MI; ++i)
+        for (int i = 0; i < MI; ++i)
 #pragma unroll
-        for (int r = 0; r < 16; ++r) {
-            const int row = m0 + wm + i * 32 + 8 * (r >> 2) + 4 * lh + (r & 3);
-            if (MASK && row >= mst) continue;
-            const int col = n0 + wn + l32;
-            int32_t *crow = C + (size_t)row * ldc + col;
+            for (int j = 0; j < 2; ++j) acc[i][j] = (v16i32){0};
+
+        struct Ops {
+            v2i64 a[MI], b[2];
+        };
+        auto read_ops = [&](Ops &o, int stage, int sub, int h) __attribute__((always_inline)) {
+            const int8_t *sA = smem + stage * ST + sub * SS;
+            const int8_t *sB = sA + A_BYTES;
 #pragma unroll
-            for (int j = 0; j < 2; ++j)
-                if (!MASK || col + j * 32 < nst) __builtin_nontemporal_store(acc[i][j][r], crow + j * 32);
+            for (int j = 0; j < 2; ++j) {
+                const int r = 32 * h + tr_row, cb = (wn + 32 * j + tr_col) >> 4, sub8 = tr_col & 8;
+                const v2i32 lo = read_tr8(sB + swz_b(r, cb) + sub8);
+                const v2i32 hi = read_tr8(sB + swz_b(r + 8, cb) + sub8);
+                o.b[j] = __builtin_bit_cast(v2i64, (v4i32){lo.x, lo.y, hi.x, hi.y});
+            }
+#pragma unroll
+            for (int i = 0; i < MI; ++i) o.a[i] = *(const v2i64 *)(sA + swz_a(wm + i * 32 + l32, 2 * h + lh));
+        };
+        auto mma = [&](const Ops &o) __attribute__((always_inline)) {
+#pragma unroll
+            for (int i = 0; i < MI; ++i)
+#pragma unroll
+                for (int j = 0; j < 2; ++j) acc[i][j] = mfma32x32x32(o.a[i], o.b[j], acc[i][j]);
+        };
+        auto issue_f = [&](auto st_c, int k0) __attribute__((always_inline)) {
+            constexpr int st = decltype(st_c)::value;
+            const bool in = k0 < K;
+            const uint32_t sa = in ? (uint32_t)k0 : last_a;
+            const uint32_t sb = in ? (uint32_t)k0 * (uint32_t)N : last_b;
+#pragma unroll
+            for (int u = 0; u < SUB; ++u) {
+                dma16s(ra, base + (uint32_t)(st * ST + u * SS) + (uint32_t)wave * 1024u, (int)a_off,
+                       sa + (uint32_t)(u * BK));
+#pragma unroll
+                for (int j = 0; j < 2; ++j)
+                    dma16s(rb, base + (uint32_t)(st * ST + u * SS + A_BYTES) + (uint32_t)(2 * wave + j) * 1024u,
+                           (int)b_off[j], sb + (uint32_t)(u * BK) * (uint32_t)N);
+            }
+        };
+        using S0 = std::integral_constant<int, 0>;
+        using S1 = std::integral_constant<int, 1>;
+        using S2 = std::integral_constant<int, 2>;
+        static_assert(NST == 3, "the unrolled loop below assumes 3 stages");
+        // Ping-pong schedule as in gemm_i8_dma_kernel (slots A_j = {group 0:
+        // MFMA(j), group 1: MEM(j)}, B_j = {group 0: MEM(j+1), group 1: MFMA(j)}),
+        // with the DMA two steps ahead: MEM(s) reads step s (stage s % 3) and
+        // refills stage (s + 2) % 3 with step s + 2.  That stage held step s - 1,
+        // read in B_{s-2} and A_{s-1}; MEM(s) runs in B_{s-1} (group 0) or A_s
+        // (group 1), after both.  Before the barrier closing A_j each wave waits
+        // for its share of step j + 1: vmcnt(DPS + stores issued after the DMA
+        // of step j + 2), which leaves only those in flight (vector memory
+        // operations complete in issue order).
+        // All LDS reads of the previous tile ended before its last barrier,
+        // and its past-the-end re-loads landed (vmcnt(0) below), so the first
+        // two stages can be refilled at once.
+        issue_f(S0{}, 0);
+        issue_f(S1{}, KS);
+        DET_WAIT_VMCNT(DPS);   // step 0 landed
+        __builtin_amdgcn_s_barrier();
+        Ops q0, q1, q2, q3;
+        // MEM(s), carrying head chunk CH of the previous tile's stores
+        auto mem = [&](auto st_c, auto ch_c, int s) __attribute__((always_inline)) {
+            constexpr int st = decltype(st_c)::value, ch = decltype(ch_c)::value;
+            read_ops(q0, st, 0, 0);
+            read_ops(q1, st, 0, 1);
+            read_ops(q2, st, 1, 0);
+            read_ops(q3, st, 1, 1);
+            issue_f(std::integral_constant<int, (st + 2) % NST>{}, (s + 2) * KS);
+            if constexpr (chunk_size(ch) > 0) {
+                __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+                for (int e = ch * SPS; e < ch * SPS + chunk_size(ch); ++e) store_prev(e);
+            }
+        };
+        auto mma_all = [&]() __attribute__((always_inline)) {
+            mma(q0);
+            mma(q1);
+            mma(q2);
+            mma(q3);
+        };
+        using NONE = std::integral_constant<int, -1>;
+        // a tile carries the previous one's stores in its head when it has at
+        // least HEAD steps; otherwise they go out here, all at once
+        const bool spread = MULTI && have_prev && nk >= HEAD;
+        if (MULTI && have_prev && !spread)
+#pragma unroll
+            for (int e = 0; e < NSTORE; ++e) store_prev(e);
+        if (wave < 4) {
+            // step kt: W = head chunk issued by MEM(kt), whose stores may still
+            // be in flight; MEM(kt + 1) carries chunk kt + 1
+            auto step0 = [&](auto cur_c, auto w_c, int kt) __attribute__((always_inline)) {
+                constexpr int nxt = (decltype(cur_c)::value + 1) % NST, w = decltype(w_c)::value;
+                using CH = std::integral_constant<int, (w >= 0 && w + 1 < HEAD) ? w + 1 : -1>;
+                __builtin_amdgcn_sched_barrier(0);
+                mma_all();
+                __builtin_amdgcn_sched_barrier(0);
+                DET_WAIT_VMCNT(DPS + chunk_size(w));
+                __builtin_amdgcn_s_barrier();
+                __builtin_amdgcn_sched_barrier(0);
+                if (kt + 1 < nk) mem(std::integral_constant<int, nxt>{}, CH{}, kt + 1);
+                DET_WAIT_LGKM0();
+                __builtin_amdgcn_sched_barrier(0);
+                __builtin_amdgcn_s_barrier();
+            };
+            int kt = 0;
+            if (spread) {
+                mem(S0{}, std::integral_constant<int, 0>{}, 0);
+                DET_WAIT_LGKM0();
+                __builtin_amdgcn_s_barrier();
+                unroll_ic<0, HEAD>::run([&](auto ic) __attribute__((always_inline)) {
+                    constexpr int i = decltype(ic)::value;
+                    step0(std::integral_constant<int, i % NST>{}, ic, i);
+                });
+                kt = HEAD;
+            } else {
+                mem(S0{}, NONE{}, 0);
+                DET_WAIT_LGKM0();
+                __builtin_amdgcn_s_barrier();
+            }
+            for (; kt + NST <= nk; kt += NST) {
+                step0(S0{}, NONE{}, kt);
+                step0(S1{}, NONE{}, kt + 1);
+                step0(S2{}, NONE{}, kt + 2);
+            }
+            if (kt < nk) step0(S0{}, NONE{}, kt);
+            if (kt + 1 < nk) step0(S1{}, NONE{}, kt + 1);
+        } else {
+            __builtin_amdgcn_s_barrier();
+            auto step1 = [&](auto cur_c, auto ch_c, int kt) __attribute__((always_inline)) {
+                __builtin_amdgcn_sched_barrier(0);
+                mem(cur_c, ch_c, kt);
+                DET_WAIT_VMCNT(DPS + chunk_size(decltype(ch_c)::value));
+                DET_WAIT_LGKM0();
+                __builtin_amdgcn_s_barrier();
+                __builtin_amdgcn_sched_barrier(0);
+                mma_all();
+                __builtin_amdgcn_sched_barrier(0);
+                __builtin_amdgcn_s_barrier();
+            };
+            int kt = 0;
+            if (spread) {
+                unroll_ic<0, HEAD>::run([&](auto ic) __attribute__((always_inline)) {
+                    constexpr int i = decltype(ic)::value;
+                    step1(std::integral_constant<int, i % NST>{}, ic, i);
+                });
+                kt = HEAD;
+            }
+            for (; kt + NST <= nk; kt += NST) {
+                step1(S0{}, NONE{}, kt);
+                step1(S1{}, NONE{}, kt + 1);
+                step1(S2{}, NONE{}, kt + 2);
+            }
+            if (kt < nk) step1(S0{}, NONE{}, kt);
+            if (kt + 1 < nk) step1(S1{}, NONE{}, kt + 1);
         }
+        // the re-loads issued past the end of K must not still be writing LDS
+        // when the next tile refills its first stages
+        DET_WAIT_VMCNT(0);
+
+        if constexpr (MULTI) {
+#pragma unroll
+            for (int i = 0; i < MI; ++i)
+#pragma unroll
+                for (int j = 0; j < 2; ++j) prv[i][j] = acc[i][j];
+            pm0 = m0;
+            pn0 = n0;
+            have_prev = true;
+        } else {
+#pragma unroll
+            for (int e = 0; e < NSTORE; ++e) store_c(acc, m0, n0, e);
+        }
+    }
+    if (MULTI && have_prev)
+#pragma unroll
+        for (int e = 0; e < NSTORE; ++e) store_prev(e);
 }
 }  // namespace h128
 }  // namespace i8g
@@ -910,13 +1003,21 @@ static void launch_i8_on_grid(const int8_t *A, const int8_t *B, int32_t *C, int 
     // 128-row tiles when 256 x 256 tiles would not fill more than one round
     // of the chip (or do not fit the shape)
     if (full128 && (!full || tiles_m * tiles_n <= cu_count())) {
-        const int tm128 = M / h128::BM;
-        if (mask)
-            hipLaunchKernelGGL(h128::gemm_i8_h128_kernel<true>, dim3(tm128 * tiles_n), block, 0, s, A, B, C, M, N, K,
-                               tm128, tiles_n, ldc, mst, nst);
-        else
-            hipLaunchKernelGGL(h128::gemm_i8_h128_kernel<false>, dim3(tm128 * tiles_n), block, 0, s, A, B, C, M, N, K,
-                               tm128, tiles_n, ldc, mst, nst);
+        const int tm128 = M / h128::BM, nt = tm128 * tiles_n;
+        // persistent workgroups: as many rounds of tiles as the CUs need, the
+        // tiles spread evenly over a multiple of 8 workgroups (one XCD each)
+        const int rounds = (nt + cu_count() - 1) / cu_count();
+        const int wgs = rounds == 1 ? nt : ((nt + rounds - 1) / rounds + 7) / 8 * 8;
+        auto go = [&](auto kern) {
+            hipLaunchKernelGGL(kern, dim3(wgs), block, 0, s, A, B, C, M, N, K, tm128, tiles_n, ldc, mst, nst);
+        };
+        if (mask) {
+            if (rounds > 1) go(h128::gemm_i8_h128_kernel<true, true>);
+            else go(h128::gemm_i8_h128_kernel<true, false>);
+        } else {
+            if (rounds > 1) go(h128::gemm_i8_h128_kernel<false, true>);
+            else go(h128::gemm_i8_h128_kernel<false, false>);
+        }
     } else if (full) {
         if (mask)
             hipLaunchKernelGGL((gemm_i8_dma_kernel<EPI_I8, true, true>), grid, block, 0, s, A, B, C, M, N, K, tiles_m,

@@ -633,7 +633,32 @@ def test_gemm_i8_h128_wraps_mod_2_32():
 # Operands off the 16-byte grid (K or N not a multiple of 16) or not 16-byte
 # aligned: repacked into padded panels in the workspace (arena, caller
 # workspace or scratch), or, without a workspace, the byte-load kernel.
-RAGGED_I8 = [(1, 17, 1), (37, 100, 53), (300, 1000, 77), (256, 4095, 256), (1000, 1000, 1000), (257, 4100, 1003),
+def _mt_gemm_i8(a, b, m, k, n):
+    """Full int8 product from the multithreaded CPU restatement (equal to the
+    scalar oracle at every band count, tests/test_oracle.py)."""
+    c = np.empty(m * n, np.int32)
+    assert O.lib().det_cpu_gemm_i8(a.ctypes.data, b.ctypes.data, c.ctypes.data, m, k, n) == 0
+    return c.reshape(m, n)
+
+
+# 128 x 256 tiles on persistent workgroups: two rounds whose second tile
+# carries the first one's stores (272 tiles), uneven rounds (264 tiles on 136
+# workgroups), a K too short to carry them (512: stored at the next tile's
+# start) and three rounds (561 tiles)
+PERSIST_I8 = [(2048, 768, 4352), (1408, 768, 6144), (2048, 512, 4352), (4224, 768, 4352)]
+
+
+@pytest.mark.parametrize("m,k,n", PERSIST_I8, ids=[f"{m}x{k}x{n}" for m, k, n in PERSIST_I8])
+def test_gemm_i8_persistent_rounds(m, k, n):
+    a, b = O.gen_i8(0x9E25 ^ (m * 1000003 + k * 1009 + n), m * k, k * n)
+    note(f"det_matmul_i8_dev (persistent 128x256 tiles) {m}x{k}x{n}")
+    C = _dev_run(lambda pa, pb, pc, s: M.lib().det_matmul_i8_dev(pa, pb, pc, m, k, n, s), [a, b], (m, n))
+    np.testing.assert_array_equal(C, _mt_gemm_i8(a, b, m, k, n))
+    rows = np.r_[0, 127, 128, m - 1]
+    np.testing.assert_array_equal(C[rows], O.gemm_i8_rows(a, b, m, k, n, rows))
+
+
+RAGGED_I8 = [(1, 17, 1),(37, 100, 53), (300, 1000, 77), (256, 4095, 256), (1000, 1000, 1000), (257, 4100, 1003),
              (64, 64, 64), (256, 256, 256)]
 
 
