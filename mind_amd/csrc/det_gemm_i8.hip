@@ -636,13 +636,43 @@ constexpr int BM = 128, WM = 64, MI = 2, SUB = 2, NST = 3, KS = BK * SUB;
 // groups of 8 row tiles (1024 rows, as the 256-row kernel's groups of 4):
 // each XCD's share of a 4096^3 grid then reads 4 MiB of A and 8 MiB of B
 constexpr int GROUP_M = 8;
-constexpr int A_BYTES = BM * BK, B_BYTES = BK * BN, SS = A_BYTES + B_BYTES, ST = SUB * SS;
-constexpr int DPS = SUB * 3;   // DMA instructions per wave per stage: 1 A + 2 B per sub-stage
-constexpr int NSTORE = MI * 16 * 2;                // store instructions per wave per tile
-constexpr int HEAD = 6;                            // K steps that carry the previous tile's stores
-constexpr int SPS = (NSTORE + HEAD - 1) / HEAD;    // stores per head step
+constexpr int A_BYTES = BM * BK;
+constexpr int HEAD = 6;   // K steps that carry the previous tile's stores
 static_assert(HEAD % NST == 0 && HEAD >= NST, "the head must end on a stage-0 step");
-static_assert(DPS + SPS < 64, "vmcnt holds at most 63");
+
+// Tile width TN = 256 (waves 64 x 64: 2 x 2 blocks) or 128 (waves 64 x 32:
+// 2 x 1 blocks, for grids that 128 x 256 tiles would leave half empty).
+// B sub-stage [64 k][TN n]: TN = 256 uses swz_b; for TN = 128 a row is 128
+// bytes (two rows per 64-bank cycle) and its eight chunks are XOR-swizzled by
+// 2 * ((row >> 1) & 3): the 32 lanes of a transposing read (rows k0..k0+7,
+// chunks c and c + 1, c even) then hit 16 distinct 16-byte bank groups.
+template <int TN>
+struct Tile {
+    static constexpr int WNT = TN / 4, NJ = WNT / 32;
+    static constexpr int B_BYTES = BK * TN, SS = A_BYTES + B_BYTES, ST = SUB * SS;
+    static constexpr int DPS = SUB * (1 + NJ);   // DMA instructions per wave per stage
+    static constexpr int NSTORE = MI * 16 * NJ;   // store instructions per wave per tile
+    static constexpr int SPS = (NSTORE + HEAD - 1) / HEAD;   // stores per head step
+    static_assert(DPS + SPS < 64, "vmcnt holds at most 63");
+    static __device__ __forceinline__ int swz(int row, int chunk) {
+        if constexpr (TN == 256) return swz_b(row, chunk);
+        else return row * 128 + ((chunk ^ (((row >> 1) & 3) << 1)) << 4);
+    }
+    // LDS slot (16-byte unit) of a B sub-stage -> the k-row and n-chunk it holds
+    static __device__ __forceinline__ void b_chunk(int slot, int &br, int &bc) {
+        if constexpr (TN == 256) {
+            br = slot >> 4;
+            bc = (slot & 15) ^ ((br & 7) << 1);
+        } else {
+            br = slot >> 3;
+            bc = (slot & 7) ^ (((br >> 1) & 3) << 1);
+        }
+    }
+    // stores carried by head step c (none outside the head)
+    static __host__ __device__ constexpr int chunk_size(int c) {
+        return (c < 0 || c >= HEAD) ? 0 : (NSTORE - c * SPS < SPS ? NSTORE - c * SPS : SPS);
+    }
+};
 
 // f(integral_constant<int, I>) for I = I0 .. N-1, in order
 template <int I, int N>
@@ -656,25 +686,22 @@ struct unroll_ic {
     }
 };
 
-// stores carried by head step c (none outside the head)
-__host__ __device__ constexpr int chunk_size(int c) {
-    return (c < 0 || c >= HEAD) ? 0 : (NSTORE - c * SPS < SPS ? NSTORE - c * SPS : SPS);
-}
-
 // MULTI: tiles may outnumber the workgroups (several rounds); otherwise each
 // workgroup computes exactly one tile and stores it at the end.
-template <bool MASK, bool MULTI>
+template <bool MASK, bool MULTI, int TN>
 __global__ __launch_bounds__(THREADS, 1) void gemm_i8_h128_kernel(const int8_t *__restrict__ A,
                                                                   const int8_t *__restrict__ B,
                                                                   int32_t *__restrict__ C, int M, int N, int K,
                                                                   int tiles_m, int tiles_n, int ldc, int mst,
                                                                   int nst) {
+    using T = Tile<TN>;
+    constexpr int NJ = T::NJ, SS = T::SS, ST = T::ST, DPS = T::DPS, NSTORE = T::NSTORE, SPS = T::SPS;
     __shared__ __attribute__((aligned(1024))) int8_t smem[NST * ST];
 
     const int ntiles = tiles_m * tiles_n;
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-    const int wm = (wave >> 2) * WM, wn = (wave & 3) * WN;
+    const int wm = (wave >> 2) * WM, wn = (wave & 3) * T::WNT;
     const int l32 = lane & 31, lh = lane >> 5;
     const int tg = lane >> 4, ti = lane & 15;
     const int tr_row = 16 * (tg >> 1) + (ti >> 1);
@@ -682,32 +709,32 @@ __global__ __launch_bounds__(THREADS, 1) void gemm_i8_h128_kernel(const int8_t *
 
     const v4i32 ra = rsrc_words(A, (uint32_t)M * (uint32_t)K);
     const v4i32 rb = rsrc_words(B, (uint32_t)K * (uint32_t)N);
-    // this lane's chunk of the wave's A block (1 KiB = 16 rows) and of its two
-    // B blocks (1 KiB = 4 k-rows each) of a sub-stage, relative to the tile
-    // origin: the inverse swizzles
-    uint32_t a_rel, b_rel[2];
+    // this lane's chunk of the wave's A block (1 KiB = 16 rows) and of its NJ
+    // B blocks (1 KiB = 1024 / TN k-rows each) of a sub-stage, relative to the
+    // tile origin: the inverse swizzles
+    uint32_t a_rel, b_rel[NJ];
     {
         const int slot = 64 * wave + lane;
         const int ar = slot >> 2, ac = (slot & 3) ^ ((ar >> 2) & 3);
         a_rel = (uint32_t)ar * (uint32_t)K + (uint32_t)(16 * ac);
     }
 #pragma unroll
-    for (int j = 0; j < 2; ++j) {
-        const int slot = 64 * (2 * wave + j) + lane;
-        const int br = slot >> 4, bc = (slot & 15) ^ ((br & 7) << 1);
+    for (int j = 0; j < NJ; ++j) {
+        int br, bc;
+        T::b_chunk(64 * (NJ * wave + j) + lane, br, bc);
         b_rel[j] = (uint32_t)br * (uint32_t)N + (uint32_t)(16 * bc);
     }
 
-    v16i32 acc[MI][2], prv[MI][2];
+    v16i32 acc[MI][NJ], prv[MI][NJ];
     int pm0 = 0, pn0 = 0;   // origin of the tile held in prv
     bool have_prev = false;
 
-    // store e of tile (tm0, tn0) from v: e = (i * 16 + r) * 2 + j.  The address
+    // store e of tile (tm0, tn0) from v: e = (i * 16 + r) * NJ + j.  The address
     // is a wave-uniform row pointer plus this lane's byte offset (4 lh rows and
     // l32 columns, below 2^32 since ldc < 2^24)
     const uint32_t lane_b = (uint32_t)(4 * lh) * (uint32_t)ldc * 4u + (uint32_t)l32 * 4u;
-    auto store_c = [&](const v16i32 (&v)[MI][2], int tm0, int tn0, int e) __attribute__((always_inline)) {
-        const int i = e >> 5, r = (e >> 1) & 15, j = e & 1;
+    auto store_c = [&](const v16i32 (&v)[MI][NJ], int tm0, int tn0, int e) __attribute__((always_inline)) {
+        const int i = e / (16 * NJ), r = (e / NJ) & 15, j = e % NJ;
         const int rowu = tm0 + wm + i * 32 + 8 * (r >> 2) + (r & 3);   // wave-uniform part
         const int colu = tn0 + wn + 32 * j;
         int32_t *dst = (int32_t *)((char *)(C + (size_t)rowu * ldc + colu) + lane_b);
@@ -728,28 +755,28 @@ __global__ __launch_bounds__(THREADS, 1) void gemm_i8_h128_kernel(const int8_t *
         const int gsize = min(tiles_m - first_m, GROUP_M);
         const int tm = first_m + (pid % in_group) % gsize;
         const int tn = (pid % in_group) / gsize;
-        const int m0 = tm * BM, n0 = tn * BN;
+        const int m0 = tm * BM, n0 = tn * TN;
         const uint32_t a_off = (uint32_t)m0 * (uint32_t)K + a_rel;
-        uint32_t b_off[2];
+        uint32_t b_off[NJ];
 #pragma unroll
-        for (int j = 0; j < 2; ++j) b_off[j] = b_rel[j] + (uint32_t)n0;
+        for (int j = 0; j < NJ; ++j) b_off[j] = b_rel[j] + (uint32_t)n0;
 
 #pragma unroll
         for (int i = 0; i < MI; ++i)
 #pragma unroll
-            for (int j = 0; j < 2; ++j) acc[i][j] = (v16i32){0};
+            for (int j = 0; j < NJ; ++j) acc[i][j] = (v16i32){0};
 
         struct Ops {
-            v2i64 a[MI], b[2];
+            v2i64 a[MI], b[NJ];
         };
         auto read_ops = [&](Ops &o, int stage, int sub, int h) __attribute__((always_inline)) {
             const int8_t *sA = smem + stage * ST + sub * SS;
             const int8_t *sB = sA + A_BYTES;
 #pragma unroll
-            for (int j = 0; j < 2; ++j) {
+            for (int j = 0; j < NJ; ++j) {
                 const int r = 32 * h + tr_row, cb = (wn + 32 * j + tr_col) >> 4, sub8 = tr_col & 8;
-                const v2i32 lo = read_tr8(sB + swz_b(r, cb) + sub8);
-                const v2i32 hi = read_tr8(sB + swz_b(r + 8, cb) + sub8);
+                const v2i32 lo = read_tr8(sB + T::swz(r, cb) + sub8);
+                const v2i32 hi = read_tr8(sB + T::swz(r + 8, cb) + sub8);
                 o.b[j] = __builtin_bit_cast(v2i64, (v4i32){lo.x, lo.y, hi.x, hi.y});
             }
 #pragma unroll
@@ -759,7 +786,7 @@ __global__ __launch_bounds__(THREADS, 1) void gemm_i8_h128_kernel(const int8_t *
 #pragma unroll
             for (int i = 0; i < MI; ++i)
 #pragma unroll
-                for (int j = 0; j < 2; ++j) acc[i][j] = mfma32x32x32(o.a[i], o.b[j], acc[i][j]);
+                for (int j = 0; j < NJ; ++j) acc[i][j] = mfma32x32x32(o.a[i], o.b[j], acc[i][j]);
         };
         auto issue_f = [&](auto st_c, int k0) __attribute__((always_inline)) {
             constexpr int st = decltype(st_c)::value;
@@ -771,8 +798,8 @@ __global__ __launch_bounds__(THREADS, 1) void gemm_i8_h128_kernel(const int8_t *
                 dma16s(ra, base + (uint32_t)(st * ST + u * SS) + (uint32_t)wave * 1024u, (int)a_off,
                        sa + (uint32_t)(u * BK));
 #pragma unroll
-                for (int j = 0; j < 2; ++j)
-                    dma16s(rb, base + (uint32_t)(st * ST + u * SS + A_BYTES) + (uint32_t)(2 * wave + j) * 1024u,
+                for (int j = 0; j < NJ; ++j)
+                    dma16s(rb, base + (uint32_t)(st * ST + u * SS + A_BYTES) + (uint32_t)(NJ * wave + j) * 1024u,
                            (int)b_off[j], sb + (uint32_t)(u * BK) * (uint32_t)N);
             }
         };
@@ -805,10 +832,10 @@ __global__ __launch_bounds__(THREADS, 1) void gemm_i8_h128_kernel(const int8_t *
             read_ops(q2, st, 1, 0);
             read_ops(q3, st, 1, 1);
             issue_f(std::integral_constant<int, (st + 2) % NST>{}, (s + 2) * KS);
-            if constexpr (chunk_size(ch) > 0) {
+            if constexpr (T::chunk_size(ch) > 0) {
                 __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-                for (int e = ch * SPS; e < ch * SPS + chunk_size(ch); ++e) store_prev(e);
+                for (int e = ch * SPS; e < ch * SPS + T::chunk_size(ch); ++e) store_prev(e);
             }
         };
         auto mma_all = [&]() __attribute__((always_inline)) {
@@ -833,7 +860,7 @@ __global__ __launch_bounds__(THREADS, 1) void gemm_i8_h128_kernel(const int8_t *
                 __builtin_amdgcn_sched_barrier(0);
                 mma_all();
                 __builtin_amdgcn_sched_barrier(0);
-                DET_WAIT_VMCNT(DPS + chunk_size(w));
+                DET_WAIT_VMCNT(DPS + T::chunk_size(w));
                 __builtin_amdgcn_s_barrier();
                 __builtin_amdgcn_sched_barrier(0);
                 if (kt + 1 < nk) mem(std::integral_constant<int, nxt>{}, CH{}, kt + 1);
@@ -868,7 +895,7 @@ __global__ __launch_bounds__(THREADS, 1) void gemm_i8_h128_kernel(const int8_t *
             auto step1 = [&](auto cur_c, auto ch_c, int kt) __attribute__((always_inline)) {
                 __builtin_amdgcn_sched_barrier(0);
                 mem(cur_c, ch_c, kt);
-                DET_WAIT_VMCNT(DPS + chunk_size(decltype(ch_c)::value));
+                DET_WAIT_VMCNT(DPS + T::chunk_size(decltype(ch_c)::value));
                 DET_WAIT_LGKM0();
                 __builtin_amdgcn_s_barrier();
                 __builtin_amdgcn_sched_barrier(0);
@@ -900,7 +927,7 @@ __global__ __launch_bounds__(THREADS, 1) void gemm_i8_h128_kernel(const int8_t *
 #pragma unroll
             for (int i = 0; i < MI; ++i)
 #pragma unroll
-                for (int j = 0; j < 2; ++j) prv[i][j] = acc[i][j];
+                for (int j = 0; j < NJ; ++j) prv[i][j] = acc[i][j];
             pm0 = m0;
             pn0 = n0;
             have_prev = true;
@@ -1000,23 +1027,30 @@ static void launch_i8_on_grid(const int8_t *A, const int8_t *B, int32_t *C, int 
     const dim3 grid(tiles_m * tiles_n), block(THREADS);
     const bool full = K > 0 && M % BM == 0 && N % BN == 0 && K % (BK * NSTAGE) == 0;
     const bool full128 = K > 0 && M % h128::BM == 0 && N % BN == 0 && K % h128::KS == 0;
-    // 128-row tiles when 256 x 256 tiles would not fill more than one round
-    // of the chip (or do not fit the shape)
-    if (full128 && (!full || tiles_m * tiles_n <= cu_count())) {
-        const int tm128 = M / h128::BM, nt = tm128 * tiles_n;
+    const bool full128n = K > 0 && M % h128::BM == 0 && N % 128 == 0 && K % h128::KS == 0;
+    const int cus = cu_count(), tm128 = M / h128::BM;
+    // 128 x 128 tiles when they fit one round of the chip (M N <= 2^22 on 256
+    // CUs: 128 x 256 tiles would leave half the CUs idle); otherwise 128 x 256
+    // tiles when 256 x 256 tiles would not fill more than one round (or do
+    // not fit the shape)
+    const bool use128n = full128n && tm128 * (N / 128) <= cus;
+    const bool use128 = !use128n && full128 && (!full || tiles_m * tiles_n <= cus);
+    if (use128 || use128n) {
+        const int tn = use128n ? N / 128 : N / BN, nt = tm128 * tn;
         // persistent workgroups: as many rounds of tiles as the CUs need, the
         // tiles spread evenly over a multiple of 8 workgroups (one XCD each)
-        const int rounds = (nt + cu_count() - 1) / cu_count();
+        const int rounds = (nt + cus - 1) / cus;
         const int wgs = rounds == 1 ? nt : ((nt + rounds - 1) / rounds + 7) / 8 * 8;
         auto go = [&](auto kern) {
-            hipLaunchKernelGGL(kern, dim3(wgs), block, 0, s, A, B, C, M, N, K, tm128, tiles_n, ldc, mst, nst);
+            hipLaunchKernelGGL(kern, dim3(wgs), block, 0, s, A, B, C, M, N, K, tm128, tn, ldc, mst, nst);
         };
-        if (mask) {
-            if (rounds > 1) go(h128::gemm_i8_h128_kernel<true, true>);
-            else go(h128::gemm_i8_h128_kernel<true, false>);
+        using namespace h128;
+        if (use128n) {   // one round by construction
+            if (mask) go(gemm_i8_h128_kernel<true, false, 128>);
+            else go(gemm_i8_h128_kernel<false, false, 128>);
         } else {
-            if (rounds > 1) go(h128::gemm_i8_h128_kernel<false, true>);
-            else go(h128::gemm_i8_h128_kernel<false, false>);
+            if (mask) rounds > 1 ? go(gemm_i8_h128_kernel<true, true, 256>) : go(gemm_i8_h128_kernel<true, false, 256>);
+            else rounds > 1 ? go(gemm_i8_h128_kernel<false, true, 256>) : go(gemm_i8_h128_kernel<false, false, 256>);
         }
     } else if (full) {
         if (mask)

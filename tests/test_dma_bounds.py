@@ -100,24 +100,29 @@ def test_full_tile_model_catches_the_old_past_end_offset():
     assert ((br * N + bnc) + K * N).max() + 16 > K * N
 
 
-def _h128_addresses(M, N, K):
-    """gemm_i8_h128_kernel: 128-row tiles, K steps of 128 as two 64-wide
-    sub-stages, each wave one A block and two B blocks per sub-stage, DMA two
-    steps ahead (prologue steps 0 and 1, MEM(s) issues step s + 2)."""
+def _h128_addresses(M, N, K, tn=256):
+    """gemm_i8_h128_kernel: 128-row tiles of width tn, K steps of 128 as two
+    64-wide sub-stages, each wave one A block and tn / 128 B blocks per
+    sub-stage, DMA two steps ahead (prologue steps 0 and 1, MEM(s) issues
+    step s + 2)."""
     KS = 2 * BK
+    nj = tn // 128
     wave = np.arange(8)[:, None]
     lane = np.arange(64)[None, :]
     slot = (64 * wave + lane).ravel()
     ar = slot >> 2
     akc = 16 * ((slot & 3) ^ ((ar >> 2) & 3))
-    _, _, br, bnc = _lane_chunks()
-    assert ar.max() < 128
+    bslot = (64 * (nj * np.arange(8)[:, None, None] + np.arange(nj)[None, :, None])
+             + np.arange(64)[None, None, :]).ravel()
+    br, bc = _b_chunk(bslot, tn)
+    bnc = 16 * bc
+    assert ar.max() < 128 and br.max() < 64 and bnc.max() + 16 <= tn
     nk = K // KS
     lo = [None, None]
     hi = [None, None]
     for m0 in range(0, M, 128):
         a_off = (m0 + ar) * K + akc
-        for n0 in range(0, N, BN):
+        for n0 in range(0, N, tn):
             b_off = br * N + n0 + bnc
             for step in range(0, nk + 2):
                 k0 = step * KS
@@ -130,11 +135,12 @@ def _h128_addresses(M, N, K):
     return (lo[0], hi[0] + 16, M * K), (lo[1], hi[1] + 16, K * N)
 
 
-@pytest.mark.parametrize("M,N,K", [(128, 256, 128), (4096, 4096, 4096), (384, 512, 384), (2048, 2048, 2048),
-                                   (128, 768, 1152)])
-def test_h128_tile_dma_stays_inside_operands(M, N, K):
-    assert M % 128 == 0 and N % BN == 0 and K % 128 == 0 and K > 0
-    for lo, end, lim in _h128_addresses(M, N, K):
+@pytest.mark.parametrize("M,N,K,tn", [(128, 256, 128, 256), (4096, 4096, 4096, 256), (384, 512, 384, 256),
+                                      (2048, 2048, 2048, 256), (128, 768, 1152, 256), (128, 128, 128, 128),
+                                      (2048, 2048, 2048, 128), (384, 640, 1152, 128)])
+def test_h128_tile_dma_stays_inside_operands(M, N, K, tn):
+    assert M % 128 == 0 and N % tn == 0 and K % 128 == 0 and K > 0
+    for lo, end, lim in _h128_addresses(M, N, K, tn):
         assert lo >= 0 and end <= lim, (end, lim)
 
 
@@ -182,3 +188,64 @@ def test_pad_kernel_reads_stay_inside_and_assemble_the_rows(rows, cols, base):
     want = np.zeros((rows, dcols), np.uint8)
     want[:, :cols] = src.reshape(rows, cols)
     np.testing.assert_array_equal(got, want)
+
+
+def _b_chunk(slot, tn):
+    """LDS slot (16-byte unit) of a B sub-stage -> (k-row, n-chunk) it holds
+    (Tile<TN>::b_chunk)."""
+    if tn == 256:
+        br = slot >> 4
+        return br, (slot & 15) ^ ((br & 7) << 1)
+    br = slot >> 3
+    return br, (slot & 7) ^ (((br >> 1) & 3) << 1)
+
+
+def _b_swz(row, chunk, tn):
+    """Byte offset of (k-row, n-chunk) in a B sub-stage (Tile<TN>::swz)."""
+    if tn == 256:
+        return row * 256 + ((chunk ^ ((row & 7) << 1)) << 4)
+    return row * 128 + ((chunk ^ (((row >> 1) & 3) << 1)) << 4)
+
+
+@pytest.mark.parametrize("tn", [256, 128])
+def test_h128_b_stage_layout_round_trips_and_reads_conflict_free(tn):
+    """The B sub-stage of gemm_i8_h128_kernel<., ., TN>: the DMA places the
+    global chunk b_chunk(slot) at slot (16 bytes per lane); the transposing
+    reads (ds_read_b64_tr_b8: lane t of a 16-lane group gets byte t & 7 of
+    the segments of lanes 2j + (t >> 3)) must hand lane l the MFMA B operand
+    B[32h + 16 (l >> 5) + 0..15][wn + 32 j + (l & 31)], and each half-wave
+    must touch all 64 four-byte banks exactly once."""
+    nj = tn // 128
+    rng = np.random.default_rng(tn)
+    tile = rng.integers(0, 256, size=(64, tn), dtype=np.uint8)   # one sub-stage: B[k][n]
+    lds = np.zeros(64 * tn, np.uint8)
+    written = np.zeros(64 * tn, bool)
+    for slot in range(64 * tn // 16):
+        br, bc = _b_chunk(slot, tn)
+        assert 0 <= br < 64 and 0 <= bc < tn // 16
+        lds[16 * slot:16 * slot + 16] = tile[br, 16 * bc:16 * bc + 16]
+        written[16 * slot:16 * slot + 16] = True
+    assert written.all()
+    lane = np.arange(64)
+    tg, ti = lane >> 4, lane & 15
+    tr_row = 16 * (tg >> 1) + (ti >> 1)
+    tr_col = 16 * (tg & 1) + 8 * (ti & 1)
+    for wn in range(0, tn, tn // 4):
+        for j in range(nj):
+            for h in range(2):
+                got = np.zeros((64, 16), np.uint8)
+                for half, dr in enumerate((0, 8)):
+                    r = 32 * h + tr_row + dr
+                    cb = (wn + 32 * j + tr_col) >> 4
+                    addr = np.array([_b_swz(int(r[i]), int(cb[i]), tn) for i in range(64)]) + (tr_col & 8)
+                    for w in (slice(0, 32), slice(32, 64)):
+                        banks = np.concatenate([(addr[w] // 4) % 64, (addr[w] // 4 + 1) % 64])
+                        assert len(set(banks.tolist())) == 64
+                    for t in range(64):
+                        g = 16 * (t >> 4)
+                        for jj in range(8):
+                            src = g + 2 * jj + ((t & 15) >> 3)
+                            got[t, 8 * half + jj] = lds[addr[src] + (t & 7)]
+                want = np.stack([tile[32 * h + 16 * (t >> 5):32 * h + 16 * (t >> 5) + 16, wn + 32 * j + (t & 31)]
+                                 for t in range(64)])
+                np.testing.assert_array_equal(got, want)
