@@ -39,6 +39,11 @@ extern "C" {
 #define DET_DOT_Q16 0
 #define DET_DOT_L1_Q16 1
 #define DET_DOT_I16 2
+/* f32 metrics of det_rows_metric_f32[_dev] */
+#define DET_F32_DOT 0
+#define DET_F32_L1 1
+#define DET_F32_LINF 2
+#define DET_F32_LINF_V 3
 
 /* ------------------------------------------------------------------------
  * Layer 1: the reference's intrinsic symbols (arity table
@@ -93,6 +98,22 @@ int64_t __mind_blas_dot_f32(int64_t a, int64_t b, int64_t len);
 /* Replaces __mind_blas_dot_f32_v (vector-dialect twin, same schedule):
  * src/type_checker/mod.rs (dot_f32_v), src/mlir/lowering.rs:5528-5690. */
 int64_t __mind_blas_dot_f32_v(int64_t a, int64_t b, int64_t len);
+/* Replaces __mind_blas_dot_l1_f32(a, b, len): sum of |a[i] - b[i]| (sign
+ * bit cleared) on the dot's 8-lane schedule and fold; packed f32 bits, 0 for
+ * len <= 0 or NULL (runtime-support/mind_intrinsics.c:1286-1351; arity
+ * src/type_checker/mod.rs:2247).  Clears det_last_error() like the dot. */
+int64_t __mind_blas_dot_l1_f32(int64_t a, int64_t b, int64_t len);
+/* Replaces __mind_blas_dot_l1_f32_v (vector-dialect twin, same schedule):
+ * src/mlir/lowering.rs:6219-6401 (emit_vec_dot_metric_f32, L1). */
+int64_t __mind_blas_dot_l1_f32_v(int64_t a, int64_t b, int64_t len);
+/* Replaces __mind_blas_dot_linf_f32(a, b, len): the largest |a[i] - b[i]|
+ * from 0.0f, a NaN difference skipped as by the reference's `d > m` test
+ * (runtime-support/mind_intrinsics.c:1353-1411; arity type_checker:2258). */
+int64_t __mind_blas_dot_linf_f32(int64_t a, int64_t b, int64_t len);
+/* Replaces __mind_blas_dot_linf_f32_v (arith.maximumf, lowering.rs:
+ * 6219-6401): the same maximum, or a NaN (0x7fc00000) once any difference is
+ * NaN. */
+int64_t __mind_blas_dot_linf_f32_v(int64_t a, int64_t b, int64_t len);
 /* Replaces __mind_blas_matmul_rmajor_f32(w, x, y, rows, cols): y[r] = the
  * strict dot of row r with x; -1 on a NULL pointer, 0 (y untouched) when
  * rows <= 0 or cols <= 0: runtime-support/mind_intrinsics.c:1418-1444. */
@@ -161,6 +182,12 @@ int64_t det_dot_i16(const int16_t *a, const int16_t *b, int64_t len);
  * dot; y[r] receives row r's dot with x.  Return 0 or a negative error. */
 int64_t det_dot_f32(const float *a, const float *b, int64_t len, float *out);
 int64_t det_matmul_rmajor_f32(const float *w, const float *x, float *y, int64_t rows, int64_t cols);
+/* y[r] = metric op (DET_F32_*) of W row r and x, each exactly the value of
+ * the matching single-vector symbol (dot / l1 / linf / linf_v) on that row:
+ * one query against many rows (no reference counterpart; the batched form of
+ * __mind_blas_dot_l1_f32 etc., as __mind_blas_matmul_rmajor_f32 is of the
+ * dot).  cols == 0 gives +0.0f rows. */
+int64_t det_rows_metric_f32(int64_t op, const float *w, const float *x, float *y, int64_t rows, int64_t cols);
 /* batch independent fft256 transforms, transform f at re + f * n and
  * im + f * n (the reference transforms one per call); batch * n <= 2^31
  * points, else DET_ERR_ARG. */
@@ -185,6 +212,8 @@ int64_t det_gemv_i16_dev(const int16_t *w, const int16_t *x, int32_t *y, int64_t
 int64_t det_dot_dev(int64_t op, const void *a, const void *b, int64_t len, int32_t *out, void *stream);
 int64_t det_matmul_rmajor_f32_dev(const float *w, const float *x, float *y, int64_t rows, int64_t cols,
                                   void *stream);
+int64_t det_rows_metric_f32_dev(int64_t op, const float *w, const float *x, float *y, int64_t rows, int64_t cols,
+                                void *stream);
 /* Device form of det_fft_q16 (n >= 4096 borrows the workspace arena, whose
  * size det_fft_workspace_bytes reports). */
 int64_t det_fft_q16_dev(int64_t *re, int64_t *im, const int64_t *tw, int64_t logn, int64_t n, int64_t batch,

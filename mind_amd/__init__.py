@@ -25,6 +25,7 @@ HEADER = os.path.join(os.path.dirname(HERE), "include", "mind_det.h")
 
 DET_OP_I8, DET_OP_I16, DET_OP_Q16 = 1, 2, 3
 DET_DOT_Q16, DET_DOT_L1_Q16, DET_DOT_I16 = 0, 1, 2
+DET_F32_DOT, DET_F32_L1, DET_F32_LINF, DET_F32_LINF_V = 0, 1, 2, 3
 DET_ERR_ARG, DET_ERR_HIP, DET_ERR_DEVICE = -22, -5, -19
 
 _i64 = ctypes.c_int64
@@ -59,7 +60,8 @@ def _bind(L):
     for name in ("det_dot_q16", "det_dot_l1_q16", "det_dot_i16"):
         f = getattr(L, name); f.argtypes = [_p, _p, _i64]; f.restype = _i64
     L.det_dot_dev.argtypes = [_i64, _p, _p, _i64, _p, _p]; L.det_dot_dev.restype = _i64
-    for name in ("__mind_blas_dot_f32", "__mind_blas_dot_f32_v", "dotf32"):
+    for name in ("__mind_blas_dot_f32", "__mind_blas_dot_f32_v", "dotf32", "__mind_blas_dot_l1_f32",
+                 "__mind_blas_dot_l1_f32_v", "__mind_blas_dot_linf_f32", "__mind_blas_dot_linf_f32_v"):
         f = getattr(L, name); f.argtypes = [_i64] * 3; f.restype = _i64
     for name in ("__mind_blas_matmul_rmajor_f32", "__mind_blas_matmul_rmajor_f32_v", "mmf32"):
         f = getattr(L, name); f.argtypes = [_i64] * 5; f.restype = _i64
@@ -73,6 +75,9 @@ def _bind(L):
     L.det_fft_workspace_bytes.argtypes = [_i64, _i64]; L.det_fft_workspace_bytes.restype = _i64
     L.det_matmul_rmajor_f32_dev.argtypes = [_p, _p, _p, _i64, _i64, _p]
     L.det_matmul_rmajor_f32_dev.restype = _i64
+    L.det_rows_metric_f32.argtypes = [_i64, _p, _p, _p, _i64, _i64]; L.det_rows_metric_f32.restype = _i64
+    L.det_rows_metric_f32_dev.argtypes = [_i64, _p, _p, _p, _i64, _i64, _p]
+    L.det_rows_metric_f32_dev.restype = _i64
     for name in ("det_matmul_i8", "det_matmul_i16", "det_matmul_q16"):
         f = getattr(L, name); f.argtypes = [_p, _p, _p, _i64, _i64, _i64]; f.restype = _i64
     for name in ("det_gemv_q16", "det_gemv_i16"):

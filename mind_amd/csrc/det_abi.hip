@@ -324,8 +324,9 @@ int64_t dot_host(int op, int64_t a, int64_t b, int64_t len) {
     return (int64_t)(int32_t)out;
 }
 
-// Host-pointer strict-FP f32 rows: y[r] = dot(W row r, x).  rows, cols > 0.
-int64_t f32_rows_host(const float *w, const float *x, float *y, int64_t rows, int64_t cols) {
+// Host-pointer strict-FP f32 rows: y[r] = metric met of (W row r, x).
+// rows, cols > 0.
+int64_t f32_rows_host(const float *w, const float *x, float *y, int64_t rows, int64_t cols, int met) {
     if (rows >= (1LL << 31) || cols >= (1LL << 31)) return set_err(DET_ERR_ARG, "dimension out of range [0, 2^31)");
     int64_t rc = 0;
     const int d = cur_device(&rc);
@@ -341,7 +342,7 @@ int64_t f32_rows_host(const float *w, const float *x, float *y, int64_t rows, in
     DET_HIP_CHECK(hipMemcpyAsync(io, w, bytes_w, hipMemcpyHostToDevice, s));
     DET_HIP_CHECK(hipMemcpyAsync(io + off_x, x, bytes_x, hipMemcpyHostToDevice, s));
     DET_HIP_CHECK(det::launch_rows_f32((const float *)io, (const float *)(io + off_x), (float *)(io + off_y), rows,
-                                       cols, s));
+                                       cols, met, s));
     DET_HIP_CHECK(hipMemcpyAsync(y, io + off_y, bytes_y, hipMemcpyDeviceToHost, s));
     DET_HIP_CHECK(hipStreamSynchronize(s));
     return 0;
@@ -357,11 +358,11 @@ int64_t pack_f32(float v) {
 // The packed f32 return cannot carry an error code (a failure returns the
 // bits of +0.0f), so the error text is cleared on entry: after the call an
 // empty det_last_error() means success.
-int64_t dot_f32_host(int64_t a, int64_t b, int64_t len) {
+int64_t dot_f32_host(int64_t a, int64_t b, int64_t len, int met = det::F32_DOT) {
     g_err[0] = 0;
     if (len <= 0 || !a || !b) return pack_f32(0.0f);
     float out = 0.0f;
-    if (f32_rows_host((const float *)(intptr_t)a, (const float *)(intptr_t)b, &out, 1, len) != 0) return 0;
+    if (f32_rows_host((const float *)(intptr_t)a, (const float *)(intptr_t)b, &out, 1, len, met) != 0) return 0;
     return pack_f32(out);
 }
 
@@ -475,14 +476,24 @@ int64_t __mind_blas_dot_l1_q16_v(int64_t a, int64_t b, int64_t len) { return dot
 int64_t __mind_blas_dot_i16_v(int64_t a, int64_t b, int64_t len) { return dot_host(det::DOT_I16, a, b, len); }
 int64_t __mind_blas_dot_f32(int64_t a, int64_t b, int64_t len) { return dot_f32_host(a, b, len); }
 int64_t __mind_blas_dot_f32_v(int64_t a, int64_t b, int64_t len) { return dot_f32_host(a, b, len); }
+int64_t __mind_blas_dot_l1_f32(int64_t a, int64_t b, int64_t len) { return dot_f32_host(a, b, len, det::F32_L1); }
+int64_t __mind_blas_dot_l1_f32_v(int64_t a, int64_t b, int64_t len) { return dot_f32_host(a, b, len, det::F32_L1); }
+int64_t __mind_blas_dot_linf_f32(int64_t a, int64_t b, int64_t len) {
+    return dot_f32_host(a, b, len, det::F32_LINF);
+}
+int64_t __mind_blas_dot_linf_f32_v(int64_t a, int64_t b, int64_t len) {
+    return dot_f32_host(a, b, len, det::F32_LINF_V);
+}
 int64_t __mind_blas_matmul_rmajor_f32(int64_t w, int64_t x, int64_t y, int64_t rows, int64_t cols) {
     if (!w || !x || !y) return -1;
     if (rows <= 0 || cols <= 0) return 0;
-    return f32_rows_host((const float *)(intptr_t)w, (const float *)(intptr_t)x, (float *)(intptr_t)y, rows, cols);
+    return f32_rows_host((const float *)(intptr_t)w, (const float *)(intptr_t)x, (float *)(intptr_t)y, rows, cols,
+                         det::F32_DOT);
 }
 int64_t __mind_blas_matmul_rmajor_f32_v(int64_t w, int64_t x, int64_t y, int64_t rows, int64_t cols) {
     if (!w || !x || !y || rows <= 0 || cols <= 0) return 0;
-    return f32_rows_host((const float *)(intptr_t)w, (const float *)(intptr_t)x, (float *)(intptr_t)y, rows, cols);
+    return f32_rows_host((const float *)(intptr_t)w, (const float *)(intptr_t)x, (float *)(intptr_t)y, rows, cols,
+                         det::F32_DOT);
 }
 
 // ====================================================================== layer 2
@@ -552,12 +563,12 @@ int64_t det_dot_f32(const float *a, const float *b, int64_t len, float *out) {
         *out = 0.0f;
         return 0;
     }
-    return f32_rows_host(a, b, out, 1, len);
+    return f32_rows_host(a, b, out, 1, len, det::F32_DOT);
 }
 int64_t det_matmul_rmajor_f32(const float *w, const float *x, float *y, int64_t rows, int64_t cols) {
     if (rows < 0 || cols < 0) return set_err(DET_ERR_ARG, "dimension out of range [0, 2^31)");
     if (rows == 0 || cols == 0 || !w || !x || !y) return 0;
-    return f32_rows_host(w, x, y, rows, cols);
+    return f32_rows_host(w, x, y, rows, cols, det::F32_DOT);
 }
 
 int64_t det_matmul_i8_dev(const int8_t *a, const int8_t *b, int32_t *c, int64_t m, int64_t k, int64_t n,
@@ -638,8 +649,36 @@ int64_t det_matmul_rmajor_f32_dev(const float *w, const float *x, float *y, int6
         return set_err(DET_ERR_ARG, "dimension out of range [0, 2^31)");
     if (rows == 0 || cols == 0) return 0;
     if (!w || !x || !y) return set_err(DET_ERR_ARG, "null device pointer");
-    DET_HIP_CHECK(det::launch_rows_f32(w, x, y, rows, cols, (hipStream_t)stream));
+    DET_HIP_CHECK(det::launch_rows_f32(w, x, y, rows, cols, det::F32_DOT, (hipStream_t)stream));
     return 0;
+}
+int64_t det_rows_metric_f32_dev(int64_t op, const float *w, const float *x, float *y, int64_t rows, int64_t cols,
+                                void *stream) {
+    if (op < DET_F32_DOT || op > DET_F32_LINF_V) return set_err(DET_ERR_ARG, "unknown f32 metric");
+    if (rows < 0 || cols < 0 || rows >= (1LL << 31) || cols >= (1LL << 31))
+        return set_err(DET_ERR_ARG, "dimension out of range [0, 2^31)");
+    if (rows == 0) return 0;
+    if (!y) return set_err(DET_ERR_ARG, "null device pointer");
+    hipStream_t s = (hipStream_t)stream;
+    if (cols == 0) {   // every metric of two empty vectors is +0.0f
+        DET_HIP_CHECK(zero_i32((int32_t *)y, (size_t)rows, s));
+        return 0;
+    }
+    if (!w || !x) return set_err(DET_ERR_ARG, "null device pointer");
+    DET_HIP_CHECK(det::launch_rows_f32(w, x, y, rows, cols, (int)op, s));
+    return 0;
+}
+int64_t det_rows_metric_f32(int64_t op, const float *w, const float *x, float *y, int64_t rows, int64_t cols) {
+    if (op < DET_F32_DOT || op > DET_F32_LINF_V) return set_err(DET_ERR_ARG, "unknown f32 metric");
+    if (rows < 0 || cols < 0) return set_err(DET_ERR_ARG, "dimension out of range [0, 2^31)");
+    if (rows == 0) return 0;
+    if (!y) return set_err(DET_ERR_ARG, "null pointer");
+    if (cols == 0) {
+        memset(y, 0, (size_t)rows * 4);
+        return 0;
+    }
+    if (!w || !x) return set_err(DET_ERR_ARG, "null pointer");
+    return f32_rows_host(w, x, y, rows, cols, (int)op);
 }
 int64_t det_fft_q16(int64_t *re, int64_t *im, const int64_t *tw, int64_t logn, int64_t n, int64_t batch) {
     return fft_host((int64_t)(intptr_t)re, (int64_t)(intptr_t)im, (int64_t)(intptr_t)tw, logn, n, batch);

@@ -22,6 +22,15 @@
 // them in index order and adds the tail.  FP contraction is off for the
 // whole file, and f32 denormals are kept (gfx950's default IEEE mode), as on
 // the reference's CPUs.
+//
+// The same schedule serves the reference's f32 distances (MET template
+// argument): L1 (mind_intrinsics.c:1286-1351, lowering.rs:6219-6401) sums
+// |a - b| -- the sign bit cleared, as the reference's scalar and AVX2 paths
+// both do -- in place of a * b; L-infinity keeps the larger of acc and
+// |a - b|, which is order-free, so the 8 chains give the reference's
+// sequential result: Track A (mind_intrinsics.c:1353-1411) skips a NaN
+// difference (it fails the reference's `d > m` test), the vector twin
+// (arith.maximumf) returns NaN (0x7fc00000 here) once any difference is NaN.
 #include "det_common.h"
 #include "det_kernels.h"
 
@@ -31,6 +40,19 @@ namespace det {
 namespace f32 {
 
 constexpr int THREADS = 256;
+
+// the per-element term of metric MET, and how a chain takes it in
+template <int MET>
+__device__ __forceinline__ float term(float a, float b) {
+    if constexpr (MET == F32_DOT) return a * b;
+    else return __uint_as_float(__float_as_uint(a - b) & 0x7fffffffu);
+}
+template <int MET>
+__device__ __forceinline__ float comb(float acc, float t) {
+    if constexpr (MET == F32_DOT || MET == F32_L1) return acc + t;
+    else if constexpr (MET == F32_LINF) return t > acc ? t : acc;
+    else return (acc != acc || t != t) ? __uint_as_float(0x7fc00000u) : (t > acc ? t : acc);
+}
 
 template <int C, bool VEC>
 __device__ __forceinline__ void load_step(const float *p, float (&v)[C]) {
@@ -50,7 +72,7 @@ __device__ __forceinline__ void load_step(const float *p, float (&v)[C]) {
 }
 
 // y[row] = strict dot(W row, x); rows * T threads, T = 8 / C per row.
-template <int C, int U, int G, bool VEC>
+template <int MET, int C, int U, int G, bool VEC>
 __global__ __launch_bounds__(THREADS) void rows_kernel(const float *__restrict__ W, const float *__restrict__ x,
                                                        float *__restrict__ y, int64_t rows, int64_t cols) {
     constexpr int T = 8 / C;
@@ -86,8 +108,7 @@ __global__ __launch_bounds__(THREADS) void rows_kernel(const float *__restrict__
                 for (int u = g * (U / G); u < (g + 1) * (U / G); ++u)
 #pragma unroll
                     for (int c = 0; c < C; ++c) {
-                        const float p = wv[u][c] * xv[u][c];
-                        acc[c] = acc[c] + p;
+                        acc[c] = comb<MET>(acc[c], term<MET>(wv[u][c], xv[u][c]));
                     }
 #pragma unroll
                 for (int u = g * (U / G); u < (g + 1) * (U / G); ++u) {
@@ -104,8 +125,7 @@ __global__ __launch_bounds__(THREADS) void rows_kernel(const float *__restrict__
         load_step<C, VEC>(xq + s * 8, xv);
 #pragma unroll
         for (int c = 0; c < C; ++c) {
-            const float p = wv[c] * xv[c];
-            acc[c] = acc[c] + p;
+            acc[c] = comb<MET>(acc[c], term<MET>(wv[c], xv[c]));
         }
     }
     // gather the row's 8 chains into its first thread, in chain order
@@ -118,10 +138,9 @@ __global__ __launch_bounds__(THREADS) void rows_kernel(const float *__restrict__
     if (live && q == 0) {
         float s = lanes[0];
 #pragma unroll
-        for (int t = 1; t < 8; ++t) s = s + lanes[t];
+        for (int t = 1; t < 8; ++t) s = comb<MET>(s, lanes[t]);
         for (int64_t i = nsteps * 8; i < cols; ++i) {
-            const float p = wr[i] * x[i];
-            s = s + p;
+            s = comb<MET>(s, term<MET>(wr[i], x[i]));
         }
         y[row] = s;
     }
@@ -136,7 +155,7 @@ __global__ __launch_bounds__(THREADS) void rows_kernel(const float *__restrict__
 // in large contiguous bursts, which keeps HBM pages hot whatever the row
 // stride; the chains then run from LDS (row stride KC * 4 + 32 bytes, so the
 // 64 lanes' reads of W fall in 64 distinct banks; x reads are broadcasts).
-template <int KC, int NS>
+template <int MET, int KC, int NS>
 __global__ __launch_bounds__(64) void rows_dma_kernel(const float *__restrict__ W, const float *__restrict__ x,
                                                       float *__restrict__ y, int64_t rows, int64_t cols) {
     constexpr int RS = KC * 4 + 32;            // LDS bytes per row in a stage
@@ -191,13 +210,11 @@ __global__ __launch_bounds__(64) void rows_dma_kernel(const float *__restrict__ 
             __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
             for (int i = 0; i < KC / 8; ++i) {
-                const float p = wv[i] * xv[i];
-                acc = acc + p;
+                acc = comb<MET>(acc, term<MET>(wv[i], xv[i]));
             }
         } else {
             for (int i = 0; i < (int)left; ++i) {
-                const float p = ws[8 * i] * xs[8 * i];
-                acc = acc + p;
+                acc = comb<MET>(acc, term<MET>(ws[8 * i], xs[8 * i]));
             }
         }
         asm volatile("" ::: "memory");
@@ -209,11 +226,10 @@ __global__ __launch_bounds__(64) void rows_dma_kernel(const float *__restrict__ 
     if (r < nr && j == 0) {
         float s = lanes[0];
 #pragma unroll
-        for (int t = 1; t < 8; ++t) s = s + lanes[t];
+        for (int t = 1; t < 8; ++t) s = comb<MET>(s, lanes[t]);
         const float *wr = W + (row0 + r) * cols;
         for (int64_t i = nsteps * 8; i < cols; ++i) {
-            const float p = wr[i] * x[i];
-            s = s + p;
+            s = comb<MET>(s, term<MET>(wr[i], x[i]));
         }
         y[row0 + r] = s;
     }
@@ -237,7 +253,8 @@ __global__ __launch_bounds__(64) void rows_dma_kernel(const float *__restrict__ 
 
 }  // namespace f32
 
-hipError_t launch_rows_f32(const float *W, const float *x, float *y, int64_t rows, int64_t cols, hipStream_t s) {
+template <int MET>
+static void launch_rows_met(const float *W, const float *x, float *y, int64_t rows, int64_t cols, hipStream_t s) {
     using namespace f32;
     constexpr int C = DET_F32_C, U = DET_F32_U, G = DET_F32_G, T = 8 / C;
     // LDS DMA path: 16-byte aligned rows and x, and 8 rows (plus a chunk of
@@ -250,15 +267,26 @@ hipError_t launch_rows_f32(const float *W, const float *x, float *y, int64_t row
         const int64_t n = rows - r0 < CHUNK ? rows - r0 : CHUNK;
         const float *Wc = W + r0 * cols;
         if (dma) {
-            hipLaunchKernelGGL((rows_dma_kernel<DET_F32_KC, DET_F32_NS>), dim3((unsigned)((n + 7) / 8)), dim3(64), 0,
-                               s, Wc, x, y + r0, n, cols);
+            hipLaunchKernelGGL((rows_dma_kernel<MET, DET_F32_KC, DET_F32_NS>), dim3((unsigned)((n + 7) / 8)), dim3(64),
+                               0, s, Wc, x, y + r0, n, cols);
             continue;
         }
         const dim3 grid((unsigned)((n * T + THREADS - 1) / THREADS));
         if (vec)
-            hipLaunchKernelGGL((rows_kernel<C, U, G, true>), grid, dim3(THREADS), 0, s, Wc, x, y + r0, n, cols);
+            hipLaunchKernelGGL((rows_kernel<MET, C, U, G, true>), grid, dim3(THREADS), 0, s, Wc, x, y + r0, n, cols);
         else
-            hipLaunchKernelGGL((rows_kernel<C, U, G, false>), grid, dim3(THREADS), 0, s, Wc, x, y + r0, n, cols);
+            hipLaunchKernelGGL((rows_kernel<MET, C, U, G, false>), grid, dim3(THREADS), 0, s, Wc, x, y + r0, n, cols);
+    }
+}
+
+hipError_t launch_rows_f32(const float *W, const float *x, float *y, int64_t rows, int64_t cols, int met,
+                           hipStream_t s) {
+    switch (met) {
+    case F32_DOT: launch_rows_met<F32_DOT>(W, x, y, rows, cols, s); break;
+    case F32_L1: launch_rows_met<F32_L1>(W, x, y, rows, cols, s); break;
+    case F32_LINF: launch_rows_met<F32_LINF>(W, x, y, rows, cols, s); break;
+    case F32_LINF_V: launch_rows_met<F32_LINF_V>(W, x, y, rows, cols, s); break;
+    default: return hipErrorInvalidValue;
     }
     return hipGetLastError();
 }

@@ -66,9 +66,13 @@ hipError_t launch_gemv_q16_mfma(const int32_t *W, const int32_t *X, int32_t *Y, 
 // (DOT_I16); *out (one device uint32) is overwritten.
 enum { DOT_Q16 = 0, DOT_L1 = 1, DOT_I16 = 2 };
 hipError_t launch_dot(int op, const void *a, const void *b, int64_t n, uint32_t *out, hipStream_t s);
-// Strict-FP f32: y[r] = the reference's pinned 8-lane dot of W row r with x
-// (no fused multiply-add, fixed fold order); rows > 0, cols > 0.
-hipError_t launch_rows_f32(const float *W, const float *x, float *y, int64_t rows, int64_t cols, hipStream_t s);
+// Strict-FP f32: y[r] = metric met of W row r and x on the reference's
+// pinned 8-lane schedule: F32_DOT (no fused multiply-add, fixed fold order),
+// F32_L1 (sum of sign-cleared differences), F32_LINF (max, NaN skipped),
+// F32_LINF_V (max, NaN once any difference is NaN); rows > 0, cols > 0.
+enum { F32_DOT = 0, F32_L1 = 1, F32_LINF = 2, F32_LINF_V = 3 };
+hipError_t launch_rows_f32(const float *W, const float *x, float *y, int64_t rows, int64_t cols, int met,
+                           hipStream_t s);
 // y[M] = int16 GEMV.
 hipError_t launch_gemv_i16(const int16_t *W, const int16_t *x, int32_t *y, int M, int K, hipStream_t s);
 

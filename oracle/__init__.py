@@ -52,6 +52,11 @@ def lib():
         L.det_or_dot_f32.restype = ctypes.c_float
         L.det_or_matmul_rmajor_f32.argtypes = [_p, _p, _p, _i64, _i64]
         L.det_or_matmul_rmajor_f32.restype = None
+        for name in ("det_or_dot_l1_f32", "det_or_dot_linf_f32", "det_or_dot_linf_f32_v"):
+            getattr(L, name).argtypes = [_p, _p, _i64]
+            getattr(L, name).restype = ctypes.c_uint32
+        L.det_or_rows_metric_f32.argtypes = [ctypes.c_int, _p, _p, _p, _i64, _i64]
+        L.det_or_rows_metric_f32.restype = None
         for name in ("det_or_gen_q16", "det_or_gen_q16_sat"):
             getattr(L, name).argtypes = [_u64, ctypes.c_int, _p, _i64, _p, _i64]
             getattr(L, name).restype = None
@@ -113,7 +118,8 @@ def ref_lib():
     global _ref
     if _ref is None and os.path.exists(REF_PATH):
         R = ctypes.CDLL(REF_PATH)
-        for name in ("__mind_blas_dot_q16", "__mind_blas_dot_l1_q16", "__mind_blas_dot_f32"):
+        for name in ("__mind_blas_dot_q16", "__mind_blas_dot_l1_q16", "__mind_blas_dot_f32",
+                     "__mind_blas_dot_l1_f32", "__mind_blas_dot_linf_f32"):
             getattr(R, name).argtypes = [_i64, _i64, _i64]
             getattr(R, name).restype = _i64
         R.__mind_blas_matmul_rmajor_f32.argtypes = [_i64] * 5
@@ -292,6 +298,27 @@ def matmul_rmajor_f32(W, x, rows, cols):
     W = _c(W, np.float32); x = _c(x, np.float32)
     y = np.empty(rows, np.float32)
     lib().det_or_matmul_rmajor_f32(_ptr(W), _ptr(x), _ptr(y), rows, cols)
+    return y
+
+
+F32_DOT, F32_L1, F32_LINF, F32_LINF_V = 0, 1, 2, 3
+
+
+def dist_f32_bits(op, a, b) -> int:
+    """f32 distance op (F32_L1, F32_LINF, F32_LINF_V) as the reference packs
+    it: the f32 bits in the low 32 bits of a non-negative int64."""
+    a = _c(a, np.float32); b = _c(b, np.float32)
+    if op == F32_DOT:
+        return dot_f32_bits(a, b)
+    fn = {F32_L1: "det_or_dot_l1_f32", F32_LINF: "det_or_dot_linf_f32", F32_LINF_V: "det_or_dot_linf_f32_v"}[op]
+    return int(getattr(lib(), fn)(_ptr(a), _ptr(b), len(a)))
+
+
+def rows_metric_f32_bits(op, W, x, rows, cols):
+    """y[r] = op(W row r, x) as uint32 bits."""
+    W = _c(W, np.float32); x = _c(x, np.float32)
+    y = np.empty(rows, np.uint32)
+    lib().det_or_rows_metric_f32(op, _ptr(W), _ptr(x), _ptr(y), rows, cols)
     return y
 
 

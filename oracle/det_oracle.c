@@ -15,6 +15,7 @@
 
 #include <math.h>
 #include <stddef.h>
+#include <string.h>
 
 /* benches/det_matmul_q16.rs:196-205:  s <- s*1664525 + 1013904223 (mod 2^64);
  * sample = (u32)(s >> 16). */
@@ -188,6 +189,81 @@ float det_or_dot_f32(const float *a, const float *b, int64_t len) {
 
 void det_or_matmul_rmajor_f32(const float *W, const float *x, float *y, int64_t rows, int64_t cols) {
     for (int64_t r = 0; r < rows; ++r) y[r] = det_or_dot_f32(W + r * cols, x, cols);
+}
+
+/* |x| by clearing the sign bit (runtime-support/mind_intrinsics.c:1210-1217,
+ * the scalar twin of the AVX2 and-mask): -0.0 -> +0.0, NaN keeps its payload. */
+static float or_abs_bits(float x) {
+    uint32_t u;
+    memcpy(&u, &x, 4);
+    u &= 0x7fffffffu;
+    memcpy(&x, &u, 4);
+    return x;
+}
+
+static uint32_t or_bits(float x) {
+    uint32_t u;
+    memcpy(&u, &x, 4);
+    return u;
+}
+
+/* L1: mind_intrinsics.c:1293-1308 (scalar) -- the dot's 8-lane schedule with
+ * |a - b| for the product: lane j sums positions j, j+8, ... in order, the
+ * lanes fold left to right, then the len % 8 tail in order. */
+uint32_t det_or_dot_l1_f32(const float *a, const float *b, int64_t len) {
+    if (len <= 0 || a == NULL || b == NULL) return 0;
+    float acc[8] = {0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f};
+    int64_t i = 0;
+    for (; i + 8 <= len; i += 8)
+        for (int j = 0; j < 8; ++j) acc[j] = acc[j] + or_abs_bits(a[i + j] - b[i + j]);
+    float s = acc[0];
+    for (int j = 1; j < 8; ++j) s = s + acc[j];
+    for (; i < len; ++i) s = s + or_abs_bits(a[i] - b[i]);
+    return or_bits(s);
+}
+
+/* L-infinity, Track A: mind_intrinsics.c:1355-1365 (scalar) -- m = 0; for
+ * each i: d = a - b, negated when d < 0, kept when d > m.  A NaN d fails both
+ * comparisons and is skipped. */
+uint32_t det_or_dot_linf_f32(const float *a, const float *b, int64_t len) {
+    if (len <= 0 || a == NULL || b == NULL) return 0;
+    float m = 0.0f;
+    for (int64_t i = 0; i < len; ++i) {
+        float d = a[i] - b[i];
+        if (d < 0.0f) d = -d;
+        if (d > m) m = d;
+    }
+    return or_bits(m);
+}
+
+/* L-infinity, vector twin: src/mlir/lowering.rs:6219-6401
+ * (emit_vec_dot_metric_f32, VecMetric::Linf) -- arith.maximumf over the
+ * sign-masked differences from 0.0: IEEE 754-2019 maximum, so any NaN
+ * difference makes the result NaN.  Which NaN the reference returns is not
+ * fixed by its lowering; this returns the quiet NaN 0x7fc00000. */
+uint32_t det_or_dot_linf_f32_v(const float *a, const float *b, int64_t len) {
+    if (len <= 0 || a == NULL || b == NULL) return 0;
+    float m = 0.0f;
+    for (int64_t i = 0; i < len; ++i) {
+        const float d = or_abs_bits(a[i] - b[i]);
+        if (d != d) return 0x7fc00000u;
+        if (d > m) m = d;
+    }
+    return or_bits(m);
+}
+
+/* Row-major batched form: y[r] = metric(W row r, x), op 0 = dot, 1 = L1,
+ * 2 = L-infinity (Track A), 3 = L-infinity (vector twin); results as bits. */
+void det_or_rows_metric_f32(int op, const float *W, const float *x, uint32_t *y, int64_t rows, int64_t cols) {
+    for (int64_t r = 0; r < rows; ++r) {
+        const float *w = W + r * cols;
+        uint32_t v = 0;
+        if (op == 0) v = or_bits(det_or_dot_f32(w, x, cols));
+        else if (op == 1) v = det_or_dot_l1_f32(w, x, cols);
+        else if (op == 2) v = det_or_dot_linf_f32(w, x, cols);
+        else v = det_or_dot_linf_f32_v(w, x, cols);
+        y[r] = v;
+    }
 }
 
 void det_or_gen_f32_unit(uint64_t seed, float *a, int64_t na, float *b, int64_t nb) {

@@ -28,6 +28,16 @@
  *   det_or_matmul_rmajor_f32  matmul-f32-v-64x64 (ec5adb99...); the reference's
  *                          own __mind_blas_dot_f32 / __mind_blas_matmul_rmajor_f32
  *                          on both of its dispatch paths (oracle/_ref).
+ *   det_or_dot_l1_f32,  -> the reference's own __mind_blas_dot_l1_f32 /
+ *   det_or_dot_linf_f32    __mind_blas_dot_linf_f32 on both dispatch paths
+ *                          (oracle/_ref; outputs in tests/golden/
+ *                          dot_f32_metric_ref.json); exact closed forms (L-inf
+ *                          = numpy max |a - b|, L1 of equal vectors = 0,
+ *                          L1 of one block of 8 = the lane fold).
+ *   det_or_dot_linf_f32_v -> the Track A max where no difference is NaN (the
+ *                          reference's own lowering, lowering.rs:6219-6401,
+ *                          is MLIR text that does not build here); NaN cases
+ *                          pinned by the maximumf definition only.
  *   det_or_gen_*        -> the golden hashes above fix the reference draw order
  *                          and sample maps (next_i8 / next_i16 / next_q16).
  */
@@ -102,6 +112,15 @@ int64_t det_or_dot_l1_q16(const int32_t *a, const int32_t *b, int64_t len);
 float det_or_dot_f32(const float *a, const float *b, int64_t len);
 /* y[r] = det_or_dot_f32(W + r*cols, x, cols). */
 void det_or_matmul_rmajor_f32(const float *W, const float *x, float *y, int64_t rows, int64_t cols);
+/* f32 distances, results as their f32 bits (len <= 0 or NULL -> 0):
+ * L1 = sum |a - b| on the dot's 8-lane schedule (sign-bit |x|);
+ * L-infinity Track A = max over the non-NaN |a - b| (NaN skipped);
+ * L-infinity vector twin = the same max, or 0x7fc00000 if any |a - b| is NaN. */
+uint32_t det_or_dot_l1_f32(const float *a, const float *b, int64_t len);
+uint32_t det_or_dot_linf_f32(const float *a, const float *b, int64_t len);
+uint32_t det_or_dot_linf_f32_v(const float *a, const float *b, int64_t len);
+/* y[r] = op(W row r, x) as bits: op 0 dot, 1 L1, 2 L-inf, 3 L-inf vector twin. */
+void det_or_rows_metric_f32(int op, const float *W, const float *x, uint32_t *y, int64_t rows, int64_t cols);
 /* f32 samples in [-1, 1): ((float)u32 / (float)UINT32_MAX) * 2 - 1, a then b
  * (tests/cross_substrate_identity.rs:2579-2598). */
 void det_or_gen_f32_unit(uint64_t seed, float *a, int64_t na, float *b, int64_t nb);

@@ -247,6 +247,84 @@ def test_dot_f32_vs_oracle(n, fam):
         assert f32_same(bits_to_f32(M.dot_f32_bits(a[1:], b[:-1])), bits_to_f32(O.dot_f32_bits(a[1:], b[:-1])))
 
 
+F32_METRIC_SYMS = [("__mind_blas_dot_l1_f32", O.F32_L1), ("__mind_blas_dot_l1_f32_v", O.F32_L1),
+                   ("__mind_blas_dot_linf_f32", O.F32_LINF), ("__mind_blas_dot_linf_f32_v", O.F32_LINF_V)]
+
+
+def test_f32_metric_reference_vectors():
+    """Every symbol on the committed outputs of the reference's own L1 / L-inf
+    (tests/golden/dot_f32_metric_ref.json; the vector twins equal them except
+    L-inf_v on NaN, which follows the oracle)."""
+    import importlib.util
+    spec = importlib.util.spec_from_file_location("mk_f32_metric", os.path.join(GOLD, "make_ref_f32_metric_vectors.py"))
+    mod = importlib.util.module_from_spec(spec)
+    spec.loader.exec_module(mod)
+    cases = json.load(open(os.path.join(GOLD, "dot_f32_metric_ref.json")))["cases"]
+    with np.errstate(all="ignore"):
+        for c in cases:
+            a, b = mod.inputs(c["family"], c["seed"], c["len"])
+            n = c["len"]
+            for sym, op in F32_METRIC_SYMS:
+                note(f"{sym} {c['family']} n={n}")
+                got = getattr(M.lib(), sym)(addr(a) if n else 0, addr(b) if n else 0, n)
+                want = {O.F32_L1: c["l1_scalar"], O.F32_LINF: c["linf_scalar"]}.get(op)
+                if want is None:
+                    want = O.dist_f32_bits(op, a, b)
+                assert f32_same(bits_to_f32(got), bits_to_f32(want)), (sym, c["family"], n, hex(got), hex(want))
+                assert M.lib().det_last_error() in (None, b"")
+
+
+@pytest.mark.parametrize("n", F32_LENS)
+@pytest.mark.parametrize("fam", ["unit", "wide", "special"])
+def test_f32_metrics_vs_oracle(n, fam):
+    a, b = f32_family(fam, 0xF38 ^ (n * 137) ^ len(fam), n)
+    with np.errstate(all="ignore"):
+        for sym, op in F32_METRIC_SYMS:
+            note(f"{sym} {fam} n={n}")
+            got = getattr(M.lib(), sym)(addr(a) if n else 0, addr(b) if n else 0, n)
+            assert f32_same(bits_to_f32(got), bits_to_f32(O.dist_f32_bits(op, a, b))), (sym, hex(got))
+
+
+F32_METRIC_ROWS = [(1, 1), (3, 5), (9, 100), (17, 256), (70, 777), (4099, 1024), (5, 65541), (2, 265)]
+
+
+@pytest.mark.parametrize("rows,cols", F32_METRIC_ROWS, ids=[f"{r}x{c}" for r, c in F32_METRIC_ROWS])
+def test_rows_metric_f32_vs_oracle(rows, cols):
+    """One query against many rows, host and device entry points, every
+    metric and input family (cols % 4 == 0 takes the LDS DMA kernel)."""
+    s = M.Stream()
+    for fam in ("unit", "wide", "special"):
+        W, _ = f32_family(fam, 0xF39 ^ rows * 7 ^ cols, rows * cols)
+        x, _ = f32_family(fam, 0xF3A ^ rows ^ cols * 5, cols)
+        dW, dx, dy = M.DeviceBuffer.from_array(W), M.DeviceBuffer.from_array(x), M.DeviceBuffer(4 * rows)
+        for op in (O.F32_DOT, O.F32_L1, O.F32_LINF, O.F32_LINF_V):
+            with np.errstate(all="ignore"):
+                want = O.rows_metric_f32_bits(op, W, x, rows, cols).view(np.float32)
+            note(f"det_rows_metric_f32[_dev] op={op} {fam} rows={rows} cols={cols}")
+            y = np.full(rows, np.nan, np.float32)
+            M.check(M.lib().det_rows_metric_f32(op, addr(W), addr(x), addr(y), rows, cols))
+            assert f32_same(y, want), (fam, op)
+            dy.fill(0x7F)
+            M.check(M.lib().det_rows_metric_f32_dev(op, dW.ptr, dx.ptr, dy.ptr, rows, cols, s.ptr))
+            s.sync()
+            assert f32_same(dy.to_array(np.float32, (rows,)), want), (fam, op)
+        for buf in (dW, dx, dy):
+            buf.free()
+    s.destroy()
+
+
+def test_rows_metric_f32_arguments():
+    L = M.lib()
+    y = np.full(3, np.nan, np.float32)
+    assert L.det_rows_metric_f32(4, 0, 0, addr(y), 3, 5) == M.DET_ERR_ARG
+    assert L.det_rows_metric_f32(-1, 0, 0, addr(y), 3, 5) == M.DET_ERR_ARG
+    assert L.det_rows_metric_f32(O.F32_L1, 0, 0, addr(y), 3, 0) == 0 and not np.any(y.view(np.uint32))
+    assert L.det_rows_metric_f32(O.F32_L1, 0, 0, 0, 0, 5) == 0
+    assert L.det_rows_metric_f32(O.F32_L1, 0, 0, addr(y), 3, 5) == M.DET_ERR_ARG
+    for sym, _ in F32_METRIC_SYMS:
+        assert getattr(L, sym)(0, 0, 16) == 0 and getattr(L, sym)(addr(y), addr(y), 0) == 0
+
+
 # cols % 4 == 0 (16-byte rows) take the LDS DMA kernel: one chunk is 256
 # floats, so 4, 8, 100, 252 and 1000 end in a partial chunk, 256 / 2048 are
 # whole chunks, 260 / 772 add a tail past whole chunks; row counts that are

@@ -157,6 +157,116 @@ def test_f32_strict_matches_reference_live():
         R.__mind_blas_set_use_avx2(prev)
 
 
+def _metric_golden():
+    import importlib.util
+    spec = importlib.util.spec_from_file_location("mk_f32_metric", os.path.join(GOLD, "make_ref_f32_metric_vectors.py"))
+    mod = importlib.util.module_from_spec(spec)
+    spec.loader.exec_module(mod)
+    return mod.inputs, json.load(open(os.path.join(GOLD, "dot_f32_metric_ref.json")))["cases"]
+
+
+def test_f32_metrics_match_reference_vectors():
+    """L1 / L-inf restatements against the committed outputs of the
+    reference's own __mind_blas_dot_l1_f32 / __mind_blas_dot_linf_f32
+    (both dispatch paths agree on every case)."""
+    inputs, cases = _metric_golden()
+    assert len(cases) == 39
+    with np.errstate(all="ignore"):
+        for c in cases:
+            a, b = inputs(c["family"], c["seed"], c["len"])
+            assert c["l1_scalar"] == c["l1_avx2"] and c["linf_scalar"] == c["linf_avx2"]
+            assert O.dist_f32_bits(O.F32_L1, a, b) == c["l1_scalar"], c
+            assert O.dist_f32_bits(O.F32_LINF, a, b) == c["linf_scalar"], c
+
+
+@pytest.mark.skipif(not O.ref_built(), reason="oracle/_ref not built (reference tree absent)")
+def test_f32_metrics_match_reference_live():
+    R = O.ref_lib()
+    prev = R.__mind_blas_set_use_avx2(0)
+    rng = np.random.default_rng(0x71)
+    try:
+        for avx2 in (0, 1):
+            R.__mind_blas_set_use_avx2(avx2)
+            for n in list(range(0, 18)) + [4093, 65541]:
+                u = rng.integers(0, 1 << 32, 2 * n, dtype=np.uint64).astype(np.uint32)
+                u = np.where((u & 0x7f800000) == 0x7f800000, u & 0xbfffffff, u)   # finite, any exponent
+                for a, b in (O.gen_f32_unit(0xF32 ^ n, n, n), _f32_special_pair(n, n),
+                             (u[:n].view(np.float32).copy(), u[n:].view(np.float32).copy())):
+                    pa, pb = (a.ctypes.data, b.ctypes.data) if n else (0, 0)
+                    with np.errstate(all="ignore"):
+                        assert O.dist_f32_bits(O.F32_L1, a, b) == R.__mind_blas_dot_l1_f32(pa, pb, n)
+                        assert O.dist_f32_bits(O.F32_LINF, a, b) == R.__mind_blas_dot_linf_f32(pa, pb, n)
+    finally:
+        R.__mind_blas_set_use_avx2(prev)
+
+
+def test_f32_metric_closed_forms():
+    rng = np.random.default_rng(0x72)
+    with np.errstate(all="ignore"):
+        for n in (1, 7, 8, 9, 64, 1000, 4093):
+            a = rng.standard_normal(n).astype(np.float32) * np.float32(1e3)
+            b = rng.standard_normal(n).astype(np.float32)
+            d = np.abs(a - b)
+            # L-inf is a max: exact, whatever the order
+            assert O.dist_f32_bits(O.F32_LINF, a, b) == int(d.max().view(np.uint32))
+            assert O.dist_f32_bits(O.F32_LINF_V, a, b) == int(d.max().view(np.uint32))
+            # a vector against itself
+            assert O.dist_f32_bits(O.F32_L1, a, a) == 0 and O.dist_f32_bits(O.F32_LINF, a, a) == 0
+            # L1 against zero: the pinned 8-lane fold of |a|, against an
+            # independent numpy evaluation of that order
+            z = np.zeros(n, np.float32)
+            lanes = np.zeros(8, np.float32)
+            m = n // 8 * 8
+            for i in range(0, m, 8):
+                lanes = (lanes + np.abs(a[i:i + 8])).astype(np.float32)
+            s = lanes[0]
+            for j in range(1, 8):
+                s = np.float32(s + lanes[j])
+            for i in range(m, n):
+                s = np.float32(s + np.abs(a[i]))
+            assert O.dist_f32_bits(O.F32_L1, a, z) == int(np.float32(s).view(np.uint32))
+            # within rounding of the float64 sum
+            assert abs(float(np.float32(s)) - float(np.abs(a.astype(np.float64)).sum())) <= 1e-5 * float(np.abs(a).sum())
+        # NaN: Track A skips a NaN difference, the vector twin returns NaN
+        a = np.array([1.0, np.nan, -3.0, 2.0], np.float32)
+        b = np.array([0.0, 0.0, 0.0, np.inf], np.float32)
+        assert O.dist_f32_bits(O.F32_LINF, a, b) == int(np.float32(np.inf).view(np.uint32))
+        assert O.dist_f32_bits(O.F32_LINF_V, a, b) == 0x7fc00000
+        assert O.dist_f32_bits(O.F32_LINF, a[[0, 2]], b[[0, 2]]) == int(np.float32(3.0).view(np.uint32))
+        assert np.isnan(np.uint32(O.dist_f32_bits(O.F32_L1, a, b)).view(np.float32))
+        # signed zero: |-0 - 0| is +0 under the sign-bit clear
+        assert O.dist_f32_bits(O.F32_L1, np.array([-0.0], np.float32), np.array([0.0], np.float32)) == 0
+        # the rows form is the single-vector form per row
+        W = rng.standard_normal(5 * 37).astype(np.float32)
+        x = rng.standard_normal(37).astype(np.float32)
+        for op in (O.F32_DOT, O.F32_L1, O.F32_LINF, O.F32_LINF_V):
+            y = O.rows_metric_f32_bits(op, W, x, 5, 37)
+            assert [int(v) for v in y] == [O.dist_f32_bits(op, W[r * 37:(r + 1) * 37], x) for r in range(5)]
+
+
+def test_f32_metric_golden_rejects_a_pairwise_fold():
+    """A mistake the golden data catches: folding the 8 L1 lanes pairwise
+    instead of left to right changes the bits of some reference case."""
+    inputs, cases = _metric_golden()
+    changed = 0
+    with np.errstate(all="ignore"):
+        for c in cases:
+            if c["family"] == "special" or c["len"] < 16:
+                continue
+            a, b = inputs(c["family"], c["seed"], c["len"])
+            d = np.abs(a - b)
+            m = len(d) // 8 * 8
+            lanes = np.zeros(8, np.float32)
+            for i in range(0, m, 8):
+                lanes = (lanes + d[i:i + 8]).astype(np.float32)
+            p = ((lanes[0] + lanes[1]) + (lanes[2] + lanes[3])) + ((lanes[4] + lanes[5]) + (lanes[6] + lanes[7]))
+            s = np.float32(p)
+            for i in range(m, len(d)):
+                s = np.float32(s + d[i])
+            changed += int(np.float32(s).view(np.uint32)) != c["l1_scalar"]
+    assert changed > 0
+
+
 def test_dot_l1_q16_brute_force_and_extremes():
     # exact Python ints: (int64)(int32) sum |a - b|, including |INT32_MIN - INT32_MAX|
     # = 2^32 - 1 per term (wraps the int32 result) and the empty / length-1 cases
