@@ -548,7 +548,12 @@ __global__ __launch_bounds__(THREADS, 1) void gemm_i8_dma_kernel(const int8_t *_
 #pragma unroll
                 for (int j = 0; j < 2; ++j) {
                     const int col = n0 + wn + j * 32 + l32;
-                    if (!MASK || col < nst) __builtin_nontemporal_store(acc[i][j][r], crow + col);
+                    // masked rows (ldc != N) store partial lines: plain stores merge them in L2
+                    if constexpr (MASK) {
+                        if (col < nst) crow[col] = acc[i][j][r];
+                    } else {
+                        __builtin_nontemporal_store(acc[i][j][r], crow + col);
+                    }
                 }
             }
         }
@@ -733,12 +738,19 @@ __global__ __launch_bounds__(THREADS, 1) void gemm_i8_h128_kernel(const int8_t *
     // is a wave-uniform row pointer plus this lane's byte offset (4 lh rows and
     // l32 columns, below 2^32 since ldc < 2^24)
     const uint32_t lane_b = (uint32_t)(4 * lh) * (uint32_t)ldc * 4u + (uint32_t)l32 * 4u;
+    // Non-temporal stores (streamed past L2) for whole rows; a masked tile
+    // stores rows of ldc != N words, whose partial 128-byte lines merge
+    // better in L2 (4095^3: 3% faster with plain stores, 4096^3 slower)
     auto store_c = [&](const v16i32 (&v)[MI][NJ], int tm0, int tn0, int e) __attribute__((always_inline)) {
         const int i = e / (16 * NJ), r = (e / NJ) & 15, j = e % NJ;
         const int rowu = tm0 + wm + i * 32 + 8 * (r >> 2) + (r & 3);   // wave-uniform part
         const int colu = tn0 + wn + 32 * j;
         int32_t *dst = (int32_t *)((char *)(C + (size_t)rowu * ldc + colu) + lane_b);
-        if (!MASK || (rowu + 4 * lh < mst && colu + l32 < nst)) __builtin_nontemporal_store(v[i][j][r], dst);
+        if constexpr (MASK) {
+            if (rowu + 4 * lh < mst && colu + l32 < nst) *dst = v[i][j][r];
+        } else {
+            __builtin_nontemporal_store(v[i][j][r], dst);
+        }
     };
     auto store_prev = [&](int e) __attribute__((always_inline)) { store_c(prv, pm0, pn0, e); };
 
