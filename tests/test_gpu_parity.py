@@ -711,9 +711,6 @@ def test_gemm_i8_h128_wraps_mod_2_32():
     assert got[0, 0] == np.int32(np.uint32((k * 16384) % (1 << 32)).astype(np.int32))
 
 
-# Operands off the 16-byte grid (K or N not a multiple of 16) or not 16-byte
-# aligned: repacked into padded panels in the workspace (arena, caller
-# workspace or scratch), or, without a workspace, the byte-load kernel.
 def _mt_gemm_i8(a, b, m, k, n):
     """Full int8 product from the multithreaded CPU restatement (equal to the
     scalar oracle at every band count, tests/test_oracle.py)."""
@@ -727,6 +724,10 @@ def _mt_gemm_i8(a, b, m, k, n):
 # workgroups), a K too short to carry them (512: stored at the next tile's
 # start) and three rounds (561 tiles)
 PERSIST_I8 = [(2048, 768, 4352), (1408, 768, 6144), (2048, 512, 4352), (4224, 768, 4352)]
+# off the 16-byte grid, repacked into padded panels, on grids of several
+# rounds: persistent 128 x 256 tiles with the masked epilogue (2304 x 4352
+# panels: 306 tiles) and the masked 256 x 256 kernel (4352^2: 289 tiles)
+PERSIST_I8 += [(2100, 1000, 4100), (4100, 300, 4100)]
 
 
 @pytest.mark.parametrize("m,k,n", PERSIST_I8, ids=[f"{m}x{k}x{n}" for m, k, n in PERSIST_I8])
@@ -739,6 +740,9 @@ def test_gemm_i8_persistent_rounds(m, k, n):
     np.testing.assert_array_equal(C[rows], O.gemm_i8_rows(a, b, m, k, n, rows))
 
 
+# Operands off the 16-byte grid (K or N not a multiple of 16) or not 16-byte
+# aligned: repacked into padded panels in the workspace (arena, caller
+# workspace or scratch), or, without a workspace, the byte-load kernel.
 RAGGED_I8 = [(1, 17, 1),(37, 100, 53), (300, 1000, 77), (256, 4095, 256), (1000, 1000, 1000), (257, 4100, 1003),
              (64, 64, 64), (256, 256, 256)]
 
