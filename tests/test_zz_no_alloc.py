@@ -1,8 +1,9 @@
 """det_matmul_scratch_dev (the entry point that allocates nothing) against
 det_matmul_ws_dev (the existing workspace entry point) through the C ABI:
 bit-identical outputs on two calls in a row, the second smaller, for the
-int16 and Q16 limb GEMMs (which use the scratch) and int8 (which does not);
-a shape beyond the fixed scratch is rejected before any launch."""
+int16 and Q16 limb GEMMs (which always use the scratch) and int8 (which uses
+it only to repack operands off the 16-byte grid); a limb-GEMM shape beyond
+the fixed scratch is rejected before any launch."""
 import ctypes
 
 import numpy as np
@@ -61,6 +62,18 @@ def test_scratch_entry_matches_workspace_entry_twice(op):
     # the second call is smaller: it reuses the scratch the first one filled
     _run_both(L, f, op, 320, 1088, 272, 0x5C1, s)
     _run_both(L, f, op, 70, 200, 52, 0x5C2, s)
+    s.destroy()
+
+
+def test_scratch_entry_int8_repack_twice():
+    # both shapes are off the 16-byte grid (K % 16 != 0): their padded panels
+    # come from the scratch, the second call's smaller ones over the first's
+    L, f = _bind()
+    s = M.Stream()
+    for shape in ((300, 1000, 77), (37, 100, 53)):
+        assert 0 < L.det_workspace_bytes(M.DET_OP_I8, *shape) <= 32 << 20
+    _run_both(L, f, M.DET_OP_I8, 300, 1000, 77, 0x5C5, s)
+    _run_both(L, f, M.DET_OP_I8, 37, 100, 53, 0x5C6, s)
     s.destroy()
 
 
