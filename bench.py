@@ -480,10 +480,10 @@ def cpu_baseline_q16(A: np.ndarray, B: np.ndarray, C_gpu: np.ndarray, m: int, k:
     run()
     if not np.array_equal(c.reshape(m, n), C_gpu):
         raise SystemExit("Q16 CPU baseline output differs from the GPU output")
-    t = _time_median(run, 5)
+    t = _time_median(run, 33)
     return {"value": 2.0 * m * n * k / t / 1e12, "unit": "Q16 TOP/s (2*MNK/t)", "gmac_per_s": m * n * k / t / 1e9,
             "cores": int(L.det_cpu_threads_for(m)), "kind": "port",
-            "sample": f"the whole {m}x{k}x{n} Q16 GEMM (median of 5, {t * 1e3:.1f} ms each); oracle/det_cpu_mt.c "
+            "sample": f"the whole {m}x{k}x{n} Q16 GEMM (median of 33, {t * 1e3:.1f} ms each); oracle/det_cpu_mt.c "
                       f"restatement of the reference MT Q16 path, output equal to the GPU output",
             "cpu_model": _cpu_model()}
 
@@ -499,40 +499,55 @@ def cpu_baseline_gemv(W: np.ndarray, x: np.ndarray, y_gpu: np.ndarray, m: int, k
     run()
     if not np.array_equal(y, y_gpu.ravel()):
         raise SystemExit("GEMV CPU baseline output differs from the GPU output")
-    t = _time_median(run, 7)
+    t = _time_median(run, 33)
     nbytes = 4.0 * m * k + 4.0 * k + 4.0 * m
     return {"value": nbytes / t / 1e9, "unit": "GB/s", "ms": t * 1e3, "cores": int(L.det_cpu_threads_for(m)),
             "kind": "port",
-            "sample": f"the whole {m}x{k} batch-1 Q16 GEMV (median of 7); oracle/det_cpu_mt.c restatement of "
+            "sample": f"the whole {m}x{k} batch-1 Q16 GEMV (median of 33); oracle/det_cpu_mt.c restatement of "
                       f"__mind_blas_gemv_q16_mt's row bands, output equal to the GPU output",
             "cpu_model": _cpu_model()}
 
 
-def cpu_config_i8_256() -> dict:
-    """BASELINE config 1 (the reference's CPU bench shape, int8 256^3 from the
-    bench LCG, seed 0xDEADBEEF00000000 ^ 256, benches/det_matmul_i8.rs), on ONE
-    thread of the MT restatement (the AVX2 vpmaddwd 4x16 microkernel), beside
-    the reference's published single-thread figure."""
+# The reference's published single-thread CPU figures for its own bench
+# shapes (docs/benchmarks/RESULTS-mind-vs-rust-2026-06-09.md:45-48, MIND
+# column; Intel i7-5930K 3.5 GHz AVX2, one core).
+PUBLISHED_ST = {("i8", 256): (12.56, 45), ("i8", 512): (14.17, 46), ("q16", 256): (4.17, 47), ("q16", 512): (4.16, 48)}
+
+
+def cpu_single_thread(op: str, n: int) -> dict:
+    """The reference's CPU bench shape n^3 (seed 0xDEADBEEF00000000 ^ n, the
+    bench LCG: benches/det_matmul_i8.rs:431-446, det_matmul_q16.rs:424-437) on
+    ONE thread of the MT restatement (the AVX2 vpmaddwd 4x16 int8 / vpmuldq
+    4x8 Q16 microkernels), beside the reference's published figure.  Int8
+    256^3 is BASELINE config 1."""
     import oracle as O
 
     L = O.lib()
-    n = 256
-    a, b = O.gen_i8(0xDEADBEEF00000000 ^ n, n * n, n * n)
+    seed = 0xDEADBEEF00000000 ^ n
+    if op == "i8":
+        a, b = O.gen_i8(seed, n * n, n * n)
+        fn, want = L.det_cpu_gemm_i8, O.gemm_i8(a, b, n, n, n).ravel()
+    else:
+        a, b = O.gen_q16(seed, n * n, n * n)
+        fn, want = L.det_cpu_gemm_q16, O.gemm_q16(a, b, n, n, n).ravel()
     c = np.empty(n * n, np.int32)
     L.det_cpu_set_threads(1)
     try:
-        run = lambda: L.det_cpu_gemm_i8(a.ctypes.data, b.ctypes.data, c.ctypes.data, n, n, n)
+        run = lambda: fn(a.ctypes.data, b.ctypes.data, c.ctypes.data, n, n, n)
         run()
-        exact = bool(np.array_equal(c, O.gemm_i8(a, b, n, n, n).ravel()))
-        t = _time_median(run, 101)
+        exact = bool(np.array_equal(c, want))
+        reps = 101 if n * n * n * (1 if op == "i8" else 8) <= (1 << 27) else 33
+        t = _time_median(run, reps)
     finally:
         L.det_cpu_set_threads(0)
     if not exact:
-        raise SystemExit("int8 256^3 CPU baseline output differs from the oracle")
+        raise SystemExit(f"{op} {n}^3 CPU baseline output differs from the oracle")
+    pub, line = PUBLISHED_ST[(op, n)]
     return {"value": n ** 3 / t / 1e9, "unit": "GMAC/s", "us": t * 1e6, "cores": 1, "kind": "port",
-            "sample": "int8 256^3 (median of 101 calls), one thread, output equal to the oracle",
-            "published_reference": {"value": 12.56, "unit": "GMAC/s", "host": "Intel i7-5930K 3.5 GHz AVX2, 1 core",
-                                    "source": "docs/benchmarks/RESULTS-mind-vs-rust-2026-06-09.md:45"},
+            "sample": f"{'int8' if op == 'i8' else 'Q16.16'} {n}^3 (median of {reps} calls), one thread, "
+                      f"output equal to the oracle",
+            "published_reference": {"value": pub, "unit": "GMAC/s", "host": "Intel i7-5930K 3.5 GHz AVX2, 1 core",
+                                    "source": f"docs/benchmarks/RESULTS-mind-vs-rust-2026-06-09.md:{line}"},
             "cpu_model": _cpu_model()}
 
 
@@ -757,8 +772,12 @@ def main() -> int:
         log("cpu_baseline: MT CPU restatement on a row band of the same workload")
         result["cpu_baseline"] = cpu_baseline_int8(head["A"], head["B"], head["C"], m, k, n)
         log(f"cpu_baseline: {result['cpu_baseline']['value']:.3f} TOP/s on {result['cpu_baseline']['cores']} threads")
-        extra = {"i8_256_one_thread": cpu_config_i8_256()}
-        log(f"cpu_baseline i8 256^3, 1 thread: {extra['i8_256_one_thread']['value']:.2f} GMAC/s")
+        extra = {}
+        for op, nn in PUBLISHED_ST:
+            key = f"{op}_{nn}_one_thread"
+            extra[key] = cpu_single_thread(op, nn)
+            log(f"cpu_baseline {op} {nn}^3, 1 thread: {extra[key]['value']:.2f} GMAC/s "
+                f"(reference published {extra[key]['published_reference']['value']})")
         if "q16_1024" in runs and "A" in runs["q16_1024"]:
             r = runs["q16_1024"]
             extra["q16_1024"] = cpu_baseline_q16(r["A"], r["B"], r["C"], 1024, 1024, 1024)
