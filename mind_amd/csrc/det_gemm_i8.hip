@@ -617,19 +617,20 @@ __global__ __launch_bounds__(THREADS, 1) void gemm_i8_dma_kernel(const int8_t *_
         else epilogue(std::true_type{});
     }
 }
-// ------------------------------------------------------- 128 x 256 tiles
-// The same ping-pong schedule on a 128 x 256 C tile, for grids whose
-// 256 x 256 tiles would fill at most one round of the chip.  Small grids
-// (2048^3: 64 tiles of 256^2) use twice as many CUs, and at 4096^3 each CU
-// owns two tiles.  The price is a smaller wave tile (64 x 64: 2 x 2 blocks of
-// 32x32x32), a third more LDS bytes per MFMA, so grids of several rounds
-// stay on the 256 x 256 kernel.
+// ------------------------------------------------------- 128-row tiles
+// The same ping-pong schedule on a 128 x TN C tile (TN = 256 or 128), for
+// grids whose 256 x 256 tiles would fill at most one round of the chip.
+// Small grids (2048^3: 64 tiles of 256^2) use up to four times as many CUs,
+// and at 4096^3 each CU owns two 128 x 256 tiles.  The price is a smaller
+// wave tile (64 x 64 or 64 x 32), more LDS bytes per MFMA, so grids of
+// several rounds stay on the 256 x 256 kernel.
 // A stage holds K = 128 as two 64-wide sub-stages, each laid out like a
-// stage of the 256 x 256 kernel (A [128][64] with swz_a, B [64][256] with
-// swz_b), so every barrier slot again carries 16 MFMAs per wave; 3 stages
-// (144 KiB) with the DMA two steps ahead.  Full shapes only: M % 128 == 0,
-// N % 256 == 0, K % 128 == 0, K > 0, operands below 2^31 bytes, aligned.
-// C: row stride ldc, rows below mst and columns below nst stored.
+// stage of the 256 x 256 kernel (A [128][64] with swz_a, B [64][TN]), so a
+// barrier slot carries 16 (TN = 256) or 8 (TN = 128) MFMAs per wave; 3
+// stages (144 or 96 KiB) with the DMA two steps ahead.  Full shapes only:
+// M % 128 == 0, N % TN == 0, K % 128 == 0, K > 0, operands below 2^31
+// bytes, aligned.  C: row stride ldc, rows below mst and columns below nst
+// stored.
 //
 // Persistent: a workgroup walks tiles blockIdx.x, blockIdx.x + gridDim.x, ...
 // (gridDim.x a multiple of 8, so every tile of a workgroup stays on its XCD).
