@@ -740,6 +740,96 @@ def test_gemm_i8_persistent_rounds(m, k, n):
     np.testing.assert_array_equal(C[rows], O.gemm_i8_rows(a, b, m, k, n, rows))
 
 
+def _sweep_shapes(count, seed):
+    """Seeded int8 shapes across the router's cases: multiples of 128 / 256
+    (128 x 128, 128 x 256 one- and multi-round, 256 x 256), the 16-byte grid
+    off those multiples (edge tiles) and ragged shapes (repack)."""
+    rng = np.random.default_rng(seed)
+    out = []
+    for i in range(count):
+        kind = i % 4
+        if kind == 0:     # 128-multiples, up to 34 x 34 tiles of 128
+            m, n, k = (int(rng.integers(1, 35)) * 128 for _ in range(3))
+        elif kind == 1:   # 256-multiples
+            m, n, k = (int(rng.integers(1, 19)) * 256 for _ in range(3))
+        elif kind == 2:   # on the 16-byte grid
+            m = int(rng.integers(1, 3000)); n = int(rng.integers(1, 180)) * 16; k = int(rng.integers(1, 120)) * 16
+        else:             # ragged
+            m, n, k = (int(rng.integers(1, 3000)) for _ in range(3))
+        if m * n * k > 1 << 31:   # keep the CPU check short: shrink K on its grid
+            g = (128, 256, 16, 1)[kind]
+            k = max(g, (1 << 31) // (m * n) // g * g)
+        out.append((m, k, n))
+    return out
+
+
+SWEEP_I8 = _sweep_shapes(48, 0x5EE9)
+
+
+@pytest.mark.parametrize("m,k,n", SWEEP_I8, ids=[f"{m}x{k}x{n}" for m, k, n in SWEEP_I8])
+def test_gemm_i8_routing_sweep(m, k, n):
+    """Every kernel the router can pick, full output against the CPU
+    restatement, through the device entry point (library arena) and through
+    det_matmul_ws_dev with exactly the reported workspace."""
+    a, b = O.gen_i8(0x5EE9 ^ (m * 1000003 + k * 1009 + n), m * k, k * n)
+    want = _mt_gemm_i8(a, b, m, k, n)
+    note(f"det_matmul_i8_dev sweep {m}x{k}x{n}")
+    C = _dev_run(lambda pa, pb, pc, s: M.lib().det_matmul_i8_dev(pa, pb, pc, m, k, n, s), [a, b], (m, n), reps=1)
+    np.testing.assert_array_equal(C, want)
+    L = M.lib()
+    wsb = L.det_workspace_bytes(M.DET_OP_I8, m, k, n)
+    ws = M.DeviceBuffer(max(wsb, 256))
+    C2 = _dev_run(lambda pa, pb, pc, s: L.det_matmul_ws_dev(M.DET_OP_I8, pa, pb, pc, m, k, n, ws.ptr, wsb, s),
+                  [a, b], (m, n), reps=1)
+    ws.free()
+    np.testing.assert_array_equal(C2, want)
+
+
+def _mt_gemm(op, a, b, m, k, n):
+    """Full Q16 / int16 product from the multithreaded CPU restatement (equal
+    to the scalar oracle at every band count, tests/test_oracle.py)."""
+    c = np.empty(m * n, np.int32)
+    fn = O.lib().det_cpu_gemm_q16 if op == M.DET_OP_Q16 else O.lib().det_cpu_gemm_i16
+    assert fn(a.ctypes.data, b.ctypes.data, c.ctypes.data, m, k, n) == 0
+    return c.reshape(m, n)
+
+
+def _limb_sweep(count, seed):
+    rng = np.random.default_rng(seed)
+    out = []
+    for i in range(count):
+        if i % 2 == 0:   # tile multiples (64 for Q16, 128 rows for int16's interleave)
+            m, n, k = (int(rng.integers(1, 17)) * 64 for _ in range(3))
+        else:
+            m, n, k = (int(rng.integers(1, 1100)) for _ in range(3))
+        out.append((m, k, n))
+    return out
+
+
+SWEEP_LIMB = [(op, *shape) for op in (M.DET_OP_Q16, M.DET_OP_I16) for shape in _limb_sweep(12, 0x11B + op)]
+
+
+@pytest.mark.parametrize("op,m,k,n", SWEEP_LIMB, ids=[f"op{op}-{m}x{k}x{n}" for op, m, k, n in SWEEP_LIMB])
+def test_gemm_limb_sweep(op, m, k, n):
+    """Seeded Q16 (saturating generator) and int16 shapes, full output against
+    the CPU restatement, through det_matmul_ws_dev with exactly the reported
+    workspace refilled with garbage first."""
+    if op == M.DET_OP_Q16:
+        a, b = O.gen_q16_sat(0x11B ^ (m * 7919 + k * 31 + n), m * k, k * n, 13)
+    else:
+        a, b = O.gen_i16(0x11B ^ (m * 7919 + k * 31 + n), m * k, k * n)
+    want = _mt_gemm(op, a, b, m, k, n)
+    L = M.lib()
+    wsb = L.det_workspace_bytes(op, m, k, n)
+    ws = M.DeviceBuffer(max(wsb, 256))
+    ws.fill(0xC3)
+    note(f"det_matmul_ws_dev op={op} sweep {m}x{k}x{n}")
+    C = _dev_run(lambda pa, pb, pc, s: L.det_matmul_ws_dev(op, pa, pb, pc, m, k, n, ws.ptr, wsb, s), [a, b],
+                 (m, n), reps=1)
+    ws.free()
+    np.testing.assert_array_equal(C, want)
+
+
 # Operands off the 16-byte grid (K or N not a multiple of 16) or not 16-byte
 # aligned: repacked into padded panels in the workspace (arena, caller
 # workspace or scratch), or, without a workspace, the byte-load kernel.
