@@ -21,11 +21,10 @@
 //   * n <= 16        : one FFT per thread (fft_small_kernel);
 //   * 32 <= n <= 2048: n / 16 lanes per FFT, passes separated by an LDS
 //                      transpose, bit reversal folded into the first load,
-//                      one HBM read and one write per point; in int32 when a
-//                      bound on the inputs proves that every intermediate
-//                      fits (same integers, cheaper products:
-//                      fft_lds_kernel), the other groups in int64
-//                      (fft_lds_general_kernel);
+//                      one HBM read and one write per point (fft_lds_kernel);
+//                      a block of transforms runs in int32 when a bound on
+//                      its inputs proves that every intermediate fits (same
+//                      integers, cheaper products), else in int64;
 //   * n >= 4096      : one global-memory pass per 4-bit window, out of place
 //                      through a workspace (fft_pass_kernel).
 #include "det_common.h"
@@ -281,15 +280,14 @@ __device__ __forceinline__ void store_group(int64_t *__restrict__ dre, int64_t *
     }
 }
 
-// int32 kernel: every group whose inputs are within i32_input_bound (and a
-// table within [-2^16, 2^16]) is transformed here; the others are left to
-// fft_lds_general_kernel.  deferred[g] is written for every group g (1 =
-// left over), so the flags need no clearing between calls.
+// A block of transforms whose inputs are all within i32_input_bound (and a
+// table within [-2^16, 2^16]) runs in int32; any other block runs the int64
+// transform on the values it has already loaded (the choice is block-uniform,
+// so every thread takes the same path through the LDS transposes).
 template <int LOGN>
 __global__ __launch_bounds__(256) void fft_lds_kernel(const int64_t *__restrict__ sre, const int64_t *__restrict__ sim,
                                                       int64_t *__restrict__ dre, int64_t *__restrict__ dim,
-                                                      const int64_t *__restrict__ tw, int64_t batch,
-                                                      uint32_t *__restrict__ deferred) {
+                                                      const int64_t *__restrict__ tw, int64_t batch) {
     constexpr int N = 1 << LOGN, L = N / 16, FPB = 256 / L, NP = (LOGN + 3) / 4;
     constexpr int STRIDE = N + N / 16;
     constexpr int S1 = 4 < LOGN - 4 ? 4 : LOGN - 4, S2 = 8 < LOGN - 4 ? 8 : LOGN - 4;
@@ -316,9 +314,11 @@ __global__ __launch_bounds__(256) void fft_lds_kernel(const int64_t *__restrict_
         const bool live = fi < batch;
         int64_t xr[16], xi[16];
         const bool fits = load_group<LOGN>(sre, sim, fi, live, t, xr, xi);
-        const bool fast = __syncthreads_and(fits && tw_small);
-        if (threadIdx.x == 0) deferred[f0 / FPB] = fast ? 0u : 1u;
-        if (!fast) continue;
+        if (!__syncthreads_and(fits && tw_small)) {
+            lds_transform<LOGN>(xr, xi, tw, t, (int64_t *)smf);
+            if (live) store_group<LOGN>(dre, dim, fi, t, xr, xi);
+            continue;
+        }
         int32_t yr[16], yi[16];
 #pragma unroll
         for (int r = 0; r < 16; ++r) yr[r] = (int32_t)xr[r], yi[r] = (int32_t)xi[r];
@@ -332,31 +332,6 @@ __global__ __launch_bounds__(256) void fft_lds_kernel(const int64_t *__restrict_
             window32<S2, 8, LOGN>(yr, yi, w2);
         }
         if (live) store_group<LOGN>(dre, dim, fi, t, yr, yi);
-    }
-}
-
-// int64 kernel for the groups flagged in `deferred` (any inputs, any table;
-// twiddles read from the table as they are needed).
-template <int LOGN>
-__global__ __launch_bounds__(256) void fft_lds_general_kernel(const int64_t *__restrict__ sre,
-                                                              const int64_t *__restrict__ sim,
-                                                              int64_t *__restrict__ dre, int64_t *__restrict__ dim,
-                                                              const int64_t *__restrict__ tw, int64_t batch,
-                                                              const uint32_t *__restrict__ deferred) {
-    constexpr int N = 1 << LOGN, L = N / 16, FPB = 256 / L;
-    constexpr int STRIDE = N + N / 16;
-    __shared__ int64_t sm[FPB * STRIDE];
-    const int f = threadIdx.x / L;
-    const uint32_t t = threadIdx.x % L;
-    const int64_t groups = (batch + FPB - 1) / FPB;
-    for (int64_t g = blockIdx.x; g < groups; g += gridDim.x) {
-        if (!deferred[g]) continue;   // block-uniform
-        const int64_t fi = g * FPB + f;
-        const bool live = fi < batch;
-        int64_t xr[16], xi[16];
-        load_group<LOGN>(sre, sim, fi, live, t, xr, xi);
-        lds_transform<LOGN>(xr, xi, tw, t, sm + f * STRIDE);
-        if (live) store_group<LOGN>(dre, dim, fi, t, xr, xi);
     }
 }
 
@@ -396,11 +371,7 @@ __global__ void copy_i64_kernel(const int64_t *__restrict__ src, int64_t *__rest
 }  // namespace fft
 
 size_t fft_workspace_bytes(int logn, int64_t batch) {
-    if (logn <= 4) return 0;
-    if (logn <= 11) {   // one deferred flag per group of transforms
-        const int64_t fpb = 256 / ((1 << logn) / 16);
-        return (size_t)((batch + fpb - 1) / fpb) * sizeof(uint32_t);
-    }
+    if (logn <= 11) return 0;
     return 2 * (size_t)batch * ((size_t)1 << logn) * sizeof(int64_t);
 }
 
@@ -424,13 +395,9 @@ hipError_t launch_fft_q16(const int64_t *sre, const int64_t *sim, int64_t *dre, 
 #undef SMALL
 #define LDS(LG)                                                                                                \
     case LG: {                                                                                                 \
-        if (!ws) return hipErrorInvalidValue;                                                                  \
-        uint32_t *deferred = (uint32_t *)ws;                                                                   \
         const int64_t fpb = 256 / ((1 << LG) / 16), blocks = (batch + fpb - 1) / fpb;                        \
         const unsigned grid = (unsigned)(blocks < cap ? blocks : cap);                                         \
-        hipLaunchKernelGGL(fft_lds_kernel<LG>, dim3(grid), dim3(256), 0, s, sre, sim, dre, dim, tw, batch, deferred); \
-        hipLaunchKernelGGL(fft_lds_general_kernel<LG>, dim3(grid < 1024 ? grid : 1024), dim3(256), 0, s, sre, sim, \
-                           dre, dim, tw, batch, deferred);                                                     \
+        hipLaunchKernelGGL(fft_lds_kernel<LG>, dim3(grid), dim3(256), 0, s, sre, sim, dre, dim, tw, batch);   \
         break;                                                                                                 \
     }
     LDS(5) LDS(6) LDS(7) LDS(8) LDS(9) LDS(10) LDS(11)

@@ -474,8 +474,7 @@ def test_fft_dev_entry_point_and_workspace_path():
             gi = dim_.to_array(np.int64, (batch, n))
             assert np.array_equal(gr[sel], want[0]) and np.array_equal(gi[sel], want[1])
             want = _fft_oracle_batch(want[0], want[1], tw, logn)
-        fpb = 256 // (n // 16) if logn <= 11 else 1
-        want_ws = 4 * -(-batch // fpb) if logn <= 11 else 16 * batch * n
+        want_ws = 0 if logn <= 11 else 16 * batch * n
         assert M.lib().det_fft_workspace_bytes(logn, batch) == want_ws
         dre.free(); dim_.free(); dtw.free()
 
