@@ -530,8 +530,9 @@ __global__ __launch_bounds__(THREADS, 1) void gemm_i8_dma_kernel(const int8_t *_
             __builtin_amdgcn_s_barrier();
         }
     }
-    // the loads issued past the end of K are zero fills; none may still be
-    // writing LDS when the workgroup ends
+    // the loads issued past the end of K (re-loads of the last step on the
+    // full-tile path, zero fills on the edge path) are never read; none may
+    // still be writing LDS when the workgroup ends
     DET_WAIT_VMCNT(0);
     }
 
