@@ -7,27 +7,31 @@
 //
 // Why: the one-vector kernel (det_gemv.hip) spends ~8 VALU slots per term on
 // the 64-bit product; with 8 vectors that is ~4x the VALU budget HBM speed
-// allows.  Here, per W element, the VALU only splits W into limbs (3 ops) and
+// allows.  Here, per W element, the VALU only splits W into limbs and
 // computes the residue for each vector (1 op per term):
-//   * S = sum_k W x exactly (mod 2^48) from int8 limb-pair MFMAs with the
-//     bias identity (see det_gemm_limb.hip): W and x are written as signed
-//     int8 limbs t_p (low bytes biased by -128 = u ^ 0x80), c = 0x808080,
-//     sum W x = sum T(W)T(x) + c sum W + c sum x - K c^2, and
-//     sum T(W)T(x) = sum_{p+q<=5} 2^{8(p+q)} sum_k t_p(W) t_q(x).
-//     v_mfma_i32_16x16x64_i8 with 16 W rows as A and the query vectors as the
-//     16 B columns (nb used, column 8 = a ones vector in limb 0, which yields
-//     sum_k t_p(W) -- the row sums -- for free).
+//   * S = sum_k W x exactly (mod 2^48) from int8 limb-pair MFMAs.  W is
+//     written as signed int8 limbs t_p (low bytes biased by -128 = u ^ 0x80,
+//     c = 0x808080): W = sum_p 2^(8p) t_p + c.  The query vectors (small,
+//     prepared once) are written in five balanced base-256 digits
+//     d_q in [-128, 127]: x = sum_q 2^(8q) d_q.  Then
+//         sum_k W x = sum_{p,q} 2^(8(p+q)) sum_k t_p d_q + c sum_k x,
+//     and only pairs with p + q <= 5 matter mod 2^48.  The sum of x is exact
+//     and cheap (prep); no row sums of W are needed.
+//     v_mfma_i32_16x16x64_i8 takes 16 W rows as A and two digits of the 8
+//     query vectors as the 16 B columns (columns 0-7: digit 2Q, 8-15: digit
+//     2Q + 1), so 10 MFMAs per 64-wide K step cover every needed pair.
 //   * R = sum_k ((W x) mod 2^16) = sum_k ((lo16 W * lo16 x) mod 2^16) with
 //     v_pk_mul_lo_u16 + v_dot2_u32_u16 (two terms per pair of ops).
 //   * y = (int32)(((S - R) mod 2^48) >> 16).
-// Exactness bounds: K <= 32768 keeps the exact shift-0 / shift-1 MFMA sets
-// below 2^31 (|t_p t_q| <= 2^14) and R below 2^32; sets with shift >= 2 only
-// need their value mod 2^32 (i32 wrap-around).
+// Exactness bounds: K <= 32768 keeps the shift-0 and shift-1 partial sums
+// (|t_p d_q| <= 2^14) below 2^31 and R below 2^32; shifts >= 2 only need
+// their value mod 2^32 (i32 wrap-around).
 //
 // Layout: a prep kernel rewrites the (small) query vectors into MFMA B
 // operands (xp) and packed low halves (xl) in exactly the per-lane K order
-// the main kernel uses; W is streamed once, straight from HBM into registers
-// (buffer loads four K steps ahead), and split into limb planes with v_perm.
+// the main kernel uses, chunk by chunk as the main kernel stages them; W is
+// streamed once, straight from HBM into registers (buffer loads four K
+// steps ahead), and split into limb planes with v_perm.
 // Lane l of a wave handles W row (l & 15) and, within each 64-wide K step,
 // the K indices {16 j + 4 (l >> 4) + e : j, e < 4}; any consistent K order
 // of the A and B operands gives the exact dot product.
@@ -38,44 +42,66 @@ namespace det {
 namespace gemv8 {
 
 constexpr int THREADS = 256, DEPTH = 4;
-constexpr uint32_t BIAS = 0x00808080u;
+constexpr uint32_t BIAS4 = 0x80808080u;
+constexpr int NQ = 3;                                   // B operands per K step: digit pairs (0,1), (2,3), (4,-)
+constexpr int CH = 4;                                   // K steps per LDS chunk (per half)
+constexpr int XP_CH = CH * NQ * 64, XL_CH = CH * 64;    // uint4 per chunk
+constexpr int X_CH = XP_CH + XL_CH;                     // 1024 uint4 = 16 KiB per chunk
+
+// Balanced base-256 digit q (in [-128, 127]) of x: x = sum_{q<5} 2^(8q) d_q.
+__device__ __forceinline__ int digit(int32_t x, int q) {
+    long long v = x;
+    int d = 0;
+#pragma unroll
+    for (int i = 0; i <= q; ++i) {
+        d = (int)((v + 128) & 255) - 128;
+        v = (v - d) >> 8;
+    }
+    return d;
+}
 
 // One 256-thread block per 64-wide K step s: the step's slice of the query
-// vectors is staged in LDS (coalesced loads), then turned into the limb
-// planes xp, the low halves xl and the exact per-step column sums part[s][b]
+// vectors is staged in LDS (coalesced loads), then turned into the digit
+// planes, the low halves and the exact per-step column sums part[s][b]
 // (summed by the main kernel: no atomics, nothing to zero beforehand).
+// Output layout, chunk by chunk (chunk c = steps CH c .. CH c + CH - 1, X_CH
+// uint4): xp entries (d8, Q, lane) at (d8 NQ + Q) 64 + lane, then xl entries
+// at XP_CH + d8 64 + ((j 4 + bp) 4 + g).
 __global__ __launch_bounds__(256) void prep_kernel(const int32_t *__restrict__ X, int nb, int K,
-                                                   uint4 *__restrict__ xp, uint4 *__restrict__ xl,
-                                                   long long *__restrict__ part) {
-    __shared__ uint32_t xs[8][65];
+                                                   uint4 *__restrict__ xw, long long *__restrict__ part) {
+    __shared__ int32_t xs[8][65];
     const int s = blockIdx.x, t = threadIdx.x;
+    uint4 *xc = xw + (size_t)(s / CH) * X_CH;
+    const int d8 = s % CH;
 #pragma unroll
     for (int e = t; e < 512; e += 256) {
         const int b = e >> 6, k = e & 63;
-        xs[b][k] = b < nb ? (uint32_t)X[(size_t)b * K + 64 * s + k] : 0u;
+        xs[b][k] = b < nb ? X[(size_t)b * K + 64 * s + k] : 0;
     }
     __syncthreads();
-    {   // xp[s][plane q][lane l]: 16 limb bytes of column b = l & 15, group g = l >> 4
-        const int q = t >> 6, l = t & 63, b = l & 15, g = l >> 4;
+    if (t < NQ * 64) {
+        // B operand Q, lane l: column b = l & 15 (vector b & 7, digit
+        // 2Q + (b >> 3)), group g = l >> 4: 16 digit bytes at K 16 j + 4 g + e
+        const int Q = t >> 6, l = t & 63, b = l & 15, g = l >> 4;
+        const int v = b & 7, q = 2 * Q + (b >> 3);
         uint32_t w[4];
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
-            uint32_t v = 0;
+            uint32_t word = 0;
 #pragma unroll
             for (int e = 0; e < 4; ++e) {
                 const int k = 16 * j + 4 * g + e;
-                uint32_t byte;
-                if (b < nb) byte = ((xs[b][k] ^ BIAS) >> (8 * q)) & 0xffu;
-                else byte = (b == 8 && q == 0) ? 1u : 0u;
-                v |= byte << (8 * e);
+                const uint32_t byte = (v < nb && q < 5) ? (uint32_t)(digit(xs[v][k], q) & 0xff) : 0u;
+                word |= byte << (8 * e);
             }
-            w[j] = v;
+            w[j] = word;
         }
-        xp[((size_t)s * 4 + q) * 64 + l] = make_uint4(w[0], w[1], w[2], w[3]);
-    }
-    if (t < 64) {   // xl[s][j][bp][g]: low halves of vectors 2bp, 2bp+1 at K 16j+4g+{0,1},{2,3}
-                    // (g fastest: the four K groups read adjacent 16-byte slots, no bank conflict)
-        const int g = t >> 4, j = (t >> 2) & 3, bp = t & 3;
+        xc[(d8 * NQ + Q) * 64 + l] = make_uint4(w[0], w[1], w[2], w[3]);
+    } else {
+        // low halves of vectors 2bp, 2bp+1 at K 16j+4g+{0,1},{2,3}
+        // (g fastest: the four K groups read adjacent 16-byte slots, no bank
+        // conflict); then the exact column sums of this step
+        const int u = t - NQ * 64, g = u >> 4, j = (u >> 2) & 3, bp = u & 3;
         uint32_t d[4];
 #pragma unroll
         for (int h = 0; h < 2; ++h) {
@@ -83,15 +109,16 @@ __global__ __launch_bounds__(256) void prep_kernel(const int32_t *__restrict__ X
 #pragma unroll
             for (int pr = 0; pr < 2; ++pr) {
                 const int k0 = 16 * j + 4 * g + 2 * pr;
-                d[2 * h + pr] = (xs[b][k0] & 0xffffu) | (xs[b][k0 + 1] << 16);
+                d[2 * h + pr] = ((uint32_t)xs[b][k0] & 0xffffu) | ((uint32_t)xs[b][k0 + 1] << 16);
             }
         }
-        xl[(((size_t)s * 4 + j) * 4 + bp) * 4 + g] = make_uint4(d[0], d[1], d[2], d[3]);
-    } else if (t >= 64 && t < 72) {   // exact column sums of this step
-        long long sum = 0;
+        xc[XP_CH + d8 * 64 + (j * 4 + bp) * 4 + g] = make_uint4(d[0], d[1], d[2], d[3]);
+        if (u < 8) {
+            long long sum = 0;
 #pragma unroll 8
-        for (int k = 0; k < 64; ++k) sum += (int32_t)xs[t - 64][k];
-        part[(size_t)s * 8 + (t - 64)] = sum;
+            for (int k = 0; k < 64; ++k) sum += xs[u][k];
+            part[(size_t)s * 8 + u] = sum;
+        }
     }
 }
 
@@ -104,33 +131,29 @@ __device__ __forceinline__ uint32_t residue2(uint32_t w2, uint32_t x2, uint32_t 
 // One block = 8 waves (2 per SIMD, so one wave's LDS / MFMA latency hides
 // behind the other's VALU work) on 64 W rows: wave w takes rows
 // 16 (w & 3) .. +16 and K half (w >> 2).  The query operands of a chunk of CH
-// K steps of both halves (xp: 4 KiB per step, xl: 1 KiB per step) are staged
+// K steps of both halves (xp: 3 KiB per step, xl: 1 KiB per step) are staged
 // in LDS, double buffered, by all threads through registers: LDS reads wait
 // on lgkmcnt, so the only vector-memory loads a step waits for are its own W
 // rows, kept DEPTH steps ahead in a register ring (vmcnt retires in order,
 // so mixing other loads into that stream would drain the ring).  The staging
 // loads of chunk c+1 are issued at the start of chunk c and written to LDS
 // at its end.  The two K halves are combined exactly at the end (int64 for
-// the exact shift-0/1 sets).
+// the shift-0/1 sums).
 // Requires K % 512 == 0, K <= 32768, W < 2^31 bytes, nb <= 8.
-constexpr int CH = 4;                                   // K steps per LDS chunk (per half)
-constexpr int XP_CH = CH * 4 * 64, XL_CH = CH * 64;     // uint4 per chunk per half
-constexpr int X_HALF = XP_CH + XL_CH;                   // 1280 uint4 = 20 KiB
 constexpr int WAVES = 8, THREADS8 = WAVES * 64;
-constexpr int STAGE_PER_THREAD = 2 * X_HALF / THREADS8; // 5
+constexpr int STAGE_PER_THREAD = 2 * X_CH / THREADS8;  // 4
 struct Tail {                                           // post-loop reduction (aliases the staging)
     int32_t acc[WAVES][6][16][17];
     uint32_t r[WAVES][16][8];
 };
-constexpr int SMEM_BYTES = sizeof(Tail) > 2 * 2 * X_HALF * 16 ? sizeof(Tail) : 2 * 2 * X_HALF * 16;
+constexpr int SMEM_BYTES = sizeof(Tail) > 2 * 2 * X_CH * 16 ? sizeof(Tail) : 2 * 2 * X_CH * 16;
 
 __global__ __launch_bounds__(THREADS8, 1) void gemv8_kernel(const int32_t *__restrict__ W,
-                                                            const uint4 *__restrict__ xp,
-                                                            const uint4 *__restrict__ xl,
+                                                            const uint4 *__restrict__ xw,
                                                             const long long *__restrict__ part,
                                                             int32_t *__restrict__ Y, int M, int K, int nb) {
     __shared__ __attribute__((aligned(16))) char smem[SMEM_BYTES];
-    uint4 *s_x = (uint4 *)smem;                       // [2 buffers][2 halves][X_HALF]
+    uint4 *s_x = (uint4 *)smem;                       // [2 buffers][2 halves][X_CH]
     Tail &tail = *(Tail *)smem;
 
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
@@ -143,33 +166,30 @@ __global__ __launch_bounds__(THREADS8, 1) void gemv8_kernel(const int32_t *__res
     const int sbeg = kh * half;
     const uint32_t wbase = ((uint32_t)myrow * (uint32_t)K + 4u * g) * 4u;   // bytes
 
-    // staging of chunk c (both halves), one fixed source per slot: slots 0..1
-    // xp of half 0, slots 2..3 xp of half 1, slot 4 xl (half tid >> 8).
-    // Buffer loads with 32-bit offsets and no per-thread source select keep
-    // the address registers apart from the data, so the loads stay in flight
-    // (the wait is at the LDS store at the end of the chunk).
-    static_assert(STAGE_PER_THREAD == 5 && XP_CH == 2 * THREADS8 && XL_CH == THREADS8 / 2, "staging slots");
-    const __amdgpu_buffer_rsrc_t rxp = make_rsrc(xp, (uint32_t)K * 64u);
-    const __amdgpu_buffer_rsrc_t rxl = make_rsrc(xl, (uint32_t)K * 16u);
-    const int xl_h = tid >> 8, xl_f = tid & 255;
+    // staging of chunk c of both halves: 2 X_CH uint4, slot i of thread tid
+    // = entry f = i THREADS8 + tid, half f / X_CH (global chunk c, or
+    // half / CH + c), entry f % X_CH of that chunk.  One buffer resource over
+    // all chunks; buffer loads with 32-bit offsets keep the address registers
+    // apart from the data, so the loads stay in flight (the wait is at the
+    // LDS store at the end of the chunk).
+    static_assert(STAGE_PER_THREAD == 4 && X_CH == 2 * THREADS8, "staging slots");
+    const __amdgpu_buffer_rsrc_t rx = make_rsrc(xw, (uint32_t)(K / 64 / CH) * X_CH * 16u);
     uint4 stg[STAGE_PER_THREAD];
     auto stage_load = [&](int c) {
         const uint32_t c0 = (uint32_t)c, c1 = (uint32_t)(half / CH + c);
 #pragma unroll
         for (int i = 0; i < 2; ++i) {
-            stg[i] = buf_load16(rxp, ((c0 * XP_CH) + i * THREADS8 + tid) * 16u);
-            stg[2 + i] = buf_load16(rxp, ((c1 * XP_CH) + i * THREADS8 + tid) * 16u);
+            stg[i] = buf_load16(rx, ((c0 * X_CH) + i * THREADS8 + tid) * 16u);
+            stg[2 + i] = buf_load16(rx, ((c1 * X_CH) + i * THREADS8 + tid) * 16u);
         }
-        stg[4] = buf_load16(rxl, (((xl_h ? c1 : c0) * XL_CH) + xl_f) * 16u);
     };
     auto stage_store = [&](int buf) {
-        uint4 *d = s_x + buf * 2 * X_HALF;
+        uint4 *d = s_x + buf * 2 * X_CH;
 #pragma unroll
         for (int i = 0; i < 2; ++i) {
             d[i * THREADS8 + tid] = stg[i];
-            d[X_HALF + i * THREADS8 + tid] = stg[2 + i];
+            d[X_CH + i * THREADS8 + tid] = stg[2 + i];
         }
-        d[xl_h * X_HALF + XP_CH + xl_f] = stg[4];
     };
 
     v4i32 acc[6];
@@ -205,7 +225,7 @@ __global__ __launch_bounds__(THREADS8, 1) void gemv8_kernel(const int32_t *__res
         const int buf = c & 1;
         stage_load(c + 1 < nch ? c + 1 : c);   // branch-free; the last reload is unused
         __builtin_amdgcn_sched_barrier(0);      // keep its LDS stores at the end of the chunk
-        const uint4 *sxp = s_x + (buf * 2 + kh) * X_HALF;
+        const uint4 *sxp = s_x + (buf * 2 + kh) * X_CH;
         const uint4 *sxl = sxp + XP_CH;
 #pragma unroll
         for (int d8 = 0; d8 < CH; ++d8) {
@@ -214,12 +234,15 @@ __global__ __launch_bounds__(THREADS8, 1) void gemv8_kernel(const int32_t *__res
             const int st = sbeg + ls;
             // consume the ring slot (limb transpose, low halves) before
             // reloading it: the reload then reuses the same registers, so no
-            // register copy has to wait for a load still in flight
+            // register copy has to wait for a load still in flight.  The
+            // bias goes on after the transpose: planes 0-2 only
             uint32_t T[4][4], L[4][2];
 #pragma unroll
             for (int j = 0; j < 4; ++j) {
                 const uint4 w = wb[d][j];
-                transpose4x4(w.x ^ BIAS, w.y ^ BIAS, w.z ^ BIAS, w.w ^ BIAS, T[j][0], T[j][1], T[j][2], T[j][3]);
+                transpose4x4(w.x, w.y, w.z, w.w, T[j][0], T[j][1], T[j][2], T[j][3]);
+#pragma unroll
+                for (int pl = 0; pl < 3; ++pl) T[j][pl] ^= BIAS4;
                 L[j][0] = perm(w.y, w.x, 0x05040100u);   // lo16 of K e=0,1
                 L[j][1] = perm(w.w, w.z, 0x05040100u);   // lo16 of K e=2,3
             }
@@ -237,16 +260,18 @@ __global__ __launch_bounds__(THREADS8, 1) void gemv8_kernel(const int32_t *__res
             for (int j = 0; j < 2; ++j)
 #pragma unroll
                 for (int bp = 0; bp < 4; ++bp) XV[j][bp] = sxl[((d8 * 4 + j) * 4 + bp) * 4 + g];
-            v2i64 B[4];
+            v2i64 B[NQ];
 #pragma unroll
-            for (int q = 0; q < 4; ++q) B[q] = __builtin_bit_cast(v2i64, sxp[(d8 * 4 + q) * 64 + lane]);
-            // A operands: W limb planes (byte p of W ^ BIAS for 16 K)
+            for (int q = 0; q < NQ; ++q) B[q] = __builtin_bit_cast(v2i64, sxp[(d8 * NQ + q) * 64 + lane]);
+            // A operands: W limb planes t_p for 16 K; B operand Q holds digits
+            // 2Q (columns 0-7) and 2Q + 1 (8-15): accumulator set p + 2Q gets
+            // shift p + 2Q in columns 0-7 and p + 2Q + 1 in 8-15
 #pragma unroll
             for (int p = 0; p < 4; ++p) {
                 const v2i64 A = __builtin_bit_cast(v2i64, (v4i32){(int)T[0][p], (int)T[1][p], (int)T[2][p], (int)T[3][p]});
 #pragma unroll
-                for (int q = 0; q < 4; ++q)
-                    if (p + q <= 5) acc[p + q] = mfma16x16x64(A, B[q], acc[p + q]);
+                for (int q = 0; q < NQ; ++q)
+                    if (p + 2 * q <= 5) acc[p + 2 * q] = mfma16x16x64(A, B[q], acc[p + 2 * q]);
             }
             // residues for every query vector
             __builtin_amdgcn_sched_barrier(0);
@@ -296,27 +321,25 @@ __global__ __launch_bounds__(THREADS8, 1) void gemv8_kernel(const int32_t *__res
     const int rgo = tid >> 7, row = (tid >> 3) & 15, b = tid & 7;
     const int grow = blockIdx.x * 64 + rgo * 16 + row;
     if (b >= nb || grow >= M) return;
-    const unsigned long long cb = 0x808080ull;
-    const unsigned long long kc = (unsigned long long)(unsigned)K * cb;
-    long long tw = 0, s0x = 0, s1x = 0;
+    // shift 0: set 0 columns 0-7; shift s >= 1: set s - 1 columns 8-15 plus
+    // set s columns 0-7 (exact in int64 for s <= 1, mod 2^32 above)
+    long long s0 = 0, s1 = 0;
     uint32_t hi[4] = {0, 0, 0, 0}, rsum = 0;
 #pragma unroll
     for (int h = 0; h < 2; ++h) {
         const int wv = h * 4 + rgo;
+        s0 += tail.acc[wv][0][row][b];
+        s1 += (long long)tail.acc[wv][0][row][8 + b] + tail.acc[wv][1][row][b];
 #pragma unroll
-        for (int sft = 0; sft < 4; ++sft) tw += (long long)tail.acc[wv][sft][row][8] * (1ll << (8 * sft));
-        s0x += tail.acc[wv][0][row][b];
-        s1x += tail.acc[wv][1][row][b];
-#pragma unroll
-        for (int sft = 2; sft < 6; ++sft) hi[sft - 2] += (uint32_t)tail.acc[wv][sft][row][b];
+        for (int sft = 2; sft < 6; ++sft)
+            hi[sft - 2] += (uint32_t)tail.acc[wv][sft - 1][row][8 + b] + (uint32_t)tail.acc[wv][sft][row][b];
         rsum += tail.r[wv][row][b];
     }
-    const unsigned long long rowsum = (unsigned long long)tw + kc;   // sum_k W[row, k]
     long long colsum_b = 0;
 #pragma unroll
     for (int w = 0; w < WAVES; ++w) colsum_b += s_cs[w][b];
-    unsigned long long S = cb * (rowsum + (unsigned long long)colsum_b) - kc * cb;
-    S += (unsigned long long)s0x + ((unsigned long long)s1x << 8);
+    unsigned long long S = 0x808080ull * (unsigned long long)colsum_b;   // c sum_k x
+    S += (unsigned long long)s0 + ((unsigned long long)s1 << 8);
 #pragma unroll
     for (int sft = 2; sft < 6; ++sft) S += (unsigned long long)hi[sft - 2] << (8 * sft);
     S -= (unsigned long long)rsum;
@@ -325,7 +348,9 @@ __global__ __launch_bounds__(THREADS8, 1) void gemv8_kernel(const int32_t *__res
 
 }  // namespace gemv8
 
-size_t gemv8_workspace_bytes(int K) { return (size_t)K * 64 + (size_t)K * 16 + (size_t)K / 64 * 8 * 8; }
+size_t gemv8_workspace_bytes(int K) {
+    return (size_t)K / 64 / gemv8::CH * gemv8::X_CH * 16 + (size_t)K / 64 * 8 * 8;
+}
 
 bool gemv8_eligible(const int32_t *W, const int32_t *X, int M, int K) {
     return M >= 16 && K % 512 == 0 && K <= 32768 && (size_t)M * K * 4 < 0x80000000ull &&
@@ -336,11 +361,10 @@ bool gemv8_eligible(const int32_t *W, const int32_t *X, int M, int K) {
 hipError_t launch_gemv_q16_mfma(const int32_t *W, const int32_t *X, int32_t *Y, int M, int K, int nb, void *ws,
                                 hipStream_t s) {
     using namespace gemv8;
-    uint4 *xp = (uint4 *)ws;
-    uint4 *xl = xp + (size_t)K / 64 * 4 * 64;
-    long long *part = (long long *)(xl + (size_t)K / 64 * 64);
-    hipLaunchKernelGGL(prep_kernel, dim3(K / 64), dim3(256), 0, s, X, nb, K, xp, xl, part);
-    hipLaunchKernelGGL(gemv8_kernel, dim3((M + 63) / 64), dim3(THREADS8), 0, s, W, xp, xl, part, Y, M, K, nb);
+    uint4 *xw = (uint4 *)ws;
+    long long *part = (long long *)(xw + (size_t)K / 64 / CH * X_CH);
+    hipLaunchKernelGGL(prep_kernel, dim3(K / 64), dim3(THREADS), 0, s, X, nb, K, xw, part);
+    hipLaunchKernelGGL(gemv8_kernel, dim3((M + 63) / 64), dim3(THREADS8), 0, s, W, xw, part, Y, M, K, nb);
     return hipGetLastError();
 }
 
