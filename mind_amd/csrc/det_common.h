@@ -107,14 +107,17 @@ __device__ __forceinline__ v4i32 rsrc_words(const void *base, uint32_t bytes) {
     return (v4i32){(int)(uint32_t)a, (int)(uint32_t)(a >> 32) & 0xffff, (int)bytes, 0x00020000};
 }
 // One buffer_load_dwordx4 ... lds: lane i's 16 bytes at `voff` land at LDS
-// byte lds + 16 i (an offset past num_records lands zeros).  Written as
+// byte lds + 16 i (an offset past num_records lands zeros).  The LDS DMA
+// reads M0 one wait state after the SALU write at the earliest (the
+// compiler keeps the same distance for its own LDS DMA), hence the s_nop;
+// the compiler's hazard pass does not look inside inline assembly.  Written as
 // inline assembly so the compiler's wait-count pass does not treat every
 // later LDS read as dependent on it (it would drain all loads in flight); a
 // kernel using it orders these loads itself with explicit s_waitcnt vmcnt
 // and s_barrier, and issues no other vector-memory loads while they are
 // outstanding.
 __device__ __forceinline__ void dma16(v4i32 rsrc, uint32_t lds, int voff) {
-    asm volatile("s_mov_b32 m0, %0\n\tbuffer_load_dwordx4 %1, %2, 0 offen lds" ::"s"(lds), "v"(voff), "s"(rsrc)
+    asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tbuffer_load_dwordx4 %1, %2, 0 offen lds" ::"s"(lds), "v"(voff), "s"(rsrc)
                  : "memory", "m0");
 }
 // The same with a uniform byte offset added from an SGPR (soffset), so a
@@ -123,7 +126,7 @@ __device__ __forceinline__ void dma16(v4i32 rsrc, uint32_t lds, int voff) {
 // itself stay inside the buffer (an out-of-range soffset is a real access,
 // not a zero fill).
 __device__ __forceinline__ void dma16s(v4i32 rsrc, uint32_t lds, int voff, uint32_t soff) {
-    asm volatile("s_mov_b32 m0, %0\n\tbuffer_load_dwordx4 %1, %2, %3 offen lds" ::"s"(lds), "v"(voff), "s"(rsrc),
+    asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tbuffer_load_dwordx4 %1, %2, %3 offen lds" ::"s"(lds), "v"(voff), "s"(rsrc),
                  "s"(soff)
                  : "memory", "m0");
 }
