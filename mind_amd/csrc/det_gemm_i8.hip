@@ -979,15 +979,17 @@ static int cu_count() {
 // up to 256) in the workspace, and the full-tile kernels run on those with
 // C's own row stride and row / column bounds.  The padding is zero on both sides of
 // every product, so C is unchanged.  One launch for both operands
-// (blockIdx.z); each thread writes 16 bytes of a panel row.  Where the 20
+// (blockIdx.z), or for B alone when A already suits the full-tile kernels
+// (16-byte aligned, M % 128 == 0, K % 256 == 0: B' is [K][Np] and A is used
+// in place); each thread writes 16 bytes of a panel row.  Where the 20
 // dword-aligned bytes covering its 16 source bytes lie inside the source
 // buffer it reads those (one 16-byte and one 4-byte load) and funnel-shifts
 // them (v_alignbyte); at the two ends of the buffer it reads single bytes,
 // so no load leaves the source buffer.
 __global__ __launch_bounds__(256) void pad_i8_kernel(const int8_t *__restrict__ A, const int8_t *__restrict__ B,
                                                      int M, int N, int K, int Mp, int Kp, int Np,
-                                                     uint4 *__restrict__ Ap, uint4 *__restrict__ Bp) {
-    const bool is_b = blockIdx.z != 0;
+                                                     uint4 *__restrict__ Ap, uint4 *__restrict__ Bp, int zb) {
+    const bool is_b = (int)blockIdx.z == zb;   // zb = 1: A at z = 0, B at z = 1; zb = 0: B only
     const int8_t *src = is_b ? B : A;
     uint4 *dst = is_b ? Bp : Ap;
     const int rows = is_b ? K : M, rows_out = is_b ? Kp : Mp, cols = is_b ? N : K, dcols = is_b ? Np : Kp;
@@ -1088,12 +1090,22 @@ hipError_t launch_gemm_i8(const int8_t *A, const int8_t *B, int32_t *C, int M, i
         launch_i8_on_grid(A, B, C, M, N, K, N, M, N, s);
     } else if (pad && ws) {
         const int Mp = (int)round256(M), Kp = (int)round256(K), Np = (int)round256(N);
+        if (((uintptr_t)A & 15) == 0 && M % 128 == 0 && K % 256 == 0) {
+            // A already suits the full-tile kernels (a ragged or misaligned B,
+            // e.g. N = 1000): repack only B into [K][Np] panels
+            int8_t *Bp = (int8_t *)ws;
+            const dim3 pgrid((unsigned)((Np / 16 + 255) / 256), (unsigned)(K < 65535 ? K : 65535), 1);
+            hipLaunchKernelGGL(pad_i8_kernel, pgrid, dim3(256), 0, s, A, B, M, N, K, M, K, Np, (uint4 *)nullptr,
+                               (uint4 *)Bp, 0);
+            launch_i8_on_grid(A, Bp, C, M, Np, K, N, M, N, s);
+            return hipGetLastError();
+        }
         int8_t *Ap = (int8_t *)ws;
         int8_t *Bp = Ap + (size_t)Mp * Kp;
         const int wide = Kp > Np ? Kp : Np, tall = Mp > Kp ? Mp : Kp;
         const dim3 pgrid((unsigned)((wide / 16 + 255) / 256), (unsigned)(tall < 65535 ? tall : 65535), 2);
         hipLaunchKernelGGL(pad_i8_kernel, pgrid, dim3(256), 0, s, A, B, M, N, K, Mp, Kp, Np, (uint4 *)Ap,
-                           (uint4 *)Bp);
+                           (uint4 *)Bp, 1);
         launch_i8_on_grid(Ap, Bp, C, Mp, Np, Kp, N, M, N, s);
     } else {
         const int tiles_m = (M + BM - 1) / BM, tiles_n = (N + BN - 1) / BN;

@@ -833,7 +833,9 @@ def test_gemm_limb_sweep(op, m, k, n):
 # aligned: repacked into padded panels in the workspace (arena, caller
 # workspace or scratch), or, without a workspace, the byte-load kernel.
 RAGGED_I8 = [(1, 17, 1),(37, 100, 53), (300, 1000, 77), (256, 4095, 256), (1000, 1000, 1000), (257, 4100, 1003),
-             (64, 64, 64), (256, 256, 256)]
+             (64, 64, 64), (256, 256, 256),
+             # A on the full-tile grid, B ragged: only B is repacked when A is aligned
+             (128, 256, 77), (512, 1024, 1000), (1024, 2048, 1000)]
 
 
 def _offset_buffer(a, off):
