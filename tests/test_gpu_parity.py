@@ -989,6 +989,27 @@ def test_gemv_q16_shapes(m, k, nb):
     np.testing.assert_array_equal(got, O.gemv_q16_batched(W, X, m, k, nb))
 
 
+GEMV_FULL = [(64, 512, 2), (300, 1024, 3), (130, 2048, 8), (16, 32768, 8)]
+
+
+@pytest.mark.parametrize("fam", ["full", "extreme"])
+@pytest.mark.parametrize("m,k,nb", GEMV_FULL, ids=[f"{m}x{k}b{nb}" for m, k, nb in GEMV_FULL])
+def test_gemv_q16_batched_full_range(m, k, nb, fam):
+    """The batched (MFMA) path on full-range int32 W and x: every limb of W and
+    every digit of x in use (x near 2^31 - 1 needs the fifth digit), up to the
+    kernel's largest K."""
+    rng = np.random.default_rng(m * 31 + k + nb + len(fam))
+    ext = np.array([2147483647, -2147483648, -2147483647, 2139062144, 2139062143, 0, 1, -1, 65535, -65536,
+                    -8421505, 8421504], np.int32)
+    if fam == "full":
+        W, X = O.gen_q16(0xF011 ^ (m * k + nb), m * k, nb * k, shift=0)
+    else:
+        W, X = ext[rng.integers(0, len(ext), m * k)], ext[rng.integers(0, len(ext), nb * k)]
+    note(f"det_gemv_q16_batched {fam} {m}x{k} nb={nb}")
+    got = M.det_gemv_q16(W.reshape(m, k), X.reshape(nb, k))
+    np.testing.assert_array_equal(got, O.gemv_q16_batched(W, X, m, k, nb))
+
+
 @pytest.mark.parametrize("m,k", [(1, 1), (7, 9), (256, 256), (300, 1001), (4096, 4096)])
 def test_gemv_i16_shapes(m, k):
     W, x = O.gen_i16(0xDEADBEEF ^ (m * 3 + k), m * k, k)
