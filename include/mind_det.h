@@ -265,6 +265,9 @@ int64_t det_set_device(int64_t d);
 int64_t det_device_info(int64_t *info, char *name, int64_t name_len);
 int64_t det_malloc(void **p, int64_t bytes);
 int64_t det_free(void *p);
+/* Synchronous: each returns once its bytes have landed, so work queued
+ * afterwards on any stream (the library's streams do not wait for the null
+ * stream) sees them. */
 int64_t det_memcpy_htod(void *dst, const void *src, int64_t bytes);
 int64_t det_memcpy_dtoh(void *dst, const void *src, int64_t bytes);
 int64_t det_memset_dev(void *dst, int64_t byte, int64_t bytes);

@@ -772,8 +772,16 @@ int64_t det_free(void *p) {
     if (p) DET_HIP_CHECK(hipFree(p));
     return 0;
 }
+// The copies and the fill run on the null stream, which the library's
+// non-blocking streams do not wait for: each returns only once its bytes
+// have landed, so work queued afterwards on any stream sees them (hipMemcpy
+// from pageable memory may return while the last DMA to the device is still
+// in flight, and hipMemset is asynchronous for device memory).
 int64_t det_memcpy_htod(void *dst, const void *src, int64_t bytes) {
-    if (bytes > 0) DET_HIP_CHECK(hipMemcpy(dst, src, (size_t)bytes, hipMemcpyHostToDevice));
+    if (bytes > 0) {
+        DET_HIP_CHECK(hipMemcpy(dst, src, (size_t)bytes, hipMemcpyHostToDevice));
+        DET_HIP_CHECK(hipStreamSynchronize(nullptr));
+    }
     return 0;
 }
 int64_t det_memcpy_dtoh(void *dst, const void *src, int64_t bytes) {
@@ -781,7 +789,10 @@ int64_t det_memcpy_dtoh(void *dst, const void *src, int64_t bytes) {
     return 0;
 }
 int64_t det_memset_dev(void *dst, int64_t byte, int64_t bytes) {
-    if (bytes > 0) DET_HIP_CHECK(hipMemset(dst, (int)byte, (size_t)bytes));
+    if (bytes > 0) {
+        DET_HIP_CHECK(hipMemset(dst, (int)byte, (size_t)bytes));
+        DET_HIP_CHECK(hipStreamSynchronize(nullptr));
+    }
     return 0;
 }
 int64_t det_device_sync(void) {

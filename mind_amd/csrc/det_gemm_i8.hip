@@ -639,7 +639,9 @@ __global__ __launch_bounds__(THREADS, 1) void gemm_i8_dma_kernel(const int8_t *_
 // stores are spread over the first HEAD K steps of the next tile, after each
 // step's DMA; only the last tile's stores are left exposed at the end.
 namespace h128 {
-constexpr int BM = 128, WM = 64, MI = 2, SUB = 2, NST = 3, KS = BK * SUB;
+// MI: 16-row MFMA blocks per wave (v_mfma_i32_16x16x64_i8; see the tile
+// comment below for why not 32x32x32)
+constexpr int BM = 128, WM = 64, MI = WM / 16, SUB = 2, NST = 3, KS = BK * SUB;
 // groups of 8 row tiles (1024 rows, as the 256-row kernel's groups of 4):
 // each XCD's share of a 4096^3 grid then reads 4 MiB of A and 8 MiB of B
 constexpr int GROUP_M = 8;
@@ -647,33 +649,46 @@ constexpr int A_BYTES = BM * BK;
 constexpr int HEAD = 6;   // K steps that carry the previous tile's stores
 static_assert(HEAD % NST == 0 && HEAD >= NST, "the head must end on a stage-0 step");
 
-// Tile width TN = 256 (waves 64 x 64: 2 x 2 blocks) or 128 (waves 64 x 32:
-// 2 x 1 blocks, for grids that 128 x 256 tiles would leave half empty).
-// B sub-stage [64 k][TN n]: TN = 256 uses swz_b; for TN = 128 a row is 128
-// bytes (two rows per 64-bank cycle) and its eight chunks are XOR-swizzled by
-// 2 * ((row >> 1) & 3): the 32 lanes of a transposing read (rows k0..k0+7,
-// chunks c and c + 1, c even) then hit 16 distinct 16-byte bank groups.
+// Tile width TN = 256 (waves 64 x 64: 4 x 4 blocks of 16 x 16) or 128
+// (waves 64 x 32: 4 x 2 blocks, for grids that 128 x 256 tiles would leave
+// half empty).  The blocks are v_mfma_i32_16x16x64_i8, not 32x32x32: the same
+// LDS operand bytes and accumulator registers per wave, but on random int8
+// data the 16x16x64 instruction sustains about 25% more MACs per second under
+// the power-limited clock (register-only probes: 3.9 against 3.1 POP/s), as
+// each MAC reads and writes half the accumulator bits.
+// B sub-stage [64 k][TN n]: a transposing read's 16-lane group covers 8 rows
+// of one 16-byte chunk, and the groups of k slices 0 and 1 (rows 16 apart)
+// are served together, so the chunk of row r is XOR-swizzled by
+// 2 (r & 7) ^ ((r >> 4) & 1) (TN = 256) or, with two 128-byte rows per
+// 64-bank cycle, 2 ((r >> 1) & 3) ^ ((r >> 4) & 1) (TN = 128): the 32 lanes
+// of the two groups then hit 64 distinct banks.
+// A sub-stage [128 rows][64 k]: the 16-byte chunk c of row r sits at
+// c ^ ((r >> 1) & 3).  A 16x16x64 operand read (lane l: row l & 15 of the
+// block, chunk l >> 4) is then conflict-free; the 256-row kernel's
+// (r >> 2) & 3 serves its 32-row reads but halves the rate of these
+// (measured: 218 against 128 bytes per clock per CU).
+__device__ __forceinline__ int swz_a16(int row, int chunk) {
+    return row * 64 + ((chunk ^ ((row >> 1) & 3)) << 4);
+}
+
 template <int TN>
 struct Tile {
-    static constexpr int WNT = TN / 4, NJ = WNT / 32;
+    static constexpr int WNT = TN / 4, NJ = WNT / 16;   // 16-column blocks per wave
+    static constexpr int NJD = TN / 128;                 // 1 KiB B DMA blocks per wave per sub-stage
     static constexpr int B_BYTES = BK * TN, SS = A_BYTES + B_BYTES, ST = SUB * SS;
-    static constexpr int DPS = SUB * (1 + NJ);   // DMA instructions per wave per stage
-    static constexpr int NSTORE = MI * 16 * NJ;   // store instructions per wave per tile
+    static constexpr int DPS = SUB * (1 + NJD);   // DMA instructions per wave per stage
+    static constexpr int NSTORE = MI * NJ * 4;    // store instructions per wave per tile
     static constexpr int SPS = (NSTORE + HEAD - 1) / HEAD;   // stores per head step
     static_assert(DPS + SPS < 64, "vmcnt holds at most 63");
-    static __device__ __forceinline__ int swz(int row, int chunk) {
-        if constexpr (TN == 256) return swz_b(row, chunk);
-        else return row * 128 + ((chunk ^ (((row >> 1) & 3) << 1)) << 4);
+    static __device__ __forceinline__ int cx(int row) {
+        if constexpr (TN == 256) return ((row & 7) << 1) ^ ((row >> 4) & 1);
+        else return (((row >> 1) & 3) << 1) ^ ((row >> 4) & 1);
     }
+    static __device__ __forceinline__ int swz(int row, int chunk) { return row * TN + ((chunk ^ cx(row)) << 4); }
     // LDS slot (16-byte unit) of a B sub-stage -> the k-row and n-chunk it holds
     static __device__ __forceinline__ void b_chunk(int slot, int &br, int &bc) {
-        if constexpr (TN == 256) {
-            br = slot >> 4;
-            bc = (slot & 15) ^ ((br & 7) << 1);
-        } else {
-            br = slot >> 3;
-            bc = (slot & 7) ^ (((br >> 1) & 3) << 1);
-        }
+        br = slot / (TN / 16);
+        bc = (slot % (TN / 16)) ^ cx(br);
     }
     // stores carried by head step c (none outside the head)
     static __host__ __device__ constexpr int chunk_size(int c) {
@@ -709,49 +724,57 @@ __global__ __launch_bounds__(THREADS, 1) void gemm_i8_h128_kernel(const int8_t *
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int wm = (wave >> 2) * WM, wn = (wave & 3) * T::WNT;
-    const int l32 = lane & 31, lh = lane >> 5;
-    const int tg = lane >> 4, ti = lane & 15;
-    const int tr_row = 16 * (tg >> 1) + (ti >> 1);
-    const int tr_col = 16 * (tg & 1) + 8 * (ti & 1);
+    // 16x16x64 operand lanes: row / column l16 of a block, K slice tg (16 k)
+    const int l16 = lane & 15, tg = lane >> 4;
 
     const v4i32 ra = rsrc_words(A, (uint32_t)M * (uint32_t)K);
     const v4i32 rb = rsrc_words(B, (uint32_t)K * (uint32_t)N);
     // this lane's chunk of the wave's A block (1 KiB = 16 rows) and of its NJ
     // B blocks (1 KiB = 1024 / TN k-rows each) of a sub-stage, relative to the
     // tile origin: the inverse swizzles
-    uint32_t a_rel, b_rel[NJ];
+    uint32_t a_rel, b_rel[T::NJD];
     {
         const int slot = 64 * wave + lane;
-        const int ar = slot >> 2, ac = (slot & 3) ^ ((ar >> 2) & 3);
+        const int ar = slot >> 2, ac = (slot & 3) ^ ((ar >> 1) & 3);
         a_rel = (uint32_t)ar * (uint32_t)K + (uint32_t)(16 * ac);
     }
 #pragma unroll
-    for (int j = 0; j < NJ; ++j) {
+    for (int j = 0; j < T::NJD; ++j) {
         int br, bc;
-        T::b_chunk(64 * (NJ * wave + j) + lane, br, bc);
+        T::b_chunk(64 * (T::NJD * wave + j) + lane, br, bc);
         b_rel[j] = (uint32_t)br * (uint32_t)N + (uint32_t)(16 * bc);
     }
 
-    v16i32 acc[MI][NJ], prv[MI][NJ];
+    v4i32 acc[MI][NJ], prv[MI][NJ];
     int pm0 = 0, pn0 = 0;   // origin of the tile held in prv
     bool have_prev = false;
 
-    // store e of tile (tm0, tn0) from v: e = (i * 16 + r) * NJ + j.  The address
-    // is a wave-uniform row pointer plus this lane's byte offset (4 lh rows and
-    // l32 columns, below 2^32 since ldc < 2^24)
-    const uint32_t lane_b = (uint32_t)(4 * lh) * (uint32_t)ldc * 4u + (uint32_t)l32 * 4u;
+    // store e of tile (tm0, tn0) from v, e = ((i * 4 + r) * NJ / 2 + jp) * 2 + h:
+    // blocks 2 jp and 2 jp + 1 of row block i hold, in element r, rows
+    // 4 tg + r and columns 32 jp + l16 (+ 16).  v_permlane16_swap exchanges
+    // the odd 16-lane rows of the first with the even ones of the second, so
+    // each store writes two rows (h: 4 apart; lanes 0-31 and 32-63 rows 8
+    // apart) of 32 consecutive columns: whole 128-byte lines.  The address is
+    // a wave-uniform row pointer plus this lane's byte offset (8 (lane >> 5)
+    // rows and lane & 31 columns, below 2^32 since ldc < 2^24)
+    static_assert(NJ % 2 == 0, "column blocks are stored in pairs");
+    const int l32 = lane & 31, lh = lane >> 5;
+    const uint32_t lane_b = (uint32_t)(8 * lh) * (uint32_t)ldc * 4u + (uint32_t)l32 * 4u;
     // Non-temporal stores (streamed past L2) for whole rows; a masked tile
     // stores rows of ldc != N words, whose partial 128-byte lines merge
     // better in L2 (4095^3: 3% faster with plain stores, 4096^3 slower)
-    auto store_c = [&](const v16i32 (&v)[MI][NJ], int tm0, int tn0, int e) __attribute__((always_inline)) {
-        const int i = e / (16 * NJ), r = (e / NJ) & 15, j = e % NJ;
-        const int rowu = tm0 + wm + i * 32 + 8 * (r >> 2) + (r & 3);   // wave-uniform part
-        const int colu = tn0 + wn + 32 * j;
+    auto store_c = [&](const v4i32 (&v)[MI][NJ], int tm0, int tn0, int e) __attribute__((always_inline)) {
+        const int h = e & 1, jp = (e >> 1) % (NJ / 2), r = (e / NJ) & 3, i = e / (4 * NJ);
+        const auto sw = __builtin_amdgcn_permlane16_swap((unsigned)v[i][2 * jp][r], (unsigned)v[i][2 * jp + 1][r],
+                                                         false, false);
+        const int32_t val = (int32_t)(h ? sw[1] : sw[0]);
+        const int rowu = tm0 + wm + i * 16 + r + 4 * h;   // wave-uniform part
+        const int colu = tn0 + wn + 32 * jp;
         int32_t *dst = (int32_t *)((char *)(C + (size_t)rowu * ldc + colu) + lane_b);
         if constexpr (MASK) {
-            if (rowu + 4 * lh < mst && colu + l32 < nst) *dst = v[i][j][r];
+            if (rowu + 8 * lh < mst && colu + l32 < nst) *dst = val;
         } else {
-            __builtin_nontemporal_store(v[i][j][r], dst);
+            __builtin_nontemporal_store(val, dst);
         }
     };
     auto store_prev = [&](int e) __attribute__((always_inline)) { store_c(prv, pm0, pn0, e); };
@@ -771,92 +794,119 @@ __global__ __launch_bounds__(THREADS, 1) void gemm_i8_h128_kernel(const int8_t *
         const int tn = (pid % in_group) / gsize;
         const int m0 = tm * BM, n0 = tn * TN;
         const uint32_t a_off = (uint32_t)m0 * (uint32_t)K + a_rel;
-        uint32_t b_off[NJ];
+        uint32_t b_off[T::NJD];
 #pragma unroll
-        for (int j = 0; j < NJ; ++j) b_off[j] = b_rel[j] + (uint32_t)n0;
+        for (int j = 0; j < T::NJD; ++j) b_off[j] = b_rel[j] + (uint32_t)n0;
 
 #pragma unroll
         for (int i = 0; i < MI; ++i)
 #pragma unroll
-            for (int j = 0; j < NJ; ++j) acc[i][j] = (v16i32){0};
+            for (int j = 0; j < NJ; ++j) acc[i][j] = (v4i32){0, 0, 0, 0};
 
+        // the operands of one 64-k sub-stage: lane (l16, tg) holds k
+        // 16 tg .. 16 tg + 15 of A row l16 / B column l16 of each block
         struct Ops {
             v2i64 a[MI], b[NJ];
         };
-        auto read_ops = [&](Ops &o, int stage, int sub, int h) __attribute__((always_inline)) {
+        auto read_ops = [&](Ops &o, int stage, int sub) __attribute__((always_inline)) {
             const int8_t *sA = smem + stage * ST + sub * SS;
             const int8_t *sB = sA + A_BYTES;
 #pragma unroll
             for (int j = 0; j < NJ; ++j) {
-                const int r = 32 * h + tr_row, cb = (wn + 32 * j + tr_col) >> 4, sub8 = tr_col & 8;
+                // transposing reads: lane l16 of the group gets column
+                // wn + 16 j + l16, rows 16 tg .. +7 (lo) and +8 .. +15 (hi)
+                const int r = 16 * tg + (l16 >> 1), cb = (wn + 16 * j) >> 4, sub8 = 8 * (l16 & 1);
                 const v2i32 lo = read_tr8(sB + T::swz(r, cb) + sub8);
                 const v2i32 hi = read_tr8(sB + T::swz(r + 8, cb) + sub8);
                 o.b[j] = __builtin_bit_cast(v2i64, (v4i32){lo.x, lo.y, hi.x, hi.y});
             }
 #pragma unroll
-            for (int i = 0; i < MI; ++i) o.a[i] = *(const v2i64 *)(sA + swz_a(wm + i * 32 + l32, 2 * h + lh));
+            for (int i = 0; i < MI; ++i) o.a[i] = *(const v2i64 *)(sA + swz_a16(wm + i * 16 + l16, tg));
         };
-        auto mma = [&](const Ops &o) __attribute__((always_inline)) {
-#pragma unroll
-            for (int i = 0; i < MI; ++i)
-#pragma unroll
-                for (int j = 0; j < NJ; ++j) acc[i][j] = mfma32x32x32(o.a[i], o.b[j], acc[i][j]);
-        };
-        auto issue_f = [&](auto st_c, int k0) __attribute__((always_inline)) {
-            constexpr int st = decltype(st_c)::value;
+        // DMA instruction d (0 .. DPS-1) of this wave's share of the K step at
+        // byte offset k0 into stage st: sub-stage d / (1 + NJD), then its A
+        // block or one of its B blocks
+        auto dma_one = [&](auto st_c, auto d_c, int k0) __attribute__((always_inline)) {
+            constexpr int st = decltype(st_c)::value, d = decltype(d_c)::value;
+            constexpr int u = d / (1 + T::NJD), r = d % (1 + T::NJD);
             const bool in = k0 < K;
-            const uint32_t sa = in ? (uint32_t)k0 : last_a;
-            const uint32_t sb = in ? (uint32_t)k0 * (uint32_t)N : last_b;
-#pragma unroll
-            for (int u = 0; u < SUB; ++u) {
+            if constexpr (r == 0) {
+                const uint32_t sa = in ? (uint32_t)k0 : last_a;
                 dma16s(ra, base + (uint32_t)(st * ST + u * SS) + (uint32_t)wave * 1024u, (int)a_off,
                        sa + (uint32_t)(u * BK));
-#pragma unroll
-                for (int j = 0; j < NJ; ++j)
-                    dma16s(rb, base + (uint32_t)(st * ST + u * SS + A_BYTES) + (uint32_t)(NJ * wave + j) * 1024u,
-                           (int)b_off[j], sb + (uint32_t)(u * BK) * (uint32_t)N);
+            } else {
+                const uint32_t sb = in ? (uint32_t)k0 * (uint32_t)N : last_b;
+                dma16s(rb, base + (uint32_t)(st * ST + u * SS + A_BYTES) + (uint32_t)(T::NJD * wave + r - 1) * 1024u,
+                       (int)b_off[r - 1], sb + (uint32_t)(u * BK) * (uint32_t)N);
             }
+        };
+        auto issue_f = [&](auto st_c, int k0) __attribute__((always_inline)) {
+            unroll_ic<0, DPS>::run([&](auto d_c) __attribute__((always_inline)) { dma_one(st_c, d_c, k0); });
         };
         using S0 = std::integral_constant<int, 0>;
         using S1 = std::integral_constant<int, 1>;
         using S2 = std::integral_constant<int, 2>;
         static_assert(NST == 3, "the unrolled loop below assumes 3 stages");
-        // Ping-pong schedule as in gemm_i8_dma_kernel (slots A_j = {group 0:
-        // MFMA(j), group 1: MEM(j)}, B_j = {group 0: MEM(j+1), group 1: MFMA(j)}),
-        // with the DMA two steps ahead: MEM(s) reads step s (stage s % 3) and
-        // refills stage (s + 2) % 3 with step s + 2.  That stage held step s - 1,
-        // read in B_{s-2} and A_{s-1}; MEM(s) runs in B_{s-1} (group 0) or A_s
-        // (group 1), after both.  Before the barrier closing A_j each wave waits
-        // for its share of step j + 1: vmcnt(DPS + stores issued after the DMA
-        // of step j + 2), which leaves only those in flight (vector memory
-        // operations complete in issue order).
+        // Ping-pong schedule as in gemm_i8_dma_kernel: slots A_j = {group 0:
+        // MFMA(j), group 1: MEM(j)}, B_j = {group 0: MEM(j+1), group 1: MFMA(j)}.
+        // MEM(s) reads step s (stage s % 3) into registers.  The DMA refills
+        // go half into each phase, so that the texture unit's work is spread
+        // over both slots (issued all in MEM they held it past the MFMA phase's
+        // length; all in the MFMA phase, they stall its MFMA issue):
+        //   MEM(s): the first DH instructions of step s + 2, into (s + 2) % 3
+        //   group 0, MFMA(j) in A_j: the rest of step j + 2
+        //   group 1, MFMA(j) in B_j: the rest of step j + 3, into j % 3
+        // Step s - 1 (stage (s + 2) % 3) was read in B_{s-2} and A_{s-1}, step
+        // j in B_{j-1} and A_j: both before their refills.  Before the barrier
+        // closing A_j each wave waits for its share of step j + 1 (read from
+        // B_j on) with vmcnt(DPS + the stores of its last MEM phase): vector
+        // memory operations complete in issue order, and only that many were
+        // issued after it (for group 1 also the stores of the MEM phase
+        // before, which this waits for as well).
         // All LDS reads of the previous tile ended before its last barrier,
-        // and its past-the-end re-loads landed (vmcnt(0) below), so the first
-        // two stages can be refilled at once.
+        // and its past-the-end re-loads landed (vmcnt(0) below), so the
+        // prologue refills stages at once: steps 0 and 1, and for group 1 the
+        // second half of step 2 (its MFMA phases refill three steps ahead).
+        constexpr int DH = 0;
         issue_f(S0{}, 0);
         issue_f(S1{}, KS);
-        DET_WAIT_VMCNT(DPS);   // step 0 landed
+        if (wave >= 4) {
+            unroll_ic<DH, DPS>::run([&](auto d_c) __attribute__((always_inline)) { dma_one(S2{}, d_c, 2 * KS); });
+            DET_WAIT_VMCNT(DPS + DPS - DH);   // step 0 landed
+        } else {
+            DET_WAIT_VMCNT(DPS);
+        }
         __builtin_amdgcn_s_barrier();
-        Ops q0, q1, q2, q3;
-        // MEM(s), carrying head chunk CH of the previous tile's stores
+        Ops q0, q1;
+        // MEM(s) from stage ST, carrying head chunk CH of the previous tile's stores
         auto mem = [&](auto st_c, auto ch_c, int s) __attribute__((always_inline)) {
             constexpr int st = decltype(st_c)::value, ch = decltype(ch_c)::value;
-            read_ops(q0, st, 0, 0);
-            read_ops(q1, st, 0, 1);
-            read_ops(q2, st, 1, 0);
-            read_ops(q3, st, 1, 1);
-            issue_f(std::integral_constant<int, (st + 2) % NST>{}, (s + 2) * KS);
+            read_ops(q0, st, 0);
+            read_ops(q1, st, 1);
+            unroll_ic<0, DH>::run([&](auto d_c) __attribute__((always_inline)) {
+                dma_one(std::integral_constant<int, (st + 2) % NST>{}, d_c, (s + 2) * KS);
+            });
             if constexpr (T::chunk_size(ch) > 0) {
                 __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
                 for (int e = ch * SPS; e < ch * SPS + T::chunk_size(ch); ++e) store_prev(e);
             }
         };
-        auto mma_all = [&]() __attribute__((always_inline)) {
-            mma(q0);
-            mma(q1);
-            mma(q2);
-            mma(q3);
+        // the MFMA phase: MFMA e = (sub-stage, i, j) in the order (q0, q1);
+        // DMA instructions DH .. DPS-1 of the refill of stage SD with the step
+        // at k0 spread over it, one after every GAP MFMAs
+        auto mma_dma = [&](auto sd_c, int k0) __attribute__((always_inline)) {
+            constexpr int NM = 2 * MI * NJ, GAP = DPS > DH ? NM / (DPS - DH) : NM;
+            unroll_ic<0, NM>::run([&](auto e_c) __attribute__((always_inline)) {
+                constexpr int e = decltype(e_c)::value, q = e / (MI * NJ), i = (e / NJ) % MI, j = e % NJ;
+                const Ops &o = q == 0 ? q0 : q1;
+                acc[i][j] = mfma16x16x64(o.a[i], o.b[j], acc[i][j]);
+                if constexpr (e % GAP == 0 && DH + e / GAP < DPS) {
+                    __builtin_amdgcn_sched_barrier(0);
+                    dma_one(sd_c, std::integral_constant<int, DH + e / GAP>{}, k0);
+                    __builtin_amdgcn_sched_barrier(0);
+                }
+            });
         };
         using NONE = std::integral_constant<int, -1>;
         // a tile carries the previous one's stores in its head when it has at
@@ -869,10 +919,10 @@ __global__ __launch_bounds__(THREADS, 1) void gemm_i8_h128_kernel(const int8_t *
             // step kt: W = head chunk issued by MEM(kt), whose stores may still
             // be in flight; MEM(kt + 1) carries chunk kt + 1
             auto step0 = [&](auto cur_c, auto w_c, int kt) __attribute__((always_inline)) {
-                constexpr int nxt = (decltype(cur_c)::value + 1) % NST, w = decltype(w_c)::value;
+                constexpr int cur = decltype(cur_c)::value, nxt = (cur + 1) % NST, w = decltype(w_c)::value;
                 using CH = std::integral_constant<int, (w >= 0 && w + 1 < HEAD) ? w + 1 : -1>;
                 __builtin_amdgcn_sched_barrier(0);
-                mma_all();
+                mma_dma(std::integral_constant<int, (cur + 2) % NST>{}, (kt + 2) * KS);
                 __builtin_amdgcn_sched_barrier(0);
                 DET_WAIT_VMCNT(DPS + T::chunk_size(w));
                 __builtin_amdgcn_s_barrier();
@@ -913,7 +963,7 @@ __global__ __launch_bounds__(THREADS, 1) void gemm_i8_h128_kernel(const int8_t *
                 DET_WAIT_LGKM0();
                 __builtin_amdgcn_s_barrier();
                 __builtin_amdgcn_sched_barrier(0);
-                mma_all();
+                mma_dma(cur_c, (kt + 3) * KS);
                 __builtin_amdgcn_sched_barrier(0);
                 __builtin_amdgcn_s_barrier();
             };
