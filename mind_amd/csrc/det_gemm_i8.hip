@@ -1096,11 +1096,12 @@ static void launch_i8_on_grid(const int8_t *A, const int8_t *B, int32_t *C, int 
     const bool full128n = K > 0 && M % h128::BM == 0 && N % 128 == 0 && K % h128::KS == 0;
     const int cus = cu_count(), tm128 = M / h128::BM;
     // 128 x 128 tiles when they fit one round of the chip (M N <= 2^22 on 256
-    // CUs: 128 x 256 tiles would leave half the CUs idle); otherwise 128 x 256
-    // tiles when 256 x 256 tiles would not fill more than one round (or do
-    // not fit the shape)
+    // CUs: 128 x 256 tiles would leave half the CUs idle); otherwise the
+    // persistent 128 x 256 tiles whenever the shape allows them (same speed
+    // as the 256 x 256 kernel on the MLP layer, 2% faster at 8192^3, 12% at
+    // 6144^3, whose 2.25 rounds of 256 x 256 tiles quantise badly)
     const bool use128n = full128n && tm128 * (N / 128) <= cus;
-    const bool use128 = !use128n && full128 && (!full || tiles_m * tiles_n <= cus);
+    const bool use128 = !use128n && full128;
     if (use128 || use128n) {
         const int tn = use128n ? N / 128 : N / BN, nt = tm128 * tn;
         // persistent workgroups: as many rounds of tiles as the CUs need, the
