@@ -377,7 +377,8 @@ def measure_peaks(stream) -> dict:
     rnd_in = M.DeviceBuffer.from_array(np.random.default_rng(0x5EED).integers(0, 256, 1024 * 16, dtype=np.uint8))
     mfma_tops = {}
     for shape, per_iter, name, src in ((0, 8 * 16384, "16x16x64", ops_in), (1, 8 * 32768, "32x32x32", ops_in),
-                                       (2, 16 * 32768, "32x32x32_random_operands", rnd_in)):
+                                       (2, 16 * 32768, "32x32x32_random_operands", rnd_in),
+                                       (3, 32 * 16384, "16x16x64_random_operands", rnd_in)):
         def mfma():
             M.check(L.det_probe_mfma_i8(src.ptr, out.ptr, blocks, iters, shape, sp))
 
@@ -641,7 +642,8 @@ def main() -> int:
         result["measured_peaks"] = pk = measure_peaks(stream)
         log(f"peaks: {pk}")
         best = max(pk["mfma_i8_tops"]["16x16x64"], pk["mfma_i8_tops"]["32x32x32"])
-        rnd = pk["mfma_i8_tops"]["32x32x32_random_operands"]
+        # the int8 GEMM kernels issue v_mfma_i32_16x16x64_i8
+        rnd = pk["mfma_i8_tops"]["16x16x64_random_operands"]
         result["roofline"]["measured_peak"] = best
         result["roofline"]["frac_of_measured_peak"] = round(tops / best, 4)
         result["roofline"]["measured_peak_random_operands"] = rnd

@@ -286,7 +286,9 @@ int64_t det_event_elapsed_ms(void *start, void *stop, float *ms);
  * ints); shape 0 = 16x16x64, 1 = 32x32x32;
  * ops = blocks * 4 * iters * 8 * (16384 or 32768) * 2; shape 2 = 32x32x32
  * cycling 8 operand pairs, 16 MFMAs per iteration (in: 1024 x 16 bytes),
- * ops = blocks * 4 * iters * 16 * 32768 * 2.  det_probe_read streams
+ * ops = blocks * 4 * iters * 16 * 32768 * 2; shape 3 = 16x16x64 cycling
+ * 8 operand pairs, 32 MFMAs per iteration (in: 1024 x 16 bytes),
+ * ops = blocks * 4 * iters * 32 * 16384 * 2.  det_probe_read streams
  * `bytes` once (out: `blocks` zeroed words).  det_copy_dev is the plain copy
  * kernel of known size that calibrates the profiler's byte counters. */
 int64_t det_probe_mfma_i8(const void *in, int32_t *out, int64_t blocks, int64_t iters, int64_t shape,

@@ -278,7 +278,9 @@ struct I16Epi {
 // EPI_I8 stores C[row][col] at C + row * ldc + col for row < mst, col < nst
 // (ldc = nst = N, mst = M, except for operands repacked into padded panels:
 // see launch_gemm_i8); MASK = false: every row and column of the tile is
-// stored (full tiles of an unpadded problem).
+// stored (full tiles of an unpadded problem).  The int8 GEMM sends every
+// full-tile shape to the h128 kernel below, so EPI_I8 runs here only on the
+// edge path; the int16 GEMM (EPI_I16) uses both paths.
 template <int EPI, bool FULL, bool MASK = !FULL>
 __global__ __launch_bounds__(THREADS, 1) void gemm_i8_dma_kernel(const int8_t *__restrict__ A,
                                                                  const int8_t *__restrict__ B,
@@ -1091,15 +1093,16 @@ static void launch_i8_on_grid(const int8_t *A, const int8_t *B, int32_t *C, int 
     using namespace i8g;
     const int tiles_m = (M + BM - 1) / BM, tiles_n = (N + BN - 1) / BN;
     const dim3 grid(tiles_m * tiles_n), block(THREADS);
-    const bool full = K > 0 && M % BM == 0 && N % BN == 0 && K % (BK * NSTAGE) == 0;
     const bool full128 = K > 0 && M % h128::BM == 0 && N % BN == 0 && K % h128::KS == 0;
     const bool full128n = K > 0 && M % h128::BM == 0 && N % 128 == 0 && K % h128::KS == 0;
     const int cus = cu_count(), tm128 = M / h128::BM;
     // 128 x 128 tiles when they fit one round of the chip (M N <= 2^22 on 256
     // CUs: 128 x 256 tiles would leave half the CUs idle); otherwise the
     // persistent 128 x 256 tiles whenever the shape allows them (same speed
-    // as the 256 x 256 kernel on the MLP layer, 2% faster at 8192^3, 12% at
-    // 6144^3, whose 2.25 rounds of 256 x 256 tiles quantise badly)
+    // as the 256 x 256 full-tile kernel on the MLP layer, 2% faster at
+    // 8192^3, 12% at 6144^3, whose 2.25 rounds of 256 x 256 tiles quantise
+    // badly), so every full 256 x 256 shape lands here too; the rest go to
+    // the range-checked 256 x 256 kernel
     const bool use128n = full128n && tm128 * (N / 128) <= cus;
     const bool use128 = !use128n && full128;
     if (use128 || use128n) {
@@ -1119,13 +1122,6 @@ static void launch_i8_on_grid(const int8_t *A, const int8_t *B, int32_t *C, int 
             if (mask) rounds > 1 ? go(gemm_i8_h128_kernel<true, true, 256>) : go(gemm_i8_h128_kernel<true, false, 256>);
             else rounds > 1 ? go(gemm_i8_h128_kernel<false, true, 256>) : go(gemm_i8_h128_kernel<false, false, 256>);
         }
-    } else if (full) {
-        if (mask)
-            hipLaunchKernelGGL((gemm_i8_dma_kernel<EPI_I8, true, true>), grid, block, 0, s, A, B, C, M, N, K, tiles_m,
-                               tiles_n, ldc, mst, nst, I16Epi{});
-        else
-            hipLaunchKernelGGL((gemm_i8_dma_kernel<EPI_I8, true, false>), grid, block, 0, s, A, B, C, M, N, K, tiles_m,
-                               tiles_n, ldc, mst, nst, I16Epi{});
     } else {
         hipLaunchKernelGGL((gemm_i8_dma_kernel<EPI_I8, false>), grid, block, 0, s, A, B, C, M, N, K, tiles_m, tiles_n,
                            ldc, mst, nst, I16Epi{});

@@ -17,12 +17,33 @@ namespace probe {
 // in[512 + 64 c + l]), cycled so consecutive MFMAs see different data: with
 // random operands this is the issue rate a GEMM's data allows, since the
 // clock under int8 MFMA load depends on how many operand bits toggle.
+// SHAPE 3: the same for 16x16x64 (32 MFMAs per round, the MACs of 16
+// 32x32x32), the instruction the int8 GEMM kernels issue.
 template <int SHAPE>
 __global__ __launch_bounds__(256) void mfma_i8_kernel(const v2i64 *__restrict__ in, int *__restrict__ out, int iters) {
     const int l = threadIdx.x & 63;
     const v2i64 a = in[l], b = in[64 + l];
     int s = 0;
-    if (SHAPE == 2) {
+    if (SHAPE == 3) {
+        v2i64 x[8], y[8];
+#pragma unroll
+        for (int c = 0; c < 8; ++c) {
+            x[c] = in[64 * c + l];
+            y[c] = in[512 + 64 * c + l];
+        }
+        v4i32 c0 = {0, 0, 0, 0}, c1 = c0, c2 = c0, c3 = c0, c4 = c0, c5 = c0, c6 = c0, c7 = c0;
+        for (int it = 0; it < iters; ++it) {
+#define MF(c, i, j) asm volatile("v_mfma_i32_16x16x64_i8 %0, %1, %2, %0" : "+v"(c) : "v"(x[i]), "v"(y[j]))
+            MF(c0, 0, 0); MF(c1, 1, 1); MF(c2, 2, 2); MF(c3, 3, 3); MF(c4, 4, 4); MF(c5, 5, 5); MF(c6, 6, 6); MF(c7, 7, 7);
+            MF(c0, 1, 2); MF(c1, 2, 3); MF(c2, 3, 4); MF(c3, 4, 5); MF(c4, 5, 6); MF(c5, 6, 7); MF(c6, 7, 0); MF(c7, 0, 1);
+            MF(c0, 2, 4); MF(c1, 3, 5); MF(c2, 4, 6); MF(c3, 5, 7); MF(c4, 6, 0); MF(c5, 7, 1); MF(c6, 0, 2); MF(c7, 1, 3);
+            MF(c0, 3, 6); MF(c1, 4, 7); MF(c2, 5, 0); MF(c3, 6, 1); MF(c4, 7, 2); MF(c5, 0, 3); MF(c6, 1, 4); MF(c7, 2, 5);
+#undef MF
+        }
+        asm volatile("s_nop 7\n s_nop 7" ::);
+        const v4i32 t = c0 ^ c1 ^ c2 ^ c3 ^ c4 ^ c5 ^ c6 ^ c7;
+        s = t.x ^ t.y ^ t.z ^ t.w;
+    } else if (SHAPE == 2) {
         v2i64 x[8], y[8];
 #pragma unroll
         for (int c = 0; c < 8; ++c) {
@@ -83,19 +104,22 @@ __global__ __launch_bounds__(256) void copy_kernel(uint4 *__restrict__ dst, cons
 
 extern "C" {
 
-// in: 128 x 16 bytes of operands (shapes 0, 1) or 1024 x 16 (shape 2), out:
-// blocks*256 ints.  Returns the launch status; ops per launch = blocks * 4
-// waves * iters * MFMAs * MACs * 2: 8 x 16384 (shape 0, 16x16x64),
+// in: 128 x 16 bytes of operands (shapes 0, 1) or 1024 x 16 (shapes 2, 3),
+// out: blocks*256 ints.  Returns the launch status; ops per launch = blocks *
+// 4 waves * iters * MFMAs * MACs * 2: 8 x 16384 (shape 0, 16x16x64),
 // 8 x 32768 (shape 1, 32x32x32), 16 x 32768 (shape 2, 32x32x32 cycling
-// 8 operand pairs).
+// 8 operand pairs), 32 x 16384 (shape 3, 16x16x64 cycling 8 operand pairs).
 int64_t det_probe_mfma_i8(const void *in, int32_t *out, int64_t blocks, int64_t iters, int64_t shape, void *stream) {
-    if (!in || !out || blocks <= 0 || iters <= 0 || blocks > (1 << 20) || iters > (1 << 30) || shape < 0 || shape > 2)
+    if (!in || !out || blocks <= 0 || iters <= 0 || blocks > (1 << 20) || iters > (1 << 30) || shape < 0 || shape > 3)
         return det_fail(DET_ERR_ARG, "bad det_probe_mfma_i8 arguments");
     if (shape == 0)
         hipLaunchKernelGGL(det::probe::mfma_i8_kernel<0>, dim3((unsigned)blocks), dim3(256), 0, (hipStream_t)stream,
                            (const det::v2i64 *)in, out, (int)iters);
     else if (shape == 1)
         hipLaunchKernelGGL(det::probe::mfma_i8_kernel<1>, dim3((unsigned)blocks), dim3(256), 0, (hipStream_t)stream,
+                           (const det::v2i64 *)in, out, (int)iters);
+    else if (shape == 3)
+        hipLaunchKernelGGL(det::probe::mfma_i8_kernel<3>, dim3((unsigned)blocks), dim3(256), 0, (hipStream_t)stream,
                            (const det::v2i64 *)in, out, (int)iters);
     else
         hipLaunchKernelGGL(det::probe::mfma_i8_kernel<2>, dim3((unsigned)blocks), dim3(256), 0, (hipStream_t)stream,

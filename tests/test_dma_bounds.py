@@ -274,154 +274,3 @@ def test_h128_a_stage_layout_round_trips():
         for t in range(64):
             np.testing.assert_array_equal(lds[addr[t]:addr[t] + 16], tile[row[t], 16 * chunk[t]:16 * chunk[t] + 16])
 
-
-def _h128_addresses(M, N, K, tn=256):
-    """gemm_i8_h128_kernel: 128-row tiles of width tn, K steps of 128 as two
-    64-wide sub-stages, each wave one A block and tn / 128 B blocks per
-    sub-stage; the prologue issues steps 0 and 1 (and 2 for the second wave
-    group), the MFMA phase of step s issues step s + 2 (first group) or s + 3
-    (second group), so steps up to nk + 2 are issued."""
-    KS = 2 * BK
-    nj = tn // 128
-    wave = np.arange(8)[:, None]
-    lane = np.arange(64)[None, :]
-    slot = (64 * wave + lane).ravel()
-    ar = slot >> 2
-    akc = 16 * ((slot & 3) ^ ((ar >> 1) & 3))
-    bslot = (64 * (nj * np.arange(8)[:, None, None] + np.arange(nj)[None, :, None])
-             + np.arange(64)[None, None, :]).ravel()
-    br, bc = _b_chunk(bslot, tn)
-    bnc = 16 * bc
-    assert ar.max() < 128 and br.max() < 64 and bnc.max() + 16 <= tn
-    nk = K // KS
-    lo = [None, None]
-    hi = [None, None]
-    for m0 in range(0, M, 128):
-        a_off = (m0 + ar) * K + akc
-        for n0 in range(0, N, tn):
-            b_off = br * N + n0 + bnc
-            for step in range(0, nk + 3):
-                k0 = step * KS
-                sa = k0 if k0 < K else K - KS
-                sb = k0 * N if k0 < K else (K - KS) * N
-                for u in range(2):
-                    for i, v in enumerate((a_off + sa + u * BK, b_off + sb + u * BK * N)):
-                        lo[i] = v.min() if lo[i] is None else min(lo[i], v.min())
-                        hi[i] = v.max() if hi[i] is None else max(hi[i], v.max())
-    return (lo[0], hi[0] + 16, M * K), (lo[1], hi[1] + 16, K * N)
-
-
-@pytest.mark.parametrize("M,N,K,tn", [(128, 256, 128, 256), (4096, 4096, 4096, 256), (384, 512, 384, 256),
-                                      (2048, 2048, 2048, 256), (128, 768, 1152, 256), (128, 128, 128, 128),
-                                      (2048, 2048, 2048, 128), (384, 640, 1152, 128)])
-def test_h128_tile_dma_stays_inside_operands(M, N, K, tn):
-    assert M % 128 == 0 and N % tn == 0 and K % 128 == 0 and K > 0
-    for lo, end, lim in _h128_addresses(M, N, K, tn):
-        assert lo >= 0 and end <= lim, (end, lim)
-
-
-@pytest.mark.parametrize("M,N,K", [(1, 16, 16), (100, 48, 80), (257, 272, 320), (300, 1008, 48), (256, 256, 64)])
-def test_edge_tile_dma_stays_inside_operands(M, N, K):
-    assert K % 16 == 0 and N % 16 == 0
-    assert _edge_addresses(M, N, K) <= 0
-
-
-def _pad_row_chunks(src, base, rows, cols, dcols):
-    """pad_i8_kernel's reads for one operand, restated: returns the padded
-    panel it writes and checks every load stays inside the source buffer.
-    `src` is the buffer's bytes, `base` its address modulo 4."""
-    total = rows * cols
-    out = np.zeros((rows, dcols), np.uint8)
-    for row in range(rows):
-        for c0 in range(0, dcols, 16):
-            if c0 >= cols:
-                continue
-            p = row * cols + c0
-            at = base + p
-            a = at & ~3
-            if c0 + 16 <= cols and a >= base and a + 20 <= base + total:
-                lo = a - base
-                assert 0 <= lo and lo + 20 <= total
-                v = src[lo:lo + 20].view("<u4").astype(np.uint64)
-                sh = at & 3
-                w = [int((((v[i + 1] << np.uint64(32)) | v[i]) >> np.uint64(8 * sh)) & np.uint64(0xFFFFFFFF))
-                     for i in range(4)]
-                out[row, c0:c0 + 16] = np.array(w, "<u4").view(np.uint8)
-            else:
-                nv = min(16, cols - c0)
-                assert 0 <= p and p + nv <= total
-                out[row, c0:c0 + nv] = src[p:p + nv]
-    return out
-
-
-@pytest.mark.parametrize("rows,cols", [(1, 1), (3, 17), (5, 33), (7, 4095), (2, 64), (4, 20)])
-@pytest.mark.parametrize("base", [0, 1, 2, 3])
-def test_pad_kernel_reads_stay_inside_and_assemble_the_rows(rows, cols, base):
-    rng = np.random.default_rng(rows * 131 + cols + base)
-    src = rng.integers(0, 256, rows * cols, dtype=np.uint8)
-    dcols = (cols + 15) // 16 * 16
-    got = _pad_row_chunks(src, base, rows, cols, dcols)
-    want = np.zeros((rows, dcols), np.uint8)
-    want[:, :cols] = src.reshape(rows, cols)
-    np.testing.assert_array_equal(got, want)
-
-
-def _b_chunk(slot, tn):
-    """LDS slot (16-byte unit) of a B sub-stage -> (k-row, n-chunk) it holds
-    (Tile<TN>::b_chunk)."""
-    if tn == 256:
-        br = slot >> 4
-        return br, (slot & 15) ^ ((br & 7) << 1)
-    br = slot >> 3
-    return br, (slot & 7) ^ (((br >> 1) & 3) << 1)
-
-
-def _b_swz(row, chunk, tn):
-    """Byte offset of (k-row, n-chunk) in a B sub-stage (Tile<TN>::swz)."""
-    if tn == 256:
-        return row * 256 + ((chunk ^ ((row & 7) << 1)) << 4)
-    return row * 128 + ((chunk ^ (((row >> 1) & 3) << 1)) << 4)
-
-
-@pytest.mark.parametrize("tn", [256, 128])
-def test_h128_b_stage_layout_round_trips_and_reads_conflict_free(tn):
-    """The B sub-stage of gemm_i8_h128_kernel<., ., TN>: the DMA places the
-    global chunk b_chunk(slot) at slot (16 bytes per lane); the transposing
-    reads (ds_read_b64_tr_b8: lane t of a 16-lane group gets byte t & 7 of
-    the segments of lanes 2j + (t >> 3)) must hand lane l the MFMA B operand
-    B[32h + 16 (l >> 5) + 0..15][wn + 32 j + (l & 31)], and each half-wave
-    must touch all 64 four-byte banks exactly once."""
-    nj = tn // 128
-    rng = np.random.default_rng(tn)
-    tile = rng.integers(0, 256, size=(64, tn), dtype=np.uint8)   # one sub-stage: B[k][n]
-    lds = np.zeros(64 * tn, np.uint8)
-    written = np.zeros(64 * tn, bool)
-    for slot in range(64 * tn // 16):
-        br, bc = _b_chunk(slot, tn)
-        assert 0 <= br < 64 and 0 <= bc < tn // 16
-        lds[16 * slot:16 * slot + 16] = tile[br, 16 * bc:16 * bc + 16]
-        written[16 * slot:16 * slot + 16] = True
-    assert written.all()
-    lane = np.arange(64)
-    tg, ti = lane >> 4, lane & 15
-    tr_row = 16 * (tg >> 1) + (ti >> 1)
-    tr_col = 16 * (tg & 1) + 8 * (ti & 1)
-    for wn in range(0, tn, tn // 4):
-        for j in range(nj):
-            for h in range(2):
-                got = np.zeros((64, 16), np.uint8)
-                for half, dr in enumerate((0, 8)):
-                    r = 32 * h + tr_row + dr
-                    cb = (wn + 32 * j + tr_col) >> 4
-                    addr = np.array([_b_swz(int(r[i]), int(cb[i]), tn) for i in range(64)]) + (tr_col & 8)
-                    for w in (slice(0, 32), slice(32, 64)):
-                        banks = np.concatenate([(addr[w] // 4) % 64, (addr[w] // 4 + 1) % 64])
-                        assert len(set(banks.tolist())) == 64
-                    for t in range(64):
-                        g = 16 * (t >> 4)
-                        for jj in range(8):
-                            src = g + 2 * jj + ((t & 15) >> 3)
-                            got[t, 8 * half + jj] = lds[addr[src] + (t & 7)]
-                want = np.stack([tile[32 * h + 16 * (t >> 5):32 * h + 16 * (t >> 5) + 16, wn + 32 * j + (t & 31)]
-                                 for t in range(64)])
-                np.testing.assert_array_equal(got, want)
