@@ -890,8 +890,19 @@ __global__ __launch_bounds__(THREADS, 1) void gemm_i8_h128_kernel(const int8_t *
             });
             if constexpr (T::chunk_size(ch) > 0) {
                 __builtin_amdgcn_sched_barrier(0);
+                if constexpr (MASK) {
+                    // the masked stores' row / column tests, hoisted out of
+                    // the K loop for all NSTORE stores, spill the LDS read
+                    // addresses (reloaded with vmcnt(0) waits that drain the
+                    // DMA): an opaque copy of the tile origin keeps them here
+                    int pm = pm0, pn = pn0;
+                    asm volatile("" : "+s"(pm), "+s"(pn));
 #pragma unroll
-                for (int e = ch * SPS; e < ch * SPS + T::chunk_size(ch); ++e) store_prev(e);
+                    for (int e = ch * SPS; e < ch * SPS + T::chunk_size(ch); ++e) store_c(prv, pm, pn, e);
+                } else {
+#pragma unroll
+                    for (int e = ch * SPS; e < ch * SPS + T::chunk_size(ch); ++e) store_prev(e);
+                }
             }
         };
         // the MFMA phase: MFMA e = (sub-stage, i, j) in the order (q0, q1);
