@@ -1018,6 +1018,203 @@ __global__ __launch_bounds__(THREADS, 1) void gemm_i8_h128_kernel(const int8_t *
         for (int e = 0; e < NSTORE; ++e) store_prev(e);
 }
 }  // namespace h128
+
+// 256 x 256 tiles of 16x16x64 blocks: eight waves (two per SIMD) of 128 x 64
+// (8 x 4 blocks), K steps of 64 through four LDS stages of 32 KiB.  A 64-k
+// step brings 32 KiB per CU into LDS by DMA for 256 x 256 x 64 MACs, two
+// thirds of the h128 tiles' 48 KiB per 128 x 256 x 128; that L2-to-LDS stream
+// sets the h128 step time, so on grids of at least one full round of these
+// tiles the larger tile runs its K loop faster, though its stores are not
+// overlapped with a next tile (the accumulators fill the registers).
+namespace t256 {
+constexpr int BM = 256, TN = 256, WM = 128, WN = 64, MI = WM / 16, NJ = WN / 16;
+constexpr int NST = 4, A_BYTES = BM * BK, B_BYTES = BK * TN, SS = A_BYTES + B_BYTES;   // 32 KiB stages
+constexpr int DPS = 4;       // DMA instructions per wave per step: 2 A and 2 B blocks of 1 KiB
+constexpr int GROUP_M = 4;   // 1024 rows sharing a B column panel
+constexpr int NSTORE = MI * NJ * 4;
+using TB = h128::Tile<TN>;   // B stage [64 k][256 n], the h128 layout
+using h128::unroll_ic;
+
+template <bool MASK>
+__global__ __launch_bounds__(THREADS, 1) void gemm_i8_t256_kernel(const int8_t *__restrict__ A,
+                                                                  const int8_t *__restrict__ B,
+                                                                  int32_t *__restrict__ C, int M, int N, int K,
+                                                                  int tiles_m, int tiles_n, int ldc, int mst, int nst) {
+    __shared__ __attribute__((aligned(1024))) int8_t smem[NST * SS];
+
+    const int ntiles = tiles_m * tiles_n;
+    const int pid = xcd_remap(blockIdx.x, ntiles);
+    const int in_group = GROUP_M * tiles_n;
+    const int first_m = (pid / in_group) * GROUP_M;
+    const int gsize = min(tiles_m - first_m, GROUP_M);
+    const int m0 = (first_m + (pid % in_group) % gsize) * BM, n0 = ((pid % in_group) / gsize) * TN;
+
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int wm = (wave >> 2) * WM, wn = (wave & 3) * WN;
+    const int l16 = lane & 15, tg = lane >> 4;
+
+    const v4i32 ra = rsrc_words(A, (uint32_t)M * (uint32_t)K);
+    const v4i32 rb = rsrc_words(B, (uint32_t)K * (uint32_t)N);
+    // this lane's chunk of the wave's two A blocks (16 rows x 64 k) and two B
+    // blocks (4 k-rows x 256 n) of a stage: the inverse swizzles
+    uint32_t a_off[2], b_off[2];
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+        const int slot = 64 * (2 * wave + j) + lane;
+        const int ar = slot >> 2, ac = (slot & 3) ^ ((ar >> 1) & 3);
+        a_off[j] = (uint32_t)(m0 + ar) * (uint32_t)K + (uint32_t)(16 * ac);
+        int br, bc;
+        TB::b_chunk(slot, br, bc);
+        b_off[j] = (uint32_t)br * (uint32_t)N + (uint32_t)(n0 + 16 * bc);
+    }
+    // K advances through soffset, which the range check does not cover: a
+    // step past the end re-loads the last step (into a stage never read again)
+    const uint32_t last_a = (uint32_t)(K - BK), last_b = (uint32_t)(K - BK) * (uint32_t)N;
+    const uint32_t base = lds_addr(smem);
+    // DMA instruction d of this wave's share of the step at k0 into stage st
+    auto dma_one = [&](auto st_c, auto d_c, int k0) __attribute__((always_inline)) {
+        constexpr int st = decltype(st_c)::value, d = decltype(d_c)::value;
+        const bool in = k0 < K;
+        if constexpr (d < 2) {
+            dma16s(ra, base + (uint32_t)(st * SS) + (uint32_t)(2 * wave + d) * 1024u, (int)a_off[d],
+                   in ? (uint32_t)k0 : last_a);
+        } else {
+            dma16s(rb, base + (uint32_t)(st * SS + A_BYTES) + (uint32_t)(2 * wave + d - 2) * 1024u, (int)b_off[d - 2],
+                   in ? (uint32_t)k0 * (uint32_t)N : last_b);
+        }
+    };
+    auto issue_f = [&](auto st_c, int k0) __attribute__((always_inline)) {
+        unroll_ic<0, DPS>::run([&](auto d_c) __attribute__((always_inline)) { dma_one(st_c, d_c, k0); });
+    };
+
+    v4i32 acc[MI][NJ];
+#pragma unroll
+    for (int i = 0; i < MI; ++i)
+#pragma unroll
+        for (int j = 0; j < NJ; ++j) acc[i][j] = (v4i32){0, 0, 0, 0};
+
+    // the operands of one step: lane (l16, tg) holds k 16 tg .. 16 tg + 15 of
+    // A row l16 / B column l16 of each block
+    struct Ops {
+        v2i64 a[MI], b[NJ];
+    } q;
+    auto mem = [&](auto st_c) __attribute__((always_inline)) {
+        const int8_t *sA = smem + decltype(st_c)::value * SS;
+        const int8_t *sB = sA + A_BYTES;
+#pragma unroll
+        for (int j = 0; j < NJ; ++j) {
+            const int r = 16 * tg + (l16 >> 1), cb = (wn + 16 * j) >> 4, sub8 = 8 * (l16 & 1);
+            const v2i32 lo = read_tr8(sB + TB::swz(r, cb) + sub8);
+            const v2i32 hi = read_tr8(sB + TB::swz(r + 8, cb) + sub8);
+            q.b[j] = __builtin_bit_cast(v2i64, (v4i32){lo.x, lo.y, hi.x, hi.y});
+        }
+#pragma unroll
+        for (int i = 0; i < MI; ++i) q.a[i] = *(const v2i64 *)(sA + h128::swz_a16(wm + i * 16 + l16, tg));
+    };
+    // the MFMA phase
+    auto mma = [&]() __attribute__((always_inline)) {
+#pragma unroll
+        for (int i = 0; i < MI; ++i)
+#pragma unroll
+            for (int j = 0; j < NJ; ++j) acc[i][j] = mfma16x16x64(q.a[i], q.b[j], acc[i][j]);
+    };
+    using S0 = std::integral_constant<int, 0>;
+    using S1 = std::integral_constant<int, 1>;
+    using S2 = std::integral_constant<int, 2>;
+    using S3 = std::integral_constant<int, 3>;
+    static_assert(NST == 4, "the unrolled loop below assumes 4 stages");
+    // Ping-pong: waves w and w + 4 share a SIMD.  Slots between barriers
+    //   A_j = {group 0: MFMA(j), group 1: MEM(j)}, B_j = {group 0: MEM(j+1), group 1: MFMA(j)}
+    // MEM(s) reads step s from stage s % 4 and issues the wave's DMA share
+    // of a later step: group 1 in A_j step j + 3 into stage (j + 3) % 4 (step
+    // j - 1, read in B_{j-2} and A_{j-1}), group 0 in B_j step j + 4 into
+    // stage j % 4 (step j, read in B_{j-1} and A_j).  Before the barrier
+    // closing A_j each wave waits for its share of step j + 1: two of its
+    // later steps (8 DMA instructions) stay in flight.  The prologue fills
+    // steps 0-2, and step 3 for group 0.  (Spread over the MFMA phase
+    // instead, as the h128 kernel does, the DMA measured 2% slower here.)
+    const int nk = K / BK;
+    issue_f(S0{}, 0);
+    issue_f(S1{}, BK);
+    issue_f(S2{}, 2 * BK);
+    if (wave < 4) {
+        issue_f(S3{}, 3 * BK);
+        DET_WAIT_VMCNT(3 * DPS);
+    } else {
+        DET_WAIT_VMCNT(2 * DPS);
+    }
+    __builtin_amdgcn_s_barrier();
+    if (wave < 4) {
+        mem(S0{});
+        DET_WAIT_LGKM0();
+        __builtin_amdgcn_s_barrier();
+        auto step0 = [&](auto cur_c, int kt) __attribute__((always_inline)) {
+            constexpr int cur = decltype(cur_c)::value;
+            __builtin_amdgcn_sched_barrier(0);
+            mma();
+            __builtin_amdgcn_sched_barrier(0);
+            DET_WAIT_VMCNT(2 * DPS);
+            __builtin_amdgcn_s_barrier();
+            __builtin_amdgcn_sched_barrier(0);
+            mem(std::integral_constant<int, (cur + 1) % NST>{});   // past the last step: unused reads
+            issue_f(std::integral_constant<int, cur>{}, (kt + 4) * BK);
+            DET_WAIT_LGKM0();
+            __builtin_amdgcn_sched_barrier(0);
+            __builtin_amdgcn_s_barrier();
+        };
+        for (int kt = 0; kt < nk; kt += NST) {
+            step0(S0{}, kt);
+            step0(S1{}, kt + 1);
+            step0(S2{}, kt + 2);
+            step0(S3{}, kt + 3);
+        }
+    } else {
+        __builtin_amdgcn_s_barrier();
+        auto step1 = [&](auto cur_c, int kt) __attribute__((always_inline)) {
+            __builtin_amdgcn_sched_barrier(0);
+            mem(cur_c);
+            issue_f(std::integral_constant<int, (decltype(cur_c)::value + 3) % NST>{}, (kt + 3) * BK);
+            DET_WAIT_VMCNT(2 * DPS);
+            DET_WAIT_LGKM0();
+            __builtin_amdgcn_s_barrier();
+            __builtin_amdgcn_sched_barrier(0);
+            mma();
+            __builtin_amdgcn_sched_barrier(0);
+            __builtin_amdgcn_s_barrier();
+        };
+        for (int kt = 0; kt < nk; kt += NST) {
+            step1(S0{}, kt);
+            step1(S1{}, kt + 1);
+            step1(S2{}, kt + 2);
+            step1(S3{}, kt + 3);
+        }
+    }
+    // the re-loads issued past the end of K must not outlive the workgroup
+    DET_WAIT_VMCNT(0);
+
+    // stores as in the h128 kernel: blocks 2 jp and 2 jp + 1 of row block i
+    // paired by v_permlane16_swap, two rows (h: 4 apart; lane halves 8 apart)
+    // of 32 consecutive columns (one 128-byte line) per instruction
+    const int l32 = lane & 31, lh = lane >> 5;
+    const uint32_t lane_b = (uint32_t)(8 * lh) * (uint32_t)ldc * 4u + (uint32_t)l32 * 4u;
+#pragma unroll
+    for (int e = 0; e < NSTORE; ++e) {
+        const int h = e & 1, jp = (e >> 1) % (NJ / 2), r = (e / NJ) & 3, i = e / (4 * NJ);
+        const auto sw = __builtin_amdgcn_permlane16_swap((unsigned)acc[i][2 * jp][r], (unsigned)acc[i][2 * jp + 1][r],
+                                                         false, false);
+        const int32_t val = (int32_t)(h ? sw[1] : sw[0]);
+        const int rowu = m0 + wm + i * 16 + r + 4 * h;
+        const int colu = n0 + wn + 32 * jp;
+        int32_t *dst = (int32_t *)((char *)(C + (size_t)rowu * ldc + colu) + lane_b);
+        if constexpr (MASK) {
+            if (rowu + 8 * lh < mst && colu + l32 < nst) *dst = val;
+        } else {
+            __builtin_nontemporal_store(val, dst);
+        }
+    }
+}
+}  // namespace t256
 }  // namespace i8g
 
 // Compute units of the current device (cached per device).
@@ -1115,8 +1312,24 @@ static void launch_i8_on_grid(const int8_t *A, const int8_t *B, int32_t *C, int 
     // badly), so every full 256 x 256 shape lands here too; the rest go to
     // the range-checked 256 x 256 kernel
     const bool use128n = full128n && tm128 * (N / 128) <= cus;
-    const bool use128 = !use128n && full128;
-    if (use128 || use128n) {
+    // 256 x 256 tiles (faster K loop, stores not overlapped) when they fill
+    // their rounds of the chip to at least 7/8 (4096^3 and 8192^3: exactly,
+    // the MLP layer: 688 tiles, 0.9 of three rounds; not 6144^3: 576 tiles,
+    // 0.75 of three rounds, where the persistent 128 x 256 tiles balance
+    // better)
+    const int t256n = (M / t256::BM) * (N / t256::TN), r256 = (t256n + cus - 1) / cus;
+    const bool use256 = !use128n && K > 0 && M % t256::BM == 0 && N % t256::TN == 0 && K % (BK * t256::NST) == 0 &&
+                        t256n >= cus && 8 * t256n >= 7 * r256 * cus;
+    const bool use128 = !use128n && !use256 && full128;
+    if (use256) {
+        const int tm = M / t256::BM, tn = N / t256::TN;
+        if (mask)
+            hipLaunchKernelGGL(t256::gemm_i8_t256_kernel<true>, dim3(tm * tn), block, 0, s, A, B, C, M, N, K, tm, tn,
+                               ldc, mst, nst);
+        else
+            hipLaunchKernelGGL(t256::gemm_i8_t256_kernel<false>, dim3(tm * tn), block, 0, s, A, B, C, M, N, K, tm, tn,
+                               ldc, mst, nst);
+    } else if (use128 || use128n) {
         const int tn = use128n ? N / 128 : N / BN, nt = tm128 * tn;
         // persistent workgroups: as many rounds of tiles as the CUs need, the
         // tiles spread evenly over a multiple of 8 workgroups (one XCD each)

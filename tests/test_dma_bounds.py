@@ -251,26 +251,67 @@ def test_h128_b_stage_layout_round_trips_and_reads_conflict_free(tn):
             np.testing.assert_array_equal(got, want)
 
 
-def test_h128_a_stage_layout_round_trips():
-    """A sub-stage [128 rows][64 k] of gemm_i8_h128_kernel, chunk c of row r
-    at c ^ ((r >> 1) & 3): the DMA lane -> chunk assignment (the inverse) fills
-    every slot once, and the 16x16x64 operand read (lane l: row 16 i + (l & 15),
-    chunk l >> 4) gets row r's chunk (l >> 4)."""
+@pytest.mark.parametrize("rows", [128, 256])
+def test_a_stage_layout_round_trips(rows):
+    """A sub-stage [rows][64 k] of gemm_i8_h128_kernel (128 rows) and
+    gemm_i8_t256_kernel (256 rows), chunk c of row r at c ^ ((r >> 1) & 3):
+    the DMA lane -> chunk assignment (the inverse) fills every slot once, and
+    the 16x16x64 operand read (lane l: row 16 i + (l & 15), chunk l >> 4)
+    gets row r's chunk (l >> 4)."""
     rng = np.random.default_rng(7)
-    tile = rng.integers(0, 256, size=(128, 64), dtype=np.uint8)
-    lds = np.zeros(128 * 64, np.uint8)
-    seen = np.zeros(128 * 64 // 16, bool)
-    for slot in range(128 * 64 // 16):
+    tile = rng.integers(0, 256, size=(rows, 64), dtype=np.uint8)
+    lds = np.zeros(rows * 64, np.uint8)
+    seen = np.zeros(rows * 64 // 16, bool)
+    for slot in range(rows * 64 // 16):
         ar = slot >> 2
         ac = (slot & 3) ^ ((ar >> 1) & 3)
         lds[16 * slot:16 * slot + 16] = tile[ar, 16 * ac:16 * ac + 16]
         seen[slot] = True
     assert seen.all()
     lane = np.arange(64)
-    for i in range(8):
+    for i in range(rows // 16):
         row = 16 * i + (lane & 15)
         chunk = lane >> 4
         addr = row * 64 + ((chunk ^ ((row >> 1) & 3)) << 4)
         for t in range(64):
             np.testing.assert_array_equal(lds[addr[t]:addr[t] + 16], tile[row[t], 16 * chunk[t]:16 * chunk[t] + 16])
 
+
+def _t256_addresses(M, N, K):
+    """gemm_i8_t256_kernel: 256 x 256 tiles, K steps of 64; each of the 8
+    waves moves 2 A blocks (16 rows x 64 k) and 2 B blocks (4 k-rows x 256 n)
+    per step.  The prologue issues steps 0-2 (and 3 for the first wave
+    group), the memory phases of step j issue step j + 4 (first group) or
+    j + 3 (second group), so steps up to nk + 3 are issued (those past the
+    end re-load step nk - 1)."""
+    slot = (64 * (2 * np.arange(8)[:, None, None] + np.arange(2)[None, :, None])
+            + np.arange(64)[None, None, :]).ravel()
+    assert sorted(slot.tolist()) == list(range(1024))   # every slot of both 16 KiB halves once
+    ar = slot >> 2
+    akc = 16 * ((slot & 3) ^ ((ar >> 1) & 3))
+    br, bc = _b_chunk(slot, 256)
+    bnc = 16 * bc
+    assert ar.max() < 256 and br.max() < 64 and bnc.max() + 16 <= 256
+    nk = K // BK
+    lo = [None, None]
+    hi = [None, None]
+    for m0 in range(0, M, 256):
+        a_off = (m0 + ar) * K + akc
+        for n0 in range(0, N, 256):
+            b_off = br * N + n0 + bnc
+            for step in range(0, nk + 4):
+                k0 = step * BK
+                sa = k0 if k0 < K else K - BK
+                sb = k0 * N if k0 < K else (K - BK) * N
+                for i, v in enumerate((a_off + sa, b_off + sb)):
+                    lo[i] = v.min() if lo[i] is None else min(lo[i], v.min())
+                    hi[i] = v.max() if hi[i] is None else max(hi[i], v.max())
+    return (lo[0], hi[0] + 16, M * K), (lo[1], hi[1] + 16, K * N)
+
+
+@pytest.mark.parametrize("M,N,K", [(256, 256, 256), (4096, 4096, 4096), (512, 768, 1024), (4096, 11008, 4096),
+                                   (256, 512, 8192)])
+def test_t256_tile_dma_stays_inside_operands(M, N, K):
+    assert M % 256 == 0 and N % 256 == 0 and K % 256 == 0
+    for lo, end, lim in _t256_addresses(M, N, K):
+        assert lo >= 0 and end <= lim, (end, lim)

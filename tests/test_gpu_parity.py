@@ -725,7 +725,8 @@ def _mt_gemm_i8(a, b, m, k, n):
 PERSIST_I8 = [(2048, 768, 4352), (1408, 768, 6144), (2048, 512, 4352), (4224, 768, 4352)]
 # off the 16-byte grid, repacked into padded panels, on grids of several
 # rounds: persistent 128 x 256 tiles with the masked epilogue (2304 x 4352
-# panels: 306 tiles) and the masked 256 x 256 kernel (4352^2: 289 tiles)
+# panels: 306 tiles; 4352^2: 578 tiles, whose 289 tiles of 256 x 256 would
+# fill two rounds only to 0.56)
 PERSIST_I8 += [(2100, 1000, 4100), (4100, 300, 4100)]
 
 
@@ -736,6 +737,22 @@ def test_gemm_i8_persistent_rounds(m, k, n):
     C = _dev_run(lambda pa, pb, pc, s: M.lib().det_matmul_i8_dev(pa, pb, pc, m, k, n, s), [a, b], (m, n))
     np.testing.assert_array_equal(C, _mt_gemm_i8(a, b, m, k, n))
     rows = np.r_[0, 127, 128, m - 1]
+    np.testing.assert_array_equal(C[rows], O.gemm_i8_rows(a, b, m, k, n, rows))
+
+
+# 256 x 256 tiles (grids that fill whole rounds of them): padded panels with
+# the masked epilogue in one round (4096^2 panels) and two rounds (4096 x
+# 8192), and an unpadded grid of two rounds
+T256_I8 = [(4000, 1000, 4000), (4000, 300, 8100), (4096, 512, 8192)]
+
+
+@pytest.mark.parametrize("m,k,n", T256_I8, ids=[f"{m}x{k}x{n}" for m, k, n in T256_I8])
+def test_gemm_i8_t256_tiles(m, k, n):
+    a, b = O.gen_i8(0x7256 ^ (m * 1000003 + k * 1009 + n), m * k, k * n)
+    note(f"det_matmul_i8_dev (256x256 tiles) {m}x{k}x{n}")
+    C = _dev_run(lambda pa, pb, pc, s: M.lib().det_matmul_i8_dev(pa, pb, pc, m, k, n, s), [a, b], (m, n))
+    np.testing.assert_array_equal(C, _mt_gemm_i8(a, b, m, k, n))
+    rows = np.r_[0, 255, 256, m - 1]
     np.testing.assert_array_equal(C[rows], O.gemm_i8_rows(a, b, m, k, n, rows))
 
 
