@@ -1035,11 +1035,15 @@ constexpr int NSTORE = MI * NJ * 4;
 using TB = h128::Tile<TN>;   // B stage [64 k][256 n], the h128 layout
 using h128::unroll_ic;
 
-template <bool MASK>
+// EPI_I8: C[row][col] at C + row * ldc + col for row < mst, col < nst (MASK;
+// all rows and columns of the tile otherwise).  EPI_I16: the int16 limb
+// interleave's epilogue (see gemm_i8_dma_kernel), into e16.C.
+template <bool MASK, int EPI = EPI_I8>
 __global__ __launch_bounds__(THREADS, 1) void gemm_i8_t256_kernel(const int8_t *__restrict__ A,
                                                                   const int8_t *__restrict__ B,
                                                                   int32_t *__restrict__ C, int M, int N, int K,
-                                                                  int tiles_m, int tiles_n, int ldc, int mst, int nst) {
+                                                                  int tiles_m, int tiles_n, int ldc, int mst, int nst,
+                                                                  I16Epi e16) {
     __shared__ __attribute__((aligned(1024))) int8_t smem[NST * SS];
 
     const int ntiles = tiles_m * tiles_n;
@@ -1053,6 +1057,17 @@ __global__ __launch_bounds__(THREADS, 1) void gemm_i8_t256_kernel(const int8_t *
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int wm = (wave >> 2) * WM, wn = (wave & 3) * WN;
     const int l16 = lane & 15, tg = lane >> 4;
+    const int l32 = lane & 31, lh = lane >> 5;
+    // EPI_I16: this lane's int16 output column is the same for all its
+    // stores (see the epilogue), so its column-sum partials load here and
+    // their latency hides behind the K loop
+    const int col16 = ((n0 + wn) >> 1) + 16 * ((lane >> 4) & 1) + 8 * (lane & 1) + ((lane & 15) >> 1);
+    uint32_t cs_part[EPI == EPI_I16 ? MAX_CS : 1];
+    if constexpr (EPI == EPI_I16) {
+        const int cc = min(col16, e16.N16 - 1);
+#pragma unroll
+        for (int i = 0; i < MAX_CS; ++i) cs_part[i] = e16.colsum[(size_t)min(i, e16.ncs - 1) * e16.N16 + cc];
+    }
 
     const v4i32 ra = rsrc_words(A, (uint32_t)M * (uint32_t)K);
     const v4i32 rb = rsrc_words(B, (uint32_t)K * (uint32_t)N);
@@ -1193,10 +1208,64 @@ __global__ __launch_bounds__(THREADS, 1) void gemm_i8_t256_kernel(const int8_t *
     // the re-loads issued past the end of K must not outlive the workgroup
     DET_WAIT_VMCNT(0);
 
+    if constexpr (EPI == EPI_I16) {
+        // Lane l, element r of block (i, j) holds int8-product row 16 i + 4 tg
+        // + r (int16 row 8 i + 2 tg + (r >> 1), A limb r & 1) and column
+        // 16 j + l16 (int16 column 8 j + (l16 >> 1), B limb l16 & 1).  Per
+        // row pair p = r >> 1 a lane forms c_0Y + 2^8 c_1Y, shifted by 8 on
+        // odd lanes (B limb 1); one DPP exchange between lanes 2c and 2c + 1
+        // completes block 2 jp on the even lane and block 2 jp + 1 on the odd
+        // one (int16 columns 16 jp + c and 16 jp + 8 + c), and
+        // v_permlane16_swap of the jp = 0 and 1 results joins lane groups
+        // (tg 0, 1) and (2, 3): every store then writes two int16 rows (8 i +
+        // 2 s + p and 4 below) of 32 consecutive int32 (whole 128-byte lines),
+        // lane l at column col16.
+        const uint32_t odd = lane & 1, oddm = 0u - odd;
+        const int m16_0 = (m0 + wm) >> 1, n16_0 = (n0 + wn) >> 1;   // the wave's 64 x 32 output block
+        uint32_t cs = 0;
+#pragma unroll
+        for (int i = 0; i < MAX_CS; ++i) cs += i < e16.ncs ? cs_part[i] : 0u;
+        // bias terms c (rowsum + colsum) - K c^2, c = 0x80
+        cs = (cs << 7) - e16.kc2;
+        auto epilogue = [&](auto checked_c) __attribute__((always_inline)) {
+            constexpr bool checked = decltype(checked_c)::value;
+#pragma unroll
+            for (int i = 0; i < MI; ++i)
+#pragma unroll
+                for (int p = 0; p < 2; ++p) {
+                    uint32_t v[2];
+#pragma unroll
+                    for (int jp = 0; jp < 2; ++jp) {
+                        uint32_t part[2];
+#pragma unroll
+                        for (int jj = 0; jj < 2; ++jj) {
+                            const uint32_t lo = (uint32_t)acc[i][2 * jp + jj][2 * p];
+                            const uint32_t hi = (uint32_t)acc[i][2 * jp + jj][2 * p + 1];
+                            part[jj] = (lo + (hi << 8)) << (8 * odd);
+                        }
+                        const uint32_t send = (part[0] & oddm) | (part[1] & ~oddm);
+                        const uint32_t keep = (part[1] & oddm) | (part[0] & ~oddm);
+                        // lanes 2c <-> 2c+1: quad_perm [1, 0, 3, 2]
+                        v[jp] = keep + (uint32_t)__builtin_amdgcn_mov_dpp((int)send, 0xB1, 0xF, 0xF, false);
+                    }
+                    const auto sw = __builtin_amdgcn_permlane16_swap(v[0], v[1], false, false);
+#pragma unroll
+                    for (int sidx = 0; sidx < 2; ++sidx) {
+                        const int row = m16_0 + 8 * i + 2 * sidx + p + 4 * lh;
+                        const uint32_t o = (uint32_t)sw[sidx] + (e16.rowsum[min(row, e16.M16 - 1)] << 7) + cs;
+                        int32_t *dst = e16.C + (size_t)row * e16.N16 + col16;
+                        if (!checked || (row < e16.M16 && col16 < e16.N16)) __builtin_nontemporal_store((int32_t)o, dst);
+                    }
+                }
+        };
+        // wave-uniform: is the wave's 64 x 32 output block inside C?
+        if (m16_0 + 64 <= e16.M16 && n16_0 + 32 <= e16.N16) epilogue(std::false_type{});
+        else epilogue(std::true_type{});
+        return;
+    }
     // stores as in the h128 kernel: blocks 2 jp and 2 jp + 1 of row block i
     // paired by v_permlane16_swap, two rows (h: 4 apart; lane halves 8 apart)
     // of 32 consecutive columns (one 128-byte line) per instruction
-    const int l32 = lane & 31, lh = lane >> 5;
     const uint32_t lane_b = (uint32_t)(8 * lh) * (uint32_t)ldc * 4u + (uint32_t)l32 * 4u;
 #pragma unroll
     for (int e = 0; e < NSTORE; ++e) {
@@ -1325,10 +1394,10 @@ static void launch_i8_on_grid(const int8_t *A, const int8_t *B, int32_t *C, int 
         const int tm = M / t256::BM, tn = N / t256::TN;
         if (mask)
             hipLaunchKernelGGL(t256::gemm_i8_t256_kernel<true>, dim3(tm * tn), block, 0, s, A, B, C, M, N, K, tm, tn,
-                               ldc, mst, nst);
+                               ldc, mst, nst, I16Epi{});
         else
             hipLaunchKernelGGL(t256::gemm_i8_t256_kernel<false>, dim3(tm * tn), block, 0, s, A, B, C, M, N, K, tm, tn,
-                               ldc, mst, nst);
+                               ldc, mst, nst, I16Epi{});
     } else if (use128 || use128n) {
         const int tn = use128n ? N / 128 : N / BN, nt = tm128 * tn;
         // persistent workgroups: as many rounds of tiles as the CUs need, the
@@ -1396,7 +1465,12 @@ hipError_t launch_gemm_i8_i16epi(const int8_t *A2, const int8_t *B2, int M2, int
     const int tiles_m = (M2 + BM - 1) / BM, tiles_n = (N2 + BN - 1) / BN;
     I16Epi e{rowsum, colsum, C, M16, N16, ncs, 0x80u, (uint32_t)((uint64_t)(uint32_t)K16 * 0x4000u)};
     const bool full = Kp > 0 && M2 % BM == 0 && N2 % BN == 0 && Kp % (BK * NSTAGE) == 0;
-    if (full)
+    // 16x16x64 256 x 256 tiles when they fill whole rounds, as for int8
+    const int cus = cu_count(), nt = tiles_m * tiles_n, rounds = (nt + cus - 1) / cus;
+    if (full && nt >= cus && 8 * nt >= 7 * rounds * cus)
+        hipLaunchKernelGGL((t256::gemm_i8_t256_kernel<false, EPI_I16>), dim3(nt), dim3(THREADS), 0, s, A2, B2,
+                           (int32_t *)nullptr, M2, N2, Kp, tiles_m, tiles_n, N2, M2, N2, e);
+    else if (full)
         hipLaunchKernelGGL((gemm_i8_dma_kernel<EPI_I16, true>), dim3(tiles_m * tiles_n), dim3(THREADS), 0, s, A2, B2,
                            (int32_t *)nullptr, M2, N2, Kp, tiles_m, tiles_n, N2, M2, N2, e);
     else
