@@ -10,22 +10,31 @@
 // wrap-around, i.e. mod 2^32, which is exactly the reference's i64 sum
 // truncated to i32.
 //
-// Tiling: one 512-thread workgroup (8 waves, 2 per SIMD) per 256x256 C tile;
-// each wave owns 128x64 = 4x2 blocks of v_mfma_i32_32x32x32_i8.  K advances
-// 64 bytes per step.  Both operands move global -> registers -> LDS as raw
-// 16-byte row chunks (buffer_load_dwordx4 / ds_write_b128, XOR-swizzled so
-// both the writes and the operand reads are bank-conflict free):
-//  * A (K contiguous) is read back with ds_read_b128: lane l gets 16
-//    K-bytes of row l & 31, the MFMA A layout.
-//  * B (N contiguous) needs K-contiguous bytes per column; it is read back
-//    with gfx950's transposing LDS read ds_read_b64_tr_b8.  Within each
-//    16-lane group that instruction returns, to lane t, byte t & 7 of the
-//    8-byte segments addressed by lanes 2j + (t >> 3), j = 0..7; so when
-//    lane i addresses row k0 + (i >> 1), columns n0 + 8 (i & 1), lane t
-//    receives B[k0 .. k0+7][n0 + t] -- one column, 8 consecutive K.  Two such
-//    reads form the 16-byte B operand.
-// Loads run two K steps ahead of the MFMAs (two register sets, two LDS
-// buffers, one barrier per step).
+// Kernels (routing in launch_i8_on_grid / launch_gemm_i8, all 512 threads =
+// 8 waves, 2 per SIMD):
+//  * gemm_i8_t256_kernel: 256 x 256 tiles of v_mfma_i32_16x16x64_i8 blocks,
+//    operands moved global -> LDS by direct DMA (buffer_load ... lds), four
+//    64-k stages, the two waves of a SIMD in ping-pong (one runs MFMAs while
+//    the other reads LDS and issues DMA); grids that fill whole rounds of the
+//    CUs (4096^3, 8192^3, the MLP layer), and the int16 limb interleave.
+//  * h128::gemm_i8_h128_kernel: the same machinery on 128 x 256 tiles,
+//    persistent (a tile's stores overlap the next tile's K loop), or on
+//    128 x 128 tiles for grids that fit one round of them.
+//  * gemm_i8_dma_kernel: 256 x 256 tiles of v_mfma_i32_32x32x32_i8 with a
+//    range-checked DMA for shapes on the 16-byte grid off those multiples,
+//    and the int16 epilogue on grids the t256 kernel does not take.
+//  * gemm_i8_kernel: byte loads for operands off the 16-byte grid when no
+//    workspace is given (otherwise pad_i8_kernel repacks them into padded
+//    panels for the kernels above).
+// A (K contiguous) is read from LDS with ds_read_b128 in the MFMA A layout;
+// B (N contiguous) needs K-contiguous bytes per column and is read with
+// gfx950's transposing ds_read_b64_tr_b8: within each 16-lane group that
+// instruction returns, to lane t, byte t & 7 of the 8-byte segments
+// addressed by lanes 2j + (t >> 3), j = 0..7; so when lane i addresses row
+// k0 + (i >> 1), columns n0 + 8 (i & 1), lane t receives B[k0 .. k0+7][n0 + t]
+// -- one column, 8 consecutive K.  Two such reads form a 16-byte B operand.
+// LDS layouts are XOR-swizzled so the DMA placement and the operand reads
+// are bank-conflict free.
 #include <type_traits>
 
 #include "det_common.h"
@@ -622,11 +631,12 @@ __global__ __launch_bounds__(THREADS, 1) void gemm_i8_dma_kernel(const int8_t *_
 }
 // ------------------------------------------------------- 128-row tiles
 // The same ping-pong schedule on a 128 x TN C tile (TN = 256 or 128), for
-// grids whose 256 x 256 tiles would fill at most one round of the chip.
-// Small grids (2048^3: 64 tiles of 256^2) use up to four times as many CUs,
-// and at 4096^3 each CU owns two 128 x 256 tiles.  The price is a smaller
-// wave tile (64 x 64 or 64 x 32), more LDS bytes per MFMA, so grids of
-// several rounds stay on the 256 x 256 kernel.
+// grids that 256 x 256 tiles would fill poorly: small grids (2048^3: 64
+// tiles of 256^2) use up to four times as many CUs, and grids whose 256 x 256
+// tiles fill their last round to less than 7/8 (6144^3) balance better on
+// persistent 128 x 256 tiles.  The price is a smaller wave tile (64 x 64 or
+// 64 x 32): more LDS and DMA bytes per MFMA, so grids that fill whole rounds
+// of 256 x 256 tiles go to the t256 kernel.
 // A stage holds K = 128 as two 64-wide sub-stages, each laid out like a
 // stage of the 256 x 256 kernel (A [128][64] with swz_a, B [64][TN]), so a
 // barrier slot carries 16 (TN = 256) or 8 (TN = 128) MFMAs per wave; 3
@@ -1374,12 +1384,10 @@ static void launch_i8_on_grid(const int8_t *A, const int8_t *B, int32_t *C, int 
     const bool full128n = K > 0 && M % h128::BM == 0 && N % 128 == 0 && K % h128::KS == 0;
     const int cus = cu_count(), tm128 = M / h128::BM;
     // 128 x 128 tiles when they fit one round of the chip (M N <= 2^22 on 256
-    // CUs: 128 x 256 tiles would leave half the CUs idle); otherwise the
-    // persistent 128 x 256 tiles whenever the shape allows them (same speed
-    // as the 256 x 256 full-tile kernel on the MLP layer, 2% faster at
-    // 8192^3, 12% at 6144^3, whose 2.25 rounds of 256 x 256 tiles quantise
-    // badly), so every full 256 x 256 shape lands here too; the rest go to
-    // the range-checked 256 x 256 kernel
+    // CUs: 128 x 256 tiles would leave half the CUs idle); otherwise 256 x 256
+    // tiles when they fill their rounds (below), else the persistent
+    // 128 x 256 tiles whenever the shape allows them; the rest go to the
+    // range-checked 256 x 256 kernel
     const bool use128n = full128n && tm128 * (N / 128) <= cus;
     // 256 x 256 tiles (faster K loop, stores not overlapped) when they fill
     // their rounds of the chip to at least 7/8 (4096^3 and 8192^3: exactly,
