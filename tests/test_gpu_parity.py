@@ -982,6 +982,20 @@ def test_gemm_i16_shapes(m, k, n):
     np.testing.assert_array_equal(M.det_matmul_i16(a.reshape(m, k), b.reshape(k, n)), O.gemm_i16(a, b, m, k, n))
 
 
+# limb interleaves that fill whole rounds of 256 x 256 tiles (the 16x16x64
+# kernel with the int16 epilogue): 2048 x 1024 x 2048 (M2 = N2 = 4096, one
+# round) and 4096 x 256 x 1024 (8192 x 2048 interleave, one round)
+I16_T256 = [(2048, 1024, 2048), (4096, 256, 1024)]
+
+
+@pytest.mark.parametrize("m,k,n", I16_T256, ids=[f"{m}x{k}x{n}" for m, k, n in I16_T256])
+def test_gemm_i16_t256_tiles(m, k, n):
+    a, b = O.gen_i16(0x16256 ^ (m * 131 + k * 17 + n), m * k, k * n)
+    note(f"det_matmul_i16 (256x256 tiles) {m}x{k}x{n}")
+    got = M.det_matmul_i16(a.reshape(m, k), b.reshape(k, n))
+    np.testing.assert_array_equal(got, _mt_gemm(M.DET_OP_I16, a, b, m, k, n))
+
+
 def test_gemm_i16_extremes():
     m, k, n = 8, 70000, 8
     a = np.full((m, k), -32768, np.int16)
