@@ -627,7 +627,7 @@ def main() -> int:
                      "frac": round(tops / PEAK_INT8_TOPS, 4), "traffic": traffic,
                      "traffic_note": "HBM bytes per launch from rocprofv3 FETCH_SIZE x2.0 + WRITE_SIZE x1.0 "
                                      "(scales from a 1 GiB copy kernel); algorithmic 100,663,296",
-                     "kernel": "det::i8g::t256::gemm_i8_t256_kernel<false>",
+                     "kernel": "det::i8g::t256::gemm_i8_t256_kernel<false, 0>",
                      "algorithmic": "2*M*N*K = 1.374e11 int8 ops per launch (one launch per step)",
                      "event_ms_per_launch": round(head["ms"], 5),
                      "gmac_per_s": round(tops * 500.0, 1),
