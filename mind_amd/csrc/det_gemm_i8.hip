@@ -862,9 +862,9 @@ __global__ __launch_bounds__(THREADS, 1) void gemm_i8_h128_kernel(const int8_t *
         // Ping-pong schedule as in gemm_i8_dma_kernel: slots A_j = {group 0:
         // MFMA(j), group 1: MEM(j)}, B_j = {group 0: MEM(j+1), group 1: MFMA(j)}.
         // MEM(s) reads step s (stage s % 3) into registers.  The DMA refills
-        // go half into each phase, so that the texture unit's work is spread
-        // over both slots (issued all in MEM they held it past the MFMA phase's
-        // length; all in the MFMA phase, they stall its MFMA issue):
+        // can be split between the phases (DH instructions per step in MEM);
+        // with the 16x16x64 blocks all of them go into the MFMA phase, one
+        // after every GAP MFMAs (DH = 1, 2 or 3 measured equal or slower):
         //   MEM(s): the first DH instructions of step s + 2, into (s + 2) % 3
         //   group 0, MFMA(j) in A_j: the rest of step j + 2
         //   group 1, MFMA(j) in B_j: the rest of step j + 3, into j % 3
