@@ -315,3 +315,57 @@ def test_t256_tile_dma_stays_inside_operands(M, N, K):
     assert M % 256 == 0 and N % 256 == 0 and K % 256 == 0
     for lo, end, lim in _t256_addresses(M, N, K):
         assert lo >= 0 and end <= lim, (end, lim)
+
+
+def _permlane16_swap(a, b):
+    """v_permlane16_swap_b32 on 64-lane vectors: the second 16 lanes of each
+    32-lane half of `a` trade places with the first 16 of `b`."""
+    r0, r1 = a.copy(), b.copy()
+    for base in (0, 32):
+        r0[base + 16:base + 32] = b[base:base + 16]
+        r1[base:base + 16] = a[base + 16:base + 32]
+    return r0, r1
+
+
+def test_t256_int16_epilogue_lane_algebra():
+    """The int16 epilogue of gemm_i8_t256_kernel, restated lane by lane: from
+    the 16x16x64 result layout (lane l, element r = row 4 (l >> 4) + r,
+    column l & 15 of each block) through the per-lane limb combination, the
+    DPP exchange between lanes 2c and 2c + 1 and v_permlane16_swap, every
+    store must put sum_{X,Y} 2^(8 (X + Y)) c[2 i' + X][2 j' + Y] (mod 2^32) at
+    int16 row 8 i + 2 s + p + 4 (l >> 5), column col16(l) of the wave's
+    64 x 32 output block, and together the stores must cover it once."""
+    rng = np.random.default_rng(5)
+    c8 = rng.integers(-2**31, 2**31, size=(128, 64), dtype=np.int64).astype(np.uint32)   # wave's int8-GEMM block
+    want = np.zeros((64, 32), np.uint64)
+    for X in range(2):
+        for Y in range(2):
+            want += c8[X::2, Y::2].astype(np.uint64) << np.uint64(8 * (X + Y))
+    want &= np.uint64(0xFFFFFFFF)
+    lane = np.arange(64)
+    odd = lane & 1
+    col16 = 16 * ((lane >> 4) & 1) + 8 * (lane & 1) + ((lane & 15) >> 1)
+    seen = np.zeros((64, 32), int)
+    for i in range(8):
+        for p in range(2):
+            v = []
+            for jp in range(2):
+                part = []
+                for jj in range(2):
+                    j = 2 * jp + jj
+                    rows = 16 * i + 4 * (lane >> 4)
+                    cols = 16 * j + (lane & 15)
+                    lo = c8[rows + 2 * p, cols].astype(np.uint64)
+                    hi = c8[rows + 2 * p + 1, cols].astype(np.uint64)
+                    part.append(((lo + (hi << np.uint64(8))) << (np.uint64(8) * odd.astype(np.uint64)))
+                                & np.uint64(0xFFFFFFFF))
+                send = np.where(odd == 1, part[0], part[1])
+                keep = np.where(odd == 1, part[1], part[0])
+                recv = send[lane ^ 1]                      # quad_perm [1, 0, 3, 2]
+                v.append((keep + recv) & np.uint64(0xFFFFFFFF))
+            sw = _permlane16_swap(v[0], v[1])
+            for s in range(2):
+                row = 8 * i + 2 * s + p + 4 * (lane >> 5)
+                np.testing.assert_array_equal(sw[s], want[row, col16])
+                np.add.at(seen, (row, col16), 1)
+    assert (seen == 1).all()
