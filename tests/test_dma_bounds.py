@@ -369,3 +369,29 @@ def test_t256_int16_epilogue_lane_algebra():
                 np.testing.assert_array_equal(sw[s], want[row, col16])
                 np.add.at(seen, (row, col16), 1)
     assert (seen == 1).all()
+
+
+@pytest.mark.parametrize("mi,nj", [(8, 4), (4, 4), (4, 2)])
+def test_int8_store_pairs_cover_the_wave_tile(mi, nj):
+    """store_c of gemm_i8_t256_kernel (8 x 4 blocks per wave) and
+    gemm_i8_h128_kernel (4 x 4, 4 x 2): store e pairs blocks 2 jp and
+    2 jp + 1 of row block i through v_permlane16_swap and writes lane l to
+    row 16 i + r + 4 h + 8 (l >> 5), column 32 jp + (l & 31); every element
+    of the 16 mi x 16 nj wave tile must be written once, with its own value."""
+    rng = np.random.default_rng(mi * 10 + nj)
+    tile = rng.integers(0, 2**32, size=(16 * mi, 16 * nj), dtype=np.uint64)
+    lane = np.arange(64)
+    # element r of block (i, j) in lane l: row 16 i + 4 (l >> 4) + r, column 16 j + (l & 15)
+    acc = [[[tile[16 * i + 4 * (lane >> 4) + r, 16 * j + (lane & 15)] for r in range(4)] for j in range(nj)]
+           for i in range(mi)]
+    got = np.full(tile.shape, np.uint64(2**63))
+    count = np.zeros(tile.shape, int)
+    for e in range(mi * nj * 4):
+        h, jp, r, i = e & 1, (e >> 1) % (nj // 2), (e // nj) & 3, e // (4 * nj)
+        sw = _permlane16_swap(acc[i][2 * jp][r], acc[i][2 * jp + 1][r])
+        row = 16 * i + r + 4 * h + 8 * (lane >> 5)
+        col = 32 * jp + (lane & 31)
+        got[row, col] = sw[h]
+        np.add.at(count, (row, col), 1)
+    assert (count == 1).all()
+    np.testing.assert_array_equal(got, tile)
