@@ -1040,10 +1040,13 @@ namespace t256 {
 constexpr int BM = 256, TN = 256, WM = 128, WN = 64, MI = WM / 16, NJ = WN / 16;
 constexpr int NST = 4, A_BYTES = BM * BK, B_BYTES = BK * TN, SS = A_BYTES + B_BYTES;   // 32 KiB stages
 constexpr int DPS = 4;       // DMA instructions per wave per step: 2 A and 2 B blocks of 1 KiB
-constexpr int GROUP_M = 4;   // 1024 rows sharing a B column panel
 constexpr int NSTORE = MI * NJ * 4;
 using TB = h128::Tile<TN>;   // B stage [64 k][256 n], the h128 layout
 using h128::unroll_ic;
+// Row tiles per group sharing B column panels: 4 (1024 rows) for grids of
+// several rounds, 2 for one round (4096^3: 57.0 against 59.1 us with 4; the
+// MLP layer and 8192^3 are 1% slower with 2, and 3-5% with 1)
+inline int group_m(int rounds) { return rounds == 1 ? 2 : 4; }
 
 // EPI_I8: C[row][col] at C + row * ldc + col for row < mst, col < nst (MASK;
 // all rows and columns of the tile otherwise).  EPI_I16: the int16 limb
@@ -1053,14 +1056,15 @@ __global__ __launch_bounds__(THREADS, 1) void gemm_i8_t256_kernel(const int8_t *
                                                                   const int8_t *__restrict__ B,
                                                                   int32_t *__restrict__ C, int M, int N, int K,
                                                                   int tiles_m, int tiles_n, int ldc, int mst, int nst,
-                                                                  I16Epi e16) {
+                                                                  int group_m, I16Epi e16) {
     __shared__ __attribute__((aligned(1024))) int8_t smem[NST * SS];
 
+    // tiles taken in groups of group_m row tiles that share B column panels
     const int ntiles = tiles_m * tiles_n;
     const int pid = xcd_remap(blockIdx.x, ntiles);
-    const int in_group = GROUP_M * tiles_n;
-    const int first_m = (pid / in_group) * GROUP_M;
-    const int gsize = min(tiles_m - first_m, GROUP_M);
+    const int in_group = group_m * tiles_n;
+    const int first_m = (pid / in_group) * group_m;
+    const int gsize = min(tiles_m - first_m, group_m);
     const int m0 = (first_m + (pid % in_group) % gsize) * BM, n0 = ((pid % in_group) / gsize) * TN;
 
     const int tid = threadIdx.x, lane = tid & 63;
@@ -1399,13 +1403,13 @@ static void launch_i8_on_grid(const int8_t *A, const int8_t *B, int32_t *C, int 
                         t256n >= cus && 8 * t256n >= 7 * r256 * cus;
     const bool use128 = !use128n && !use256 && full128;
     if (use256) {
-        const int tm = M / t256::BM, tn = N / t256::TN;
+        const int tm = M / t256::BM, tn = N / t256::TN, gm = t256::group_m(r256);
         if (mask)
             hipLaunchKernelGGL(t256::gemm_i8_t256_kernel<true>, dim3(tm * tn), block, 0, s, A, B, C, M, N, K, tm, tn,
-                               ldc, mst, nst, I16Epi{});
+                               ldc, mst, nst, gm, I16Epi{});
         else
             hipLaunchKernelGGL(t256::gemm_i8_t256_kernel<false>, dim3(tm * tn), block, 0, s, A, B, C, M, N, K, tm, tn,
-                               ldc, mst, nst, I16Epi{});
+                               ldc, mst, nst, gm, I16Epi{});
     } else if (use128 || use128n) {
         const int tn = use128n ? N / 128 : N / BN, nt = tm128 * tn;
         // persistent workgroups: as many rounds of tiles as the CUs need, the
@@ -1477,7 +1481,7 @@ hipError_t launch_gemm_i8_i16epi(const int8_t *A2, const int8_t *B2, int M2, int
     const int cus = cu_count(), nt = tiles_m * tiles_n, rounds = (nt + cus - 1) / cus;
     if (full && nt >= cus && 8 * nt >= 7 * rounds * cus)
         hipLaunchKernelGGL((t256::gemm_i8_t256_kernel<false, EPI_I16>), dim3(nt), dim3(THREADS), 0, s, A2, B2,
-                           (int32_t *)nullptr, M2, N2, Kp, tiles_m, tiles_n, N2, M2, N2, e);
+                           (int32_t *)nullptr, M2, N2, Kp, tiles_m, tiles_n, N2, M2, N2, t256::group_m(rounds), e);
     else if (full)
         hipLaunchKernelGGL((gemm_i8_dma_kernel<EPI_I16, true>), dim3(tiles_m * tiles_n), dim3(THREADS), 0, s, A2, B2,
                            (int32_t *)nullptr, M2, N2, Kp, tiles_m, tiles_n, N2, M2, N2, e);
