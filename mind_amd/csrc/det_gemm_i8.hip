@@ -1326,11 +1326,21 @@ static int cu_count() {
 // every product, so C is unchanged.  One launch for both operands
 // (blockIdx.z), or for B alone when A already suits the full-tile kernels
 // (16-byte aligned, M % 128 == 0, K % 256 == 0: B' is [K][Np] and A is used
-// in place); each thread writes 16 bytes of a panel row.  Where the 20
-// dword-aligned bytes covering its 16 source bytes lie inside the source
-// buffer it reads those (one 16-byte and one 4-byte load) and funnel-shifts
-// them (v_alignbyte); at the two ends of the buffer it reads single bytes,
-// so no load leaves the source buffer.
+// in place); each thread writes 16 bytes of each of PAD_ROWS panel rows.  A wave's 64 output
+// chunks start at one byte offset sh (0..15) into the 16-byte grid of the
+// source, so each lane loads the aligned chunk under its own (lane 63 also the
+// one after the wave's span), takes its neighbour's from lane + 1 and
+// funnel-shifts the pair by sh.  Chunks that reach past either end of the
+// source buffer are read byte by byte, so no load leaves the buffer.
+constexpr int PAD_ROWS = 2;   // panel rows per thread and pass
+__device__ inline uint4 pad_load16(const int8_t *src, long long o, long long total) {
+    if (o >= 0 && o + 16 <= total) return *(const uint4 *)(src + o);
+    uint32_t w[4] = {0, 0, 0, 0};
+    for (int e = 0; e < 16; ++e)
+        if (o + e >= 0 && o + e < total) w[e >> 2] |= (uint32_t)(uint8_t)src[o + e] << (8 * (e & 3));
+    return make_uint4(w[0], w[1], w[2], w[3]);
+}
+
 __global__ __launch_bounds__(256) void pad_i8_kernel(const int8_t *__restrict__ A, const int8_t *__restrict__ B,
                                                      int M, int N, int K, int Mp, int Kp, int Np,
                                                      uint4 *__restrict__ Ap, uint4 *__restrict__ Bp, int zb) {
@@ -1339,26 +1349,57 @@ __global__ __launch_bounds__(256) void pad_i8_kernel(const int8_t *__restrict__ 
     uint4 *dst = is_b ? Bp : Ap;
     const int rows = is_b ? K : M, rows_out = is_b ? Kp : Mp, cols = is_b ? N : K, dcols = is_b ? Np : Kp;
     const long long total = (long long)rows * cols;
-    const int c0 = (blockIdx.x * 256 + threadIdx.x) * 16;
-    if (c0 >= dcols) return;
-    for (int row = blockIdx.y; row < rows_out; row += gridDim.y) {
-        uint32_t w[4] = {0, 0, 0, 0};
-        if (row < rows && c0 < cols) {
-            const long long p = (long long)row * cols + c0;
-            const uintptr_t base = (uintptr_t)src, at = base + (uintptr_t)p, a = at & ~(uintptr_t)3;
-            if (c0 + 16 <= cols && a >= base && a + 20 <= base + (uintptr_t)total) {
-                // one 16-byte load (dword-aligned) and the dword after it
-                const uint4 q = *(const uint4 *)a;
-                const uint32_t v[5] = {q.x, q.y, q.z, q.w, *(const uint32_t *)(a + 16)};
-                const uint32_t sh = (uint32_t)(at & 3);
+    const int lane = threadIdx.x & 63;
+    const int c0 = (blockIdx.x * 256 + threadIdx.x) * 16, cw = c0 - 16 * lane;   // cw: the wave's first column
+    if (cw >= dcols) return;   // uniform per wave
+    // PAD_ROWS rows per pass, their loads issued before any is used
+    for (int r0 = blockIdx.y * PAD_ROWS; r0 < rows_out; r0 += gridDim.y * PAD_ROWS) {
+        uint4 q[PAD_ROWS], q63[PAD_ROWS];
+        int sh[PAD_ROWS];
 #pragma unroll
-                for (int i = 0; i < 4; ++i) w[i] = __builtin_amdgcn_alignbyte(v[i + 1], v[i], sh);
-            } else {
-                const int nv = min(16, cols - c0);
-                for (int e = 0; e < nv; ++e) w[e >> 2] |= (uint32_t)(uint8_t)src[p + e] << (8 * (e & 3));
+        for (int r = 0; r < PAD_ROWS; ++r) {
+            const int row = r0 + r;
+            q[r] = q63[r] = make_uint4(0, 0, 0, 0);
+            sh[r] = 0;
+            if (row < rows && cw < cols) {
+                const long long p = (long long)row * cols + cw;
+                sh[r] = (int)(((uintptr_t)src + (uintptr_t)p) & 15);
+                const long long o = p - sh[r];   // lane 0's aligned chunk, relative to src
+                q[r] = pad_load16(src, o + 16 * lane, total);
+                if (lane == 63) q63[r] = pad_load16(src, o + 16 * 64, total);
             }
         }
-        dst[((long long)row * dcols + c0) >> 4] = make_uint4(w[0], w[1], w[2], w[3]);
+#pragma unroll
+        for (int r = 0; r < PAD_ROWS; ++r) {
+            const int row = r0 + r;
+            uint32_t w[4] = {0, 0, 0, 0};
+            if (row < rows && cw < cols) {   // uniform per wave: every lane takes part in the shuffles
+                uint4 n;
+                n.x = (uint32_t)__shfl_down((int)q[r].x, 1);
+                n.y = (uint32_t)__shfl_down((int)q[r].y, 1);
+                n.z = (uint32_t)__shfl_down((int)q[r].z, 1);
+                n.w = (uint32_t)__shfl_down((int)q[r].w, 1);
+                if (lane == 63) n = q63[r];
+                const uint32_t x[8] = {q[r].x, q[r].y, q[r].z, q[r].w, n.x, n.y, n.z, n.w};
+                const int s4 = sh[r] >> 2, sb = sh[r] & 3;
+                uint32_t y[5];
+#pragma unroll
+                for (int i = 0; i < 5; ++i)
+                    y[i] = s4 == 0 ? x[i] : s4 == 1 ? x[i + 1] : s4 == 2 ? x[i + 2] : x[i + 3];
+#pragma unroll
+                for (int i = 0; i < 4; ++i) w[i] = __builtin_amdgcn_alignbyte(y[i + 1], y[i], sb);
+                const int valid = cols - c0;   // bytes of this chunk inside the row
+                if (valid < 16) {
+#pragma unroll
+                    for (int i = 0; i < 4; ++i) {
+                        const int v = valid - 4 * i;
+                        w[i] = v <= 0 ? 0u : v >= 4 ? w[i] : w[i] & ((1u << (8 * v)) - 1u);
+                    }
+                }
+            }
+            if (row < rows_out && c0 < dcols)
+                dst[((long long)row * dcols + c0) >> 4] = make_uint4(w[0], w[1], w[2], w[3]);
+        }
     }
 }
 
@@ -1449,7 +1490,8 @@ hipError_t launch_gemm_i8(const int8_t *A, const int8_t *B, int32_t *C, int M, i
             // A already suits the full-tile kernels (a ragged or misaligned B,
             // e.g. N = 1000): repack only B into [K][Np] panels
             int8_t *Bp = (int8_t *)ws;
-            const dim3 pgrid((unsigned)((Np / 16 + 255) / 256), (unsigned)(K < 65535 ? K : 65535), 1);
+            const int ry = (K + PAD_ROWS - 1) / PAD_ROWS;
+            const dim3 pgrid((unsigned)((Np / 16 + 255) / 256), (unsigned)(ry < 65535 ? ry : 65535), 1);
             hipLaunchKernelGGL(pad_i8_kernel, pgrid, dim3(256), 0, s, A, B, M, N, K, M, K, Np, (uint4 *)nullptr,
                                (uint4 *)Bp, 0);
             launch_i8_on_grid(A, Bp, C, M, Np, K, N, M, N, s);
@@ -1458,7 +1500,8 @@ hipError_t launch_gemm_i8(const int8_t *A, const int8_t *B, int32_t *C, int M, i
         int8_t *Ap = (int8_t *)ws;
         int8_t *Bp = Ap + (size_t)Mp * Kp;
         const int wide = Kp > Np ? Kp : Np, tall = Mp > Kp ? Mp : Kp;
-        const dim3 pgrid((unsigned)((wide / 16 + 255) / 256), (unsigned)(tall < 65535 ? tall : 65535), 2);
+        const int ry = (tall + PAD_ROWS - 1) / PAD_ROWS;
+        const dim3 pgrid((unsigned)((wide / 16 + 255) / 256), (unsigned)(ry < 65535 ? ry : 65535), 2);
         hipLaunchKernelGGL(pad_i8_kernel, pgrid, dim3(256), 0, s, A, B, M, N, K, Mp, Kp, Np, (uint4 *)Ap,
                            (uint4 *)Bp, 1);
         launch_i8_on_grid(Ap, Bp, C, Mp, Np, Kp, N, M, N, s);

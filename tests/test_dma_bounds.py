@@ -395,3 +395,55 @@ def test_int8_store_pairs_cover_the_wave_tile(mi, nj):
         np.add.at(count, (row, col), 1)
     assert (count == 1).all()
     np.testing.assert_array_equal(got, tile)
+
+
+def _pad_model(src, base_mis, rows, cols, rows_out, dcols):
+    """pad_i8_kernel's lane algebra for one operand: per wave of 64 chunks,
+    aligned 16-byte loads (byte loads where a chunk leaves the buffer), the
+    lane + 1 exchange, the funnel shift by the row's offset into the 16-byte
+    grid and the tail mask.  Returns the panel and asserts every vector load
+    is aligned and inside the buffer."""
+    total = rows * cols
+    buf = np.frombuffer(src.tobytes(), np.uint8)
+
+    def load16(o):
+        if o >= 0 and o + 16 <= total:
+            assert (base_mis + o) % 16 == 0
+            return buf[o:o + 16].copy()
+        out = np.zeros(16, np.uint8)
+        for e in range(16):
+            if 0 <= o + e < total:
+                out[e] = buf[o + e]
+        return out
+
+    panel = np.zeros((rows_out, dcols), np.uint8)
+    for cw in range(0, dcols, 1024):
+        for row in range(rows_out):
+            if row >= rows or cw >= cols:
+                continue
+            p = row * cols + cw
+            sh = (base_mis + p) % 16
+            o = p - sh
+            q = [load16(o + 16 * lane) for lane in range(64)]
+            nxt = q[1:] + [load16(o + 16 * 64)]
+            for lane in range(64):
+                c0 = cw + 16 * lane
+                if c0 >= dcols:
+                    continue
+                w = np.concatenate([q[lane], nxt[lane]])[sh:sh + 16]
+                valid = cols - c0
+                if valid < 16:
+                    w[max(valid, 0):] = 0
+                panel[row, c0:c0 + 16] = w
+    return panel
+
+
+@pytest.mark.parametrize("rows,cols,mis", [(5, 4095, 3), (3, 1000, 0), (4, 17, 13), (2, 2100, 7), (3, 1, 1),
+                                           (6, 300, 15)])
+def test_pad_kernel_lane_algebra(rows, cols, mis):
+    rng = np.random.default_rng(rows * 131 + cols + mis)
+    src = rng.integers(-128, 128, (rows, cols), dtype=np.int8)
+    rows_out, dcols = -(-rows // 256) * 256, -(-cols // 256) * 256
+    want = np.zeros((rows_out, dcols), np.uint8)
+    want[:rows, :cols] = src.view(np.uint8)
+    assert np.array_equal(_pad_model(src, mis, rows, cols, rows_out, dcols), want)
