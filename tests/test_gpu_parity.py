@@ -676,7 +676,9 @@ def test_gemm_i8_shapes(m, k, n):
 # and two tiles, K of 1, 2, 3 and 128 steps of 128 (the 3-stage loop's
 # remainders), K not a multiple of 256.
 # 128-row tiles: 128 x 128 tiles for grids of at most 256 of them (all but the
-# last two), 128 x 256 tiles in one round (the last two: 256 tiles each)
+# last two), 128 x 256 tiles in one round (the last two: 256 tiles each).
+# 3, 5 and 9 row tiles (M = 384, 640, 1152) end in a partial group of the
+# 4 row tiles that one-round 128 x 128 grids take together.
 H128_SHAPES = [(128, 128, 256), (128, 256, 256), (256, 256, 256), (384, 384, 512), (1152, 640, 768),
                (128, 16384, 256), (640, 1280, 1536), (2048, 2048, 2048), (128, 128, 128), (384, 1152, 640),
                (2048, 1024, 4096), (4096, 256, 2048)]
