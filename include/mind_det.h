@@ -227,7 +227,9 @@ int64_t det_fft_workspace_bytes(int64_t logn, int64_t batch);
  * when K or N is not a multiple of 16: its operands are then repacked into
  * aligned zero-padded panels of Mp*Kp + Kp*Np bytes (M, K, N rounded up to
  * 256).  int8 operands that are not 16-byte aligned are repacked the same
- * way when the workspace given holds that size.  For int8 the workspace is
+ * way when the workspace given holds that size, and so are aligned shapes
+ * that no 128-row kernel takes and whose 256 x 256 tiles would not fill one
+ * round of the GPU (e.g. 1008^3), where the padded panels run faster.  For int8 the workspace is
  * optional: without it such operands run a slower byte-load kernel;
  * det_matmul_ws_dev rejects a short workspace only for int16 / Q16. */
 int64_t det_workspace_bytes(int64_t op, int64_t m, int64_t k, int64_t n);

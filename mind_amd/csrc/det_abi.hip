@@ -178,8 +178,9 @@ int64_t gemm_dev(Op op, const void *A, const void *B, void *C, int64_t m, int64_
 bool aligned16(const void *a, const void *b) { return (((uintptr_t)a | (uintptr_t)b) & 15) == 0; }
 
 // Workspace bytes of one GEMM.  int8 needs one only for operands off the
-// 16-byte grid (repacked into padded panels), which depends on the operand
-// addresses; NULL operands are taken as aligned.
+// 16-byte grid, or small grids the edge kernel would underfill (repacked
+// into padded panels), which depends on the operand addresses; NULL operands
+// are taken as aligned.
 size_t ws_need(Op op, int64_t m, int64_t k, int64_t n, const void *A = nullptr, const void *B = nullptr) {
     if (k == 0) return 0;
     if (op == Op::I8) return det::i8_workspace_bytes((int)m, (int)n, (int)k, aligned16(A, B));

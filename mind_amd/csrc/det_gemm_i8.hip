@@ -1411,10 +1411,26 @@ static bool i8_fast(const int8_t *A, const int8_t *B, int M, int N, int K) {
 // Workspace of the repack path: 0 when the operands go to the kernels as
 // they are (16-byte grid, or panels beyond the buffer fast paths' 2 GiB).
 static inline size_t round256(size_t x) { return (x + 255) / 256 * 256; }
+// Shapes on the 16-byte grid that no 128-row kernel takes go to the
+// 256 x 256 edge kernel; when its grid would not fill one round of the chip
+// (1008^3: 16 tiles, 17.2 us) the padded panels are faster (1024^3 panels on
+// 128 x 128 tiles: 6 us + the repack), so they are repacked as well.
+static bool i8_edge_underfills(int M, int N, int K) {
+    const int cus = cu_count();
+    const bool full128 = M % 128 == 0 && N % 256 == 0 && K % 128 == 0;
+    const bool one128 = M % 128 == 0 && N % 128 == 0 && K % 128 == 0 && (long long)(M / 128) * (N / 128) <= cus;
+    // ... and only when the panels fit one round of 128 x 128 tiles (3000 x
+    // 3008^2 on its 144 edge tiles: 36.6 us; on 3072-wide panels, two rounds
+    // of persistent 128 x 256 tiles: 54.6 us)
+    return !full128 && !one128 && (long long)((M + 255) / 256) * ((N + 255) / 256) < cus &&
+           (long long)(round256(M) / 128) * (long long)(round256(N) / 128) <= cus;
+}
+
 size_t i8_workspace_bytes(int M, int N, int K, bool aligned) {
     const size_t Mp = round256(M), Kp = round256(K), Np = round256(N);
     const bool grid16 = K % 16 == 0 && N % 16 == 0 && aligned;
-    if (grid16 || K == 0 || Mp * Kp >= 0x80000000ull || Kp * Np >= 0x80000000ull) return 0;
+    if (K == 0 || Mp * Kp >= 0x80000000ull || Kp * Np >= 0x80000000ull) return 0;
+    if (grid16 && !i8_edge_underfills(M, N, K)) return 0;
     return Mp * Kp + Kp * Np;
 }
 
@@ -1482,7 +1498,7 @@ hipError_t launch_gemm_i8(const int8_t *A, const int8_t *B, int32_t *C, int M, i
     using namespace i8g;
     const bool aligned = (((uintptr_t)A & 15) == 0) && (((uintptr_t)B & 15) == 0);
     const size_t pad = i8_workspace_bytes(M, N, K, aligned);
-    if (i8_fast(A, B, M, N, K)) {
+    if (i8_fast(A, B, M, N, K) && !(pad && ws)) {
         launch_i8_on_grid(A, B, C, M, N, K, N, M, N, s);
     } else if (pad && ws) {
         const int Mp = (int)round256(M), Kp = (int)round256(K), Np = (int)round256(N);

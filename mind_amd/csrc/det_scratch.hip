@@ -69,9 +69,10 @@ extern "C" int64_t det_matmul_scratch_dev(int64_t op, const void *a, const void 
         return 0;
     }
     if (op == DET_OP_I8) {
-        // int8 uses the scratch only for operands off the 16-byte grid (the
-        // repack into padded panels); beyond the scratch it takes the
-        // byte-load kernel, which needs no workspace
+        // int8 uses the scratch only to repack operands into padded panels
+        // (off the 16-byte grid, or small grids the edge kernel would
+        // underfill); beyond the scratch it takes the byte-load or edge
+        // kernel, which need no workspace
         const bool aligned = (((uintptr_t)a | (uintptr_t)b) & 15) == 0;
         const size_t need8 = det::i8_workspace_bytes(M, N, K, aligned);
         void *ws8 = nullptr;

@@ -659,8 +659,11 @@ def test_host_batched_gemv_orders_itself_after_device_arena_users():
 
 # ------------------------------------------------------------------ int8 shapes
 
+# The last three are on the 16-byte grid but off the 128-row kernels with an
+# edge grid under one round: repacked into panels (both operands, or B only).
 I8_SHAPES = [(1, 1, 1), (1, 64, 1), (3, 5, 7), (16, 16, 16), (17, 33, 65), (64, 64, 64), (255, 257, 129),
-             (256, 256, 256), (300, 1000, 77), (513, 96, 260), (100, 4096, 8), (8, 4096, 300), (1000, 17, 999)]
+             (256, 256, 256), (300, 1000, 77), (513, 96, 260), (100, 4096, 8), (8, 4096, 300), (1000, 17, 999),
+             (1008, 1008, 1008), (496, 512, 496), (1024, 1024, 1008)]
 
 
 @pytest.mark.parametrize("m,k,n", I8_SHAPES, ids=[f"{m}x{k}x{n}" for m, k, n in I8_SHAPES])
