@@ -107,8 +107,12 @@ int64_t __mind_blas_dot_l1_f32(int64_t a, int64_t b, int64_t len);
  * src/mlir/lowering.rs:6219-6401 (emit_vec_dot_metric_f32, L1). */
 int64_t __mind_blas_dot_l1_f32_v(int64_t a, int64_t b, int64_t len);
 /* Replaces __mind_blas_dot_linf_f32(a, b, len): the largest |a[i] - b[i]|
- * from 0.0f, a NaN difference skipped as by the reference's `d > m` test
- * (runtime-support/mind_intrinsics.c:1353-1411; arity type_checker:2258). */
+ * from 0.0f, a NaN difference skipped as by the reference's scalar path and
+ * its `d > m` test (runtime-support/mind_intrinsics.c:1355-1365; arity
+ * type_checker:2258).  The reference's AVX2 path (:1367-1394, chosen at load
+ * time on x86 hosts with AVX2) differs on NaN only: it returns NaN when a NaN
+ * difference is the last one its lane 7 sees in the full 8-blocks (vmaxps
+ * keeps its second operand). */
 int64_t __mind_blas_dot_linf_f32(int64_t a, int64_t b, int64_t len);
 /* Replaces __mind_blas_dot_linf_f32_v (arith.maximumf, lowering.rs:
  * 6219-6401): the same maximum, or a NaN (0x7fc00000) once any difference is
@@ -228,8 +232,10 @@ int64_t det_fft_workspace_bytes(int64_t logn, int64_t batch);
  * aligned zero-padded panels of Mp*Kp + Kp*Np bytes (M, K, N rounded up to
  * 256).  int8 operands that are not 16-byte aligned are repacked the same
  * way when the workspace given holds that size, and so are aligned shapes
- * that no 128-row kernel takes and whose 256 x 256 tiles would not fill one
- * round of the GPU (e.g. 1008^3), where the padded panels run faster.  For int8 the workspace is
+ * of at least 256 rows and columns that no 128-row kernel takes, whose
+ * 256 x 256 tiles would not fill one round of the GPU and whose padding to
+ * multiples of 256 adds at most 1/8 per dimension (e.g. 1008^3), where the
+ * padded panels run faster.  For int8 the workspace is
  * optional: without it such operands run a slower byte-load kernel;
  * det_matmul_ws_dev rejects a short workspace only for int16 / Q16. */
 int64_t det_workspace_bytes(int64_t op, int64_t m, int64_t k, int64_t n);
@@ -240,10 +246,12 @@ int64_t det_matmul_ws_dev(int64_t op, const void *a, const void *b, int32_t *c, 
  * memory (code under HIP graph capture, tight serving loops, harnesses that
  * forbid hipMalloc): det_matmul_ws_dev with the workspace taken from a fixed
  * per-device array of DET_SCRATCH_BYTES compiled into the library, so the
- * call allocates nothing.  A shape whose det_workspace_bytes exceeds it
- * returns DET_ERR_ARG (32 MiB covers Q16 up to 1024^3 and int16 up to
- * 2048^3).  Every call on one GPU shares that GPU's array: calls that
- * overlap on one GPU (two streams, two host threads) race; order them. */
+ * call allocates nothing and never synchronises.  An int16 or Q16 shape
+ * whose det_workspace_bytes exceeds it returns DET_ERR_ARG (32 MiB covers Q16
+ * up to 1024^3 and int16 up to 2048^3); an int8 shape whose padded panels
+ * exceed it runs the kernels that need no workspace instead.  Every call on
+ * one GPU shares that GPU's array: calls that overlap on one GPU (two
+ * streams, two host threads) race; order them. */
 #define DET_SCRATCH_BYTES (32LL << 20)
 int64_t det_matmul_scratch_dev(int64_t op, const void *a, const void *b, int32_t *c, int64_t m, int64_t k, int64_t n,
                                void *stream);

@@ -1414,9 +1414,16 @@ static inline size_t round256(size_t x) { return (x + 255) / 256 * 256; }
 // Shapes on the 16-byte grid that no 128-row kernel takes go to the
 // 256 x 256 edge kernel; when its grid would not fill one round of the chip
 // (1008^3: 16 tiles, 17.2 us) the padded panels are faster (1024^3 panels on
-// 128 x 128 tiles: 6 us + the repack), so they are repacked as well.
+// 128 x 128 tiles: 6 us + the repack), so they are repacked as well -- but
+// only where the padding is small: M and N at least 256 and no dimension
+// grown by more than 1/8 (496 -> 512, 1008 -> 1024, 2000 -> 2048), so small
+// shapes such as the reference sweep's 16^3 .. 256^3 stay on the edge kernel
+// with no workspace, and the panels stay within 27/64 more bytes than the
+// operands.
+static bool i8_pad_small(int d) { return round256(d) * 8 <= (size_t)d * 9; }
 static bool i8_edge_underfills(int M, int N, int K) {
     const int cus = cu_count();
+    if (M < 256 || N < 256 || !i8_pad_small(M) || !i8_pad_small(N) || !i8_pad_small(K)) return false;
     const bool full128 = M % 128 == 0 && N % 256 == 0 && K % 128 == 0;
     const bool one128 = M % 128 == 0 && N % 128 == 0 && K % 128 == 0 && (long long)(M / 128) * (N / 128) <= cus;
     // ... and only when the panels fit one round of 128 x 128 tiles (3000 x

@@ -15,10 +15,11 @@ namespace det {
 constexpr int MAX_CS = 16;
 
 // C[M,N] (i32) = A[M,K] (i8) * B[K,N] (i8).  Shapes off the 16-byte grid (K
-// or N not a multiple of 16, operands not 16-byte aligned) repack the
-// operands into `ws`, which must then hold i8_workspace_bytes(M, N, K,
-// aligned) bytes (0 on the grid; with ws == NULL they take the byte-load
-// kernel instead).
+// or N not a multiple of 16, operands not 16-byte aligned), and the small
+// on-grid shapes the edge kernel would underfill (i8_edge_underfills),
+// repack the operands into `ws`, which must then hold i8_workspace_bytes(M,
+// N, K, aligned) bytes (0 for every other shape; with ws == NULL they take
+// the byte-load or edge kernel instead).
 size_t i8_workspace_bytes(int M, int N, int K, bool aligned);
 hipError_t launch_gemm_i8(const int8_t *A, const int8_t *B, int32_t *C, int M, int N, int K, void *ws,
                           hipStream_t s);

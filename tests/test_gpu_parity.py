@@ -253,8 +253,9 @@ F32_METRIC_SYMS = [("__mind_blas_dot_l1_f32", O.F32_L1), ("__mind_blas_dot_l1_f3
 
 def test_f32_metric_reference_vectors():
     """Every symbol on the committed outputs of the reference's own L1 / L-inf
-    (tests/golden/dot_f32_metric_ref.json; the vector twins equal them except
-    L-inf_v on NaN, which follows the oracle)."""
+    (tests/golden/dot_f32_metric_ref.json, the scalar dispatch path's
+    outputs; the vector twins equal them except L-inf_v on NaN, which
+    follows the oracle)."""
     import importlib.util
     spec = importlib.util.spec_from_file_location("mk_f32_metric", os.path.join(GOLD, "make_ref_f32_metric_vectors.py"))
     mod = importlib.util.module_from_spec(spec)
@@ -262,7 +263,7 @@ def test_f32_metric_reference_vectors():
     cases = json.load(open(os.path.join(GOLD, "dot_f32_metric_ref.json")))["cases"]
     with np.errstate(all="ignore"):
         for c in cases:
-            a, b = mod.inputs(c["family"], c["seed"], c["len"])
+            a, b = mod.inputs(c["family"], c["seed"], c["len"], c.get("pos"))
             n = c["len"]
             for sym, op in F32_METRIC_SYMS:
                 note(f"{sym} {c['family']} n={n}")
@@ -664,6 +665,19 @@ def test_host_batched_gemv_orders_itself_after_device_arena_users():
 I8_SHAPES = [(1, 1, 1), (1, 64, 1), (3, 5, 7), (16, 16, 16), (17, 33, 65), (64, 64, 64), (255, 257, 129),
              (256, 256, 256), (300, 1000, 77), (513, 96, 260), (100, 4096, 8), (8, 4096, 300), (1000, 17, 999),
              (1008, 1008, 1008), (496, 512, 496), (1024, 1024, 1008)]
+
+
+def test_gemm_i8_repack_rule_leaves_small_grids_alone():
+    """Aligned on-grid int8 shapes take a workspace (padded panels) only when
+    M, N >= 256 and padding to multiples of 256 adds at most 1/8 per
+    dimension: the reference sweep's small cubes and long skinny shapes need
+    none (m, k, n order as det_workspace_bytes takes them)."""
+    L = M.lib()
+    for m, k, n in [(16, 16, 16), (64, 64, 64), (128, 128, 128), (240, 240, 240), (16, 4194304, 16),
+                    (304, 304, 304), (1008, 96, 1008)]:
+        assert L.det_workspace_bytes(M.DET_OP_I8, m, k, n) == 0, (m, k, n)
+    for m, k, n in [(1008, 1008, 1008), (496, 512, 496), (2000, 2000, 2000)]:
+        assert L.det_workspace_bytes(M.DET_OP_I8, m, k, n) > 0, (m, k, n)
 
 
 @pytest.mark.parametrize("m,k,n", I8_SHAPES, ids=[f"{m}x{k}x{n}" for m, k, n in I8_SHAPES])

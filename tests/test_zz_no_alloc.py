@@ -2,8 +2,13 @@
 det_matmul_ws_dev (the existing workspace entry point) through the C ABI:
 bit-identical outputs on two calls in a row, the second smaller, for the
 int16 and Q16 limb GEMMs (which always use the scratch) and int8 (which uses
-it only to repack operands off the 16-byte grid); a limb-GEMM shape beyond
-the fixed scratch is rejected before any launch."""
+it only to repack operands into padded panels); a limb-GEMM shape beyond
+the fixed scratch is rejected before any launch.  The property the entry
+point exists for is checked directly: after one warm-up call per op, further
+calls leave the device's free memory unchanged, and one call per op captured
+into a HIP graph (capture fails on hipMalloc or any synchronising call)
+replays three times, with eager work and synchronisations between replays,
+each time equal to the eager result."""
 import ctypes
 
 import numpy as np
@@ -99,4 +104,85 @@ def test_scratch_entry_rejects_oversized_and_handles_k0():
     M.check(f(M.DET_OP_Q16, c.ptr, c.ptr, dc.ptr, 8, 0, 8, s.ptr))   # K == 0: zeros
     s.sync()
     assert not dc.to_array(np.int32, (8, 8)).any()
+    s.destroy()
+
+
+def _hip():
+    """The HIP runtime the library is linked against (already loaded)."""
+    H = ctypes.CDLL("libamdhip64.so")
+    vp, sz = ctypes.c_void_p, ctypes.c_size_t
+    H.hipMemGetInfo.argtypes = [ctypes.POINTER(sz), ctypes.POINTER(sz)]
+    H.hipStreamBeginCapture.argtypes = [vp, ctypes.c_int]
+    H.hipStreamEndCapture.argtypes = [vp, ctypes.POINTER(vp)]
+    H.hipGraphInstantiateWithFlags.argtypes = [ctypes.POINTER(vp), vp, ctypes.c_ulonglong]
+    H.hipGraphLaunch.argtypes = [vp, vp]
+    H.hipGraphExecDestroy.argtypes = [vp]
+    H.hipGraphDestroy.argtypes = [vp]
+    for fn in ("hipMemGetInfo", "hipStreamBeginCapture", "hipStreamEndCapture", "hipGraphInstantiateWithFlags",
+               "hipGraphLaunch", "hipGraphExecDestroy", "hipGraphDestroy"):
+        getattr(H, fn).restype = ctypes.c_int
+    return H
+
+
+def _free_bytes(H):
+    free, total = ctypes.c_size_t(0), ctypes.c_size_t(0)
+    assert H.hipMemGetInfo(ctypes.byref(free), ctypes.byref(total)) == 0
+    return free.value
+
+
+def test_scratch_entry_allocates_nothing_and_captures_into_a_graph():
+    L, f = _bind()
+    H = _hip()
+    s = M.Stream()
+    # one shape per op within the scratch; the int8 one off the 16-byte grid,
+    # so its panels come from the scratch
+    cases = [(M.DET_OP_Q16, 256, 512, 192, 0x5D1), (M.DET_OP_I16, 320, 1088, 272, 0x5D2),
+             (M.DET_OP_I8, 300, 1000, 77, 0x5D3)]
+    bufs = []
+    for op, m, k, n, seed in cases:
+        a, b, want = _inputs(op, m, k, n, seed)
+        print(f"[no-alloc graph] op={op} {m}x{k}x{n} seed={seed:#x}", flush=True)
+        bufs.append((op, m, k, n, M.DeviceBuffer.from_array(a), M.DeviceBuffer.from_array(b),
+                     M.DeviceBuffer(m * n * 4), M.DeviceBuffer(m * n * 4), want.reshape(m, n)))
+    # warm-up: the first call per device looks the scratch up
+    for op, m, k, n, da, db, c_eager, c_graph, want in bufs:
+        M.check(f(op, da.ptr, db.ptr, c_eager.ptr, m, k, n, s.ptr))
+    s.sync()
+    free0 = _free_bytes(H)
+    for _ in range(3):
+        for op, m, k, n, da, db, c_eager, c_graph, want in bufs:
+            c_eager.fill(0xA5)
+            M.check(f(op, da.ptr, db.ptr, c_eager.ptr, m, k, n, s.ptr))
+        s.sync()
+        for op, m, k, n, da, db, c_eager, c_graph, want in bufs:
+            np.testing.assert_array_equal(c_eager.to_array(np.int32, (m, n)), want)
+    assert _free_bytes(H) == free0, "a warmed-up det_matmul_scratch_dev call changed free device memory"
+
+    # capture one call per op on this stream (thread-local mode: a hipMalloc
+    # or a synchronising call inside the capture fails it)
+    graph, exe = ctypes.c_void_p(0), ctypes.c_void_p(0)
+    assert H.hipStreamBeginCapture(s.ptr, 1) == 0
+    rcs = [f(op, da.ptr, db.ptr, c_graph.ptr, m, k, n, s.ptr) for op, m, k, n, da, db, c_eager, c_graph, want in bufs]
+    assert H.hipStreamEndCapture(s.ptr, ctypes.byref(graph)) == 0
+    assert rcs == [0] * len(bufs), (rcs, M.last_error())
+    assert H.hipGraphInstantiateWithFlags(ctypes.byref(exe), graph, 0) == 0
+    try:
+        for replay in range(3):
+            for op, m, k, n, da, db, c_eager, c_graph, want in bufs:
+                c_graph.fill(0x5A + replay)
+            # eager work on the same scratch between replays
+            op, m, k, n, da, db, c_eager, c_graph, want = bufs[replay % len(bufs)]
+            M.check(f(op, da.ptr, db.ptr, c_eager.ptr, m, k, n, s.ptr))
+            s.sync()
+            assert H.hipGraphLaunch(exe, s.ptr) == 0
+            s.sync()
+            for op, m, k, n, da, db, c_eager, c_graph, want in bufs:
+                np.testing.assert_array_equal(c_graph.to_array(np.int32, (m, n)), want)
+                np.testing.assert_array_equal(c_graph.to_array(np.int32, (m, n)), c_eager.to_array(np.int32, (m, n)))
+    finally:
+        H.hipGraphExecDestroy(exe)
+        H.hipGraphDestroy(graph)
+    for op, m, k, n, da, db, c_eager, c_graph, want in bufs:
+        for buf in (da, db, c_eager, c_graph):
+            buf.free()
     s.destroy()
