@@ -20,7 +20,13 @@ clock over the same region.
 Every timed output is checked bit-exact against the CPU oracle (sampled rows
 at these sizes) before its number is reported.
 
+By default the run also times the reference benches' own sweep shapes
+(host-pointer call and device-resident, under "reference_sweeps") and the
+end-to-end host-pointer calls of the headline shapes (PCIe included, under
+"host_abi"); --no-host-abi skips both.
+
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--settle S] [--only q16_1024,...] [--vendor-ref]
+                       [--no-host-abi]
 """
 from __future__ import annotations
 
@@ -50,7 +56,7 @@ def log(msg: str) -> None:
 SETTLE_S = 0.5                   # back-to-back running before each timed region (--settle)
 
 
-def time_steps(launch, steps: int, warmup: int, stream) -> tuple[float, float]:
+def time_steps(launch, steps: int, warmup: int, stream, settle: float | None = None) -> tuple[float, float]:
     """Return (event ms per step, wall ms per step) over exactly `steps` launches.
 
     After the `warmup` launches the workload keeps running back to back for
@@ -62,7 +68,7 @@ def time_steps(launch, steps: int, warmup: int, stream) -> tuple[float, float]:
     for _ in range(warmup):
         launch()
     M.check(M.lib().det_device_sync())
-    t_end = time.perf_counter() + SETTLE_S
+    t_end = time.perf_counter() + (SETTLE_S if settle is None else settle)
     while time.perf_counter() < t_end:
         for _ in range(8):
             launch()
@@ -154,9 +160,13 @@ def gemv_workload(m: int, k: int, nb: int, steps: int, warmup: int, stream, seed
     dy = M.DeviceBuffer(m * nb * 4)
     dy.fill(0xA5)
     sp = stream.ptr
+    # the caller's workspace (det_gemv_q16_ws_dev), as the GEMMs take theirs
+    # through det_matmul_ws_dev: no arena event ordering between calls
+    ws_bytes = L.det_gemv_workspace_bytes(m, k, nb)
+    ws = M.DeviceBuffer(ws_bytes) if ws_bytes else None
 
     def launch():
-        M.check(L.det_gemv_q16_dev(dw.ptr, dx.ptr, dy.ptr, m, k, nb, sp))
+        M.check(L.det_gemv_q16_ws_dev(dw.ptr, dx.ptr, dy.ptr, m, k, nb, ws.ptr if ws else None, ws_bytes, sp))
 
     ev, wall = time_steps(launch, steps, warmup, stream)
     Y = dy.to_array(np.int32, (nb, m))
@@ -167,8 +177,9 @@ def gemv_workload(m: int, k: int, nb: int, steps: int, warmup: int, stream, seed
     def verify(O):
         return bool(np.array_equal(got, O.gemv_q16_batched(Wr, X, len(rows), k, nb)))
 
-    for buf in (dw, dx, dy):
-        buf.free()
+    for buf in (dw, dx, dy, ws):
+        if buf is not None:
+            buf.free()
     nbytes = 4.0 * m * k + 4.0 * k * nb + 4.0 * m * nb
     out = {"ms": ev, "wall_ms": wall, "bytes": nbytes, "verify": verify, "checked_rows": len(rows)}
     if keep_output:
@@ -289,6 +300,13 @@ def host_abi_timings(reps: int = 3) -> dict:
     res["gemmi8_4096"] = {"ms": round(ms, 3), "tops": round(2.0 * m * n * k / ms / 1e9, 1),
                           "pcie_bytes": a.nbytes + b.nbytes + c.nbytes}
     del a, b, c
+    m = k = n = 1024
+    a, b = M.gen_q16_sat(SEED ^ 0x1016, m * k, k * n, 13)
+    c = np.empty(m * n, np.int32)
+    ms = timed(lambda: L.gemmqmm(a.ctypes.data, b.ctypes.data, c.ctypes.data, m, k, n))
+    res["gemmqmm_1024"] = {"ms": round(ms, 3), "q16_tops": round(2.0 * m * n * k / ms / 1e9, 2),
+                           "pcie_bytes": a.nbytes + b.nbytes + c.nbytes}
+    del a, b, c
     M_, K_ = 16384, 16384
     W, x = M.gen_q16(SEED ^ 0x6E3F, M_ * K_, K_, 15)
     y = np.empty(M_, np.int32)
@@ -314,6 +332,99 @@ def host_abi_timings(reps: int = 3) -> dict:
     res["note"] = ("median of %d synchronous calls after one warm-up; pageable host buffers; times include the "
                    "host-to-device and device-to-host copies" % reps)
     return res
+
+
+# The reference benches' own sweeps: benches/det_matmul_i8.rs:86 and
+# det_matmul_q16.rs:82 (n^3, n = 16 .. 512), det_matmul_i16.rs:77 (int16 GEMV
+# n x n, n = 64, 256, 512), det_gemv_q16_mt.rs:62 (the GEMV shapes including
+# the 11922 x 384 routing shape) and its 512 x 130 anchor (:76-78).  Seeds as
+# the benches draw them: the anchor shape 0xDEADBEEF, the others
+# 0xDEADBEEF00000000 ^ n (GEMV: ^ (m << 20 ^ k)).
+REF_SWEEPS = ([("gemmi8", n) for n in (16, 64, 128, 256, 512)] +
+              [("gemmqmm", n) for n in (16, 64, 128, 256, 512)] +
+              [("mmi16", n) for n in (64, 256, 512)] +
+              [("gemvq", mk) for mk in ((64, 64), (128, 96), (256, 130), (11922, 384), (512, 130))])
+
+
+def reference_sweeps(stream, steps: int) -> dict:
+    """Each shape of the reference benches' sweeps three ways: the host-pointer
+    call of the symbol its bench dlsyms (gemmi8, the fused Q16 GEMM under its
+    harness name gemmqmm, mmi16, gemvq), timed as its report_gmacs does
+    (median of 64 calls after 8 warm-up calls, PCIe copies included:
+    benches/det_matmul_i8.rs:363-408); the same work on device-resident
+    operands (HIP events over `steps` calls after a 0.1 s settle); and both
+    outputs kept for the exactness check against the oracle."""
+    L = M.lib()
+    sp = stream.ptr
+    out = {}
+    for sym, shape in REF_SWEEPS:
+        if sym == "gemvq":
+            m, k = shape
+            seed = 0xDEADBEEF if (m, k) == (512, 130) else 0xDEADBEEF00000000 ^ ((m << 20) ^ k)
+            W, x = M.gen_q16(seed, m * k, k)
+            y = np.empty(m, np.int32)
+            host = lambda: L.gemvq(W.ctypes.data, x.ctypes.data, y.ctypes.data, m, k)
+            dw, dx, dy = M.DeviceBuffer.from_array(W), M.DeviceBuffer.from_array(x), M.DeviceBuffer(m * 4)
+            dev = lambda: M.check(L.det_gemv_q16_ws_dev(dw.ptr, dx.ptr, dy.ptr, m, k, 1, None, 0, sp))
+            macs, name, ins, outs = m * k, f"gemvq_{m}x{k}", (W, x), (y, dy, (m,))
+        elif sym == "mmi16":
+            n = shape
+            W, x = M.gen_i16(0xDEADBEEF if n == 256 else 0xDEADBEEF00000000 ^ n, n * n, n)
+            y = np.empty(n, np.int32)
+            host = lambda: L.mmi16(W.ctypes.data, x.ctypes.data, y.ctypes.data, n, n)
+            dw, dx, dy = M.DeviceBuffer.from_array(W), M.DeviceBuffer.from_array(x), M.DeviceBuffer(n * 4)
+            dev = lambda: M.check(L.det_gemv_i16_dev(dw.ptr, dx.ptr, dy.ptr, n, n, sp))
+            macs, name, ins, outs = n * n, f"mmi16_{n}", (W, x), (y, dy, (n,))
+        else:
+            n = shape
+            seed = 0xDEADBEEF if n == 64 else 0xDEADBEEF00000000 ^ n
+            a, b = M.gen_i8(seed, n * n, n * n) if sym == "gemmi8" else M.gen_q16(seed, n * n, n * n)
+            op = M.DET_OP_I8 if sym == "gemmi8" else M.DET_OP_Q16
+            y = np.empty(n * n, np.int32)
+            host = lambda: getattr(L, sym)(a.ctypes.data, b.ctypes.data, y.ctypes.data, n, n, n)
+            dw, dx, dy = M.DeviceBuffer.from_array(a), M.DeviceBuffer.from_array(b), M.DeviceBuffer(n * n * 4)
+            wsb = L.det_workspace_bytes(op, n, n, n)
+            ws = M.DeviceBuffer(wsb) if wsb else None
+            dev = lambda: M.check(L.det_matmul_ws_dev(op, dw.ptr, dx.ptr, dy.ptr, n, n, n, ws.ptr if ws else None,
+                                                      wsb, sp))
+            macs, name, ins, outs = n ** 3, f"{sym}_{n}", (a, b), (y, dy, (n * n,))
+        for _ in range(8):
+            M.check(host())
+        samples = []
+        for _ in range(64):
+            t0 = time.perf_counter()
+            rc = host()
+            samples.append(time.perf_counter() - t0)
+            M.check(rc)
+        host_s = sorted(samples)[32]
+        dy.fill(0xA5)
+        ev, _ = time_steps(dev, steps, 2, stream, settle=0.1)
+        got_dev = dy.to_array(np.int32, outs[2])
+        out[name] = {"host_call_us": round(host_s * 1e6, 2), "host_gmac_per_s": round(macs / host_s / 1e9, 3),
+                     "device_us": round(ev * 1e3, 2), "device_gmac_per_s": round(macs / (ev * 1e-3) / 1e9, 1),
+                     "_check": (sym, shape, ins, outs[0].copy(), got_dev)}
+        for buf in (dw, dx, dy):
+            buf.free()
+        if sym in ("gemmi8", "gemmqmm") and ws is not None:
+            ws.free()
+        log(f"sweep {name}: host call {out[name]['host_call_us']:.1f} us ({out[name]['host_gmac_per_s']:.2f} GMAC/s), "
+            f"device {out[name]['device_us']:.2f} us")
+    return out
+
+
+def verify_sweep(O, sym, shape, ins, host_out, dev_out) -> bool:
+    """Both outputs of one sweep shape against the whole oracle output."""
+    if sym == "gemvq":
+        m, k = shape
+        want = O.gemv_q16(ins[0], ins[1], m, k)
+    elif sym == "mmi16":
+        want = O.gemv_i16(ins[0], ins[1], shape, shape)
+    elif sym == "gemmi8":
+        want = O.gemm_i8(ins[0], ins[1], shape, shape, shape)
+    else:
+        want = O.gemm_q16(ins[0], ins[1], shape, shape, shape)
+    want = np.asarray(want).ravel()
+    return bool(np.array_equal(host_out.ravel(), want) and np.array_equal(dev_out.ravel(), want))
 
 
 def vendor_int8_child(steps: int, settle_s: float) -> None:
@@ -563,8 +674,8 @@ def main() -> int:
     ap.add_argument("--vendor-ref", action="store_true",
                     help="also time the vendor int8 GEMM (torch._int_mm) on the headline shape, for context")
     ap.add_argument("--vendor-child", action="store_true", help=argparse.SUPPRESS)
-    ap.add_argument("--host-abi", action="store_true",
-                    help="also time the reference-ABI host-pointer calls end to end (PCIe included)")
+    ap.add_argument("--no-host-abi", action="store_true",
+                    help="skip the end-to-end host-pointer timings (PCIe included) and the reference sweeps")
     ap.add_argument("--settle", type=float, default=0.5,
                     help="seconds of back-to-back running before each timed region (default %(default)s)")
     args = ap.parse_args()
@@ -745,8 +856,12 @@ def main() -> int:
                          "gmac_per_s": round(t * 500.0, 1), "frac": round(t / PEAK_INT8_TOPS, 4)}
             log(f"{name}: {r['ms'] * 1e3:.1f} us  {t:.1f} TOP/s")
     result["secondary"] = sec
+    sweeps = {}
+    if not args.no_host_abi:
+        log("reference sweeps: the reference benches' shapes, host-pointer calls and device-resident")
+        sweeps = reference_sweeps(stream, K)
     stream.destroy()
-    if args.host_abi:
+    if not args.no_host_abi:
         log("host_abi: reference-ABI host-pointer calls, PCIe copies included")
         result["host_abi"] = host_abi_timings()
         log(f"host_abi: {result['host_abi']}")
@@ -762,6 +877,18 @@ def main() -> int:
         for name, r in runs.items():
             checks[name] = r["verify"](O)
             log(f"oracle check {name}: {'exact' if checks[name] else 'MISMATCH'} ({r['checked_rows']} rows)")
+        for name, r in sweeps.items():
+            checks[f"sweep_{name}"] = verify_sweep(O, *r.pop("_check"))
+            log(f"oracle check sweep {name}: {'exact' if checks['sweep_' + name] else 'MISMATCH'} (whole output, "
+                f"host call and device)")
+        if sweeps:
+            result["reference_sweeps"] = {
+                "note": "the reference benches' own sweep shapes (benches/det_matmul_i8.rs:86, det_matmul_q16.rs:82, "
+                        "det_matmul_i16.rs:77, det_gemv_q16_mt.rs:62 and its 512x130 anchor): host_call = the "
+                        "symbol its bench dlsyms, timed as its report_gmacs (median of 64 synchronous calls after 8, "
+                        "pageable buffers, PCIe copies included); device = the same work on device-resident operands "
+                        "(HIP events); each output checked whole against the oracle (exact_vs_oracle sweep_*)",
+                **sweeps}
         result["exact_vs_oracle"] = checks
         if "fft_q16_256" in sec:
             ref = cpu_fft_reference(8)

@@ -210,6 +210,18 @@ int64_t det_matmul_q16_dev(const int32_t *a, const int32_t *b, int32_t *c, int64
                            void *stream);
 int64_t det_gemv_q16_dev(const int32_t *w, const int32_t *x, int32_t *y, int64_t m, int64_t k, int64_t nb,
                          void *stream);
+/* The batched Q16 GEMV (device form of __mind_blas_gemv_q16_mt,
+ * src/mlir/lowering.rs:9822-9997, one call for nb query vectors) with the
+ * workspace from the caller, like det_matmul_ws_dev: no arena, no
+ * allocation, no event ordering between calls (calls sharing one workspace
+ * must be ordered by the caller, e.g. on one stream).  The workspace holds
+ * the query vectors' MFMA operands, det_gemv_workspace_bytes(m, k, nb) bytes
+ * for 16-byte aligned w and 4-byte aligned x (0 when no group of vectors
+ * takes the MFMA kernel); it is optional: with less, every vector runs the
+ * one-vector kernel.  Its contents need not be initialised. */
+int64_t det_gemv_workspace_bytes(int64_t m, int64_t k, int64_t nb);
+int64_t det_gemv_q16_ws_dev(const int32_t *w, const int32_t *x, int32_t *y, int64_t m, int64_t k, int64_t nb,
+                            void *ws, int64_t ws_bytes, void *stream);
 int64_t det_gemv_i16_dev(const int16_t *w, const int16_t *x, int32_t *y, int64_t m, int64_t k, void *stream);
 /* op = DET_DOT_Q16, DET_DOT_L1_Q16 or DET_DOT_I16; *out (device memory)
  * receives the int32 result (the reference's return value narrowed). */

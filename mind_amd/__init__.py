@@ -86,6 +86,9 @@ def _bind(L):
     for name in ("det_matmul_i8_dev", "det_matmul_i16_dev", "det_matmul_q16_dev"):
         f = getattr(L, name); f.argtypes = [_p, _p, _p, _i64, _i64, _i64, _p]; f.restype = _i64
     L.det_gemv_q16_dev.argtypes = [_p, _p, _p, _i64, _i64, _i64, _p]; L.det_gemv_q16_dev.restype = _i64
+    L.det_gemv_workspace_bytes.argtypes = [_i64] * 3; L.det_gemv_workspace_bytes.restype = _i64
+    L.det_gemv_q16_ws_dev.argtypes = [_p, _p, _p, _i64, _i64, _i64, _p, _i64, _p]
+    L.det_gemv_q16_ws_dev.restype = _i64
     L.det_gemv_i16_dev.argtypes = [_p, _p, _p, _i64, _i64, _p]; L.det_gemv_i16_dev.restype = _i64
     L.det_workspace_bytes.argtypes = [_i64] * 4; L.det_workspace_bytes.restype = _i64
     L.det_matmul_ws_dev.argtypes = [_i64, _p, _p, _p, _i64, _i64, _i64, _p, _i64, _p]

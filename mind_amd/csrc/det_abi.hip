@@ -611,6 +611,26 @@ int64_t det_matmul_ws_dev(int64_t op, const void *a, const void *b, int32_t *c, 
     return gemm_dev(o, a, b, c, m, k, n, enough ? ws : nullptr, (hipStream_t)stream);
 }
 
+// The batched GEMV's workspace (the query vectors' MFMA operands), assuming
+// aligned operands: 0 when no group of vectors takes the MFMA kernel.
+int64_t det_gemv_workspace_bytes(int64_t m, int64_t k, int64_t nb) {
+    if (bad_dims(m, k, nb) || m == 0 || nb == 0) return 0;
+    return (int64_t)gemv_ws_need(nullptr, nullptr, m, k, nb);
+}
+
+// det_gemv_q16_dev with the caller's workspace: no arena, so no allocation
+// and no event ordering; a short or missing workspace takes the VALU kernel.
+int64_t det_gemv_q16_ws_dev(const int32_t *w, const int32_t *x, int32_t *y, int64_t m, int64_t k, int64_t nb,
+                            void *ws, int64_t ws_bytes, void *stream) {
+    if (bad_dims(m, k, nb)) return set_err(DET_ERR_ARG, "dimension out of range [0, 2^31)");
+    if (m == 0 || nb == 0) return 0;
+    if (!y || ((!w || !x) && k > 0)) return set_err(DET_ERR_ARG, "null device pointer");
+    const size_t need = gemv_ws_need(w, x, m, k, nb);
+    const bool enough = need && ws && ws_bytes >= 0 && (size_t)ws_bytes >= need;
+    DET_HIP_CHECK(gemv_q16_any(w, x, y, m, k, nb, enough ? ws : nullptr, (hipStream_t)stream));
+    return 0;
+}
+
 int64_t det_gemv_q16_dev(const int32_t *w, const int32_t *x, int32_t *y, int64_t m, int64_t k, int64_t nb,
                          void *stream) {
     if (bad_dims(m, k, nb)) return set_err(DET_ERR_ARG, "dimension out of range [0, 2^31)");

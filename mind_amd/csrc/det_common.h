@@ -79,6 +79,12 @@ __device__ __forceinline__ uint4 buf_load16(__amdgpu_buffer_rsrc_t r, uint32_t o
     const v4i32 v = __builtin_bit_cast(v4i32, __builtin_amdgcn_raw_buffer_load_b128(r, (int)off, 0, 0));
     return make_uint4((uint32_t)v.x, (uint32_t)v.y, (uint32_t)v.z, (uint32_t)v.w);
 }
+// The same with a uniform byte offset in soffset (not range-checked: voff +
+// soff must lie inside the buffer).
+__device__ __forceinline__ uint4 buf_load16s(__amdgpu_buffer_rsrc_t r, uint32_t voff, uint32_t soff) {
+    const v4i32 v = __builtin_bit_cast(v4i32, __builtin_amdgcn_raw_buffer_load_b128(r, (int)voff, (int)soff, 0));
+    return make_uint4((uint32_t)v.x, (uint32_t)v.y, (uint32_t)v.z, (uint32_t)v.w);
+}
 __device__ __forceinline__ uint32_t buf_load4(__amdgpu_buffer_rsrc_t r, uint32_t off) {
     return __builtin_amdgcn_raw_buffer_load_b32(r, (int)off, 0, 0);
 }

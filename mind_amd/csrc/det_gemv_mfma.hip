@@ -41,85 +41,66 @@
 namespace det {
 namespace gemv8 {
 
-constexpr int THREADS = 256, DEPTH = 4;
+constexpr int DEPTH = 4;
 constexpr uint32_t BIAS4 = 0x80808080u;
 constexpr int NQ = 3;                                   // B operands per K step: digit pairs (0,1), (2,3), (4,-)
 constexpr int CH = 4;                                   // K steps per LDS chunk (per half)
 constexpr int XP_CH = CH * NQ * 64, XL_CH = CH * 64;    // uint4 per chunk
 constexpr int X_CH = XP_CH + XL_CH;                     // 1024 uint4 = 16 KiB per chunk
 
-// Balanced base-256 digit q (in [-128, 127]) of x: x = sum_{q<5} 2^(8q) d_q.
-__device__ __forceinline__ int digit(int32_t x, int q) {
-    long long v = x;
-    int d = 0;
-#pragma unroll
-    for (int i = 0; i <= q; ++i) {
-        d = (int)((v + 128) & 255) - 128;
-        v = (v - d) >> 8;
-    }
-    return d;
-}
-
-// One 256-thread block per 64-wide K step s: the step's slice of the query
-// vectors is staged in LDS (coalesced loads), then turned into the digit
-// planes, the low halves and the exact per-step column sums part[s][b]
-// (summed by the main kernel: no atomics, nothing to zero beforehand).
+// One 128-thread block per 64-wide K step s, all in registers: thread t
+// takes vector v = t >> 4 and the four K indices 16 j + 4 g + e (j = (t >> 2)
+// & 3, g = t & 3, e < 4) of the step.  The balanced digits need no loop:
+// with u = x + 0x8080808080 (exact in int64), digit q of x is byte q of u
+// minus 128, i.e. byte q of u XOR 0x80 read as int8 (adding 128 to every
+// digit position turns the balanced digits into the plain base-256 digits
+// of u).  A 4 x 4 byte transpose of the four u's low words gives digit words
+// 0-3 of this thread's slot, their high words' low bytes digit 4.  The
+// step's column sums part[s][v] (exact, int64; summed by the main kernel:
+// no atomics, nothing to zero) come from a shuffle reduction over the 16
+// threads of each vector.  Vectors v >= nb read as zero (all digits zero).
 // Output layout, chunk by chunk (chunk c = steps CH c .. CH c + CH - 1, X_CH
-// uint4): xp entries (d8, Q, lane) at (d8 NQ + Q) 64 + lane, then xl entries
-// at XP_CH + d8 64 + ((j 4 + bp) 4 + g).
-__global__ __launch_bounds__(256) void prep_kernel(const int32_t *__restrict__ X, int nb, int K,
+// uint4): xp entries (d8, Q, lane) at (d8 NQ + Q) 64 + lane, lane = b + 16 g,
+// column b = v + 8 (q & 1) for digit q = 2 Q + (b >> 3), word j; then xl
+// entries at XP_CH + d8 64 + ((j 4 + bp) 4 + g), vector 2 bp + h in its
+// dwords 2 h, 2 h + 1.
+__global__ __launch_bounds__(128) void prep_kernel(const int32_t *__restrict__ X, int nb, int K,
                                                    uint4 *__restrict__ xw, long long *__restrict__ part) {
-    __shared__ int32_t xs[8][65];
     const int s = blockIdx.x, t = threadIdx.x;
-    uint4 *xc = xw + (size_t)(s / CH) * X_CH;
+    const int v = t >> 4, j = (t >> 2) & 3, g = t & 3;
     const int d8 = s % CH;
+    uint32_t *xc = (uint32_t *)(xw + (size_t)(s / CH) * X_CH);
+    int32_t x[4] = {0, 0, 0, 0};
+    if (v < nb) {
+        const int32_t *src = X + (size_t)v * K + 64 * s + 16 * j + 4 * g;
 #pragma unroll
-    for (int e = t; e < 512; e += 256) {
-        const int b = e >> 6, k = e & 63;
-        xs[b][k] = b < nb ? X[(size_t)b * K + 64 * s + k] : 0;
+        for (int e = 0; e < 4; ++e) x[e] = src[e];
     }
-    __syncthreads();
-    if (t < NQ * 64) {
-        // B operand Q, lane l: column b = l & 15 (vector b & 7, digit
-        // 2Q + (b >> 3)), group g = l >> 4: 16 digit bytes at K 16 j + 4 g + e
-        const int Q = t >> 6, l = t & 63, b = l & 15, g = l >> 4;
-        const int v = b & 7, q = 2 * Q + (b >> 3);
-        uint32_t w[4];
+    uint32_t lo[4], hi4 = 0;
 #pragma unroll
-        for (int j = 0; j < 4; ++j) {
-            uint32_t word = 0;
-#pragma unroll
-            for (int e = 0; e < 4; ++e) {
-                const int k = 16 * j + 4 * g + e;
-                const uint32_t byte = (v < nb && q < 5) ? (uint32_t)(digit(xs[v][k], q) & 0xff) : 0u;
-                word |= byte << (8 * e);
-            }
-            w[j] = word;
-        }
-        xc[(d8 * NQ + Q) * 64 + l] = make_uint4(w[0], w[1], w[2], w[3]);
-    } else {
-        // low halves of vectors 2bp, 2bp+1 at K 16j+4g+{0,1},{2,3}
-        // (g fastest: the four K groups read adjacent 16-byte slots, no bank
-        // conflict); then the exact column sums of this step
-        const int u = t - NQ * 64, g = u >> 4, j = (u >> 2) & 3, bp = u & 3;
-        uint32_t d[4];
-#pragma unroll
-        for (int h = 0; h < 2; ++h) {
-            const int b = 2 * bp + h;
-#pragma unroll
-            for (int pr = 0; pr < 2; ++pr) {
-                const int k0 = 16 * j + 4 * g + 2 * pr;
-                d[2 * h + pr] = ((uint32_t)xs[b][k0] & 0xffffu) | ((uint32_t)xs[b][k0 + 1] << 16);
-            }
-        }
-        xc[XP_CH + d8 * 64 + (j * 4 + bp) * 4 + g] = make_uint4(d[0], d[1], d[2], d[3]);
-        if (u < 8) {
-            long long sum = 0;
-#pragma unroll 8
-            for (int k = 0; k < 64; ++k) sum += xs[u][k];
-            part[(size_t)s * 8 + u] = sum;
-        }
+    for (int e = 0; e < 4; ++e) {
+        const unsigned long long u = (unsigned long long)(long long)x[e] + 0x8080808080ull;
+        lo[e] = (uint32_t)u;
+        hi4 |= ((uint32_t)(u >> 32) & 0xffu) << (8 * e);
     }
+    uint32_t w[5];
+    transpose4x4(lo[0], lo[1], lo[2], lo[3], w[0], w[1], w[2], w[3]);
+    w[4] = hi4;
+#pragma unroll
+    for (int q = 0; q < 5; ++q) {
+        const int Q = q >> 1, b = v + 8 * (q & 1);
+        xc[((d8 * NQ + Q) * 64 + b + 16 * g) * 4 + j] = w[q] ^ BIAS4;
+    }
+    xc[((d8 * NQ + 2) * 64 + v + 8 + 16 * g) * 4 + j] = 0u;   // digit 5: none
+    // low halves: vector v's two K pairs into half h = v & 1 of entry (j, bp = v >> 1, g)
+    const uint32_t l01 = ((uint32_t)x[0] & 0xffffu) | ((uint32_t)x[1] << 16);
+    const uint32_t l23 = ((uint32_t)x[2] & 0xffffu) | ((uint32_t)x[3] << 16);
+    *(uint2 *)(xc + (XP_CH + d8 * 64 + ((j * 4 + (v >> 1)) * 4 + g)) * 4 + 2 * (v & 1)) = make_uint2(l01, l23);
+    // exact column sum of vector v over this step: the 16 threads t with t >> 4 == v
+    long long cs = (long long)x[0] + x[1] + x[2] + x[3];
+#pragma unroll
+    for (int o = 1; o < 16; o <<= 1) cs += __shfl_xor(cs, o);
+    if ((t & 15) == 0) part[(size_t)s * 8 + v] = cs;
 }
 
 __device__ __forceinline__ uint32_t residue2(uint32_t w2, uint32_t x2, uint32_t acc) {
@@ -158,7 +139,7 @@ __global__ __launch_bounds__(THREADS8, 1) void gemv8_kernel(const int32_t *__res
 
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int r = lane & 15, g = lane >> 4;
-    const int rg = wave & 3, kh = wave >> 2;
+    const int rg = wave & 3, kh = __builtin_amdgcn_readfirstlane(wave >> 2);
     const int row0 = blockIdx.x * 64 + rg * 16;
     const int myrow = min(row0 + r, M - 1);
     const __amdgpu_buffer_rsrc_t rw = make_rsrc(W, (uint32_t)M * (uint32_t)K * 4u);
@@ -205,7 +186,7 @@ __global__ __launch_bounds__(THREADS8, 1) void gemv8_kernel(const int32_t *__res
 #pragma unroll
     for (int d = 0; d < DEPTH; ++d)
 #pragma unroll
-        for (int j = 0; j < 4; ++j) wb[d][j] = buf_load16(rw, wbase + (uint32_t)(64 * (sbeg + d) + 16 * j) * 4u);
+        for (int j = 0; j < 4; ++j) wb[d][j] = buf_load16s(rw, wbase + 64u * j, (uint32_t)(256 * (sbeg + d)));
     stage_load(0);
     // column sums of the query vectors: thread t adds the per-step partials
     // i = t/8 + 64 u (u < 8, K <= 32768) of vector t % 8 (finished in the tail)
@@ -235,7 +216,12 @@ __global__ __launch_bounds__(THREADS8, 1) void gemv8_kernel(const int32_t *__res
             // consume the ring slot (limb transpose, low halves) before
             // reloading it: the reload then reuses the same registers, so no
             // register copy has to wait for a load still in flight.  The
-            // bias goes on after the transpose: planes 0-2 only
+            // bias goes on after the transpose: planes 0-2 only.  The reload
+            // is DEPTH steps ahead; past the half's end it re-reads the half's
+            // last step (never consumed), so every load stays inside this
+            // lane's W row: the step offset goes through the uniform soffset,
+            // which the range check does not cover
+            const uint32_t wsoff = (uint32_t)(256 * min(st + DEPTH, sbeg + half - 1));
             uint32_t T[4][4], L[4][2];
 #pragma unroll
             for (int j = 0; j < 4; ++j) {
@@ -248,8 +234,7 @@ __global__ __launch_bounds__(THREADS8, 1) void gemv8_kernel(const int32_t *__res
             }
 #pragma unroll
             for (int j = 0; j < 4; ++j)
-                wb[d][j] = buf_load16(rw, ls + DEPTH < half ? wbase + (uint32_t)(64 * (st + DEPTH) + 16 * j) * 4u
-                                                            : OOB_OFFSET);
+                wb[d][j] = buf_load16s(rw, wbase + 64u * j, wsoff);
             // query low halves of this step: the first half is read here, so
             // its LDS latency hides behind the MFMAs, the second half after
             // them, behind the first half's residues (reading each at its
@@ -282,11 +267,20 @@ __global__ __launch_bounds__(THREADS8, 1) void gemv8_kernel(const int32_t *__res
 #pragma unroll
             for (int j = 0; j < 4; ++j) {
                 const uint32_t L0 = L[j][0], L1 = L[j][1];
+                v2u16 P[4][4];
 #pragma unroll
                 for (int bp = 0; bp < 4; ++bp) {
                     const uint4 xv = XV[j][bp];
-                    racc[2 * bp] = residue2(L1, xv.y, residue2(L0, xv.x, racc[2 * bp]));
-                    racc[2 * bp + 1] = residue2(L1, xv.w, residue2(L0, xv.z, racc[2 * bp + 1]));
+                    P[bp][0] = __builtin_bit_cast(v2u16, L0) * __builtin_bit_cast(v2u16, xv.x);
+                    P[bp][1] = __builtin_bit_cast(v2u16, L1) * __builtin_bit_cast(v2u16, xv.y);
+                    P[bp][2] = __builtin_bit_cast(v2u16, L0) * __builtin_bit_cast(v2u16, xv.z);
+                    P[bp][3] = __builtin_bit_cast(v2u16, L1) * __builtin_bit_cast(v2u16, xv.w);
+                }
+                const v2u16 one = {1, 1};
+#pragma unroll
+                for (int bp = 0; bp < 4; ++bp) {
+                    racc[2 * bp] = __builtin_amdgcn_udot2(P[bp][1], one, __builtin_amdgcn_udot2(P[bp][0], one, racc[2 * bp], false), false);
+                    racc[2 * bp + 1] = __builtin_amdgcn_udot2(P[bp][3], one, __builtin_amdgcn_udot2(P[bp][2], one, racc[2 * bp + 1], false), false);
                 }
             }
         }
@@ -363,7 +357,7 @@ hipError_t launch_gemv_q16_mfma(const int32_t *W, const int32_t *X, int32_t *Y, 
     using namespace gemv8;
     uint4 *xw = (uint4 *)ws;
     long long *part = (long long *)(xw + (size_t)K / 64 / CH * X_CH);
-    hipLaunchKernelGGL(prep_kernel, dim3(K / 64), dim3(THREADS), 0, s, X, nb, K, xw, part);
+    hipLaunchKernelGGL(prep_kernel, dim3(K / 64), dim3(128), 0, s, X, nb, K, xw, part);
     hipLaunchKernelGGL(gemv8_kernel, dim3((M + 63) / 64), dim3(THREADS8), 0, s, W, xw, part, Y, M, K, nb);
     return hipGetLastError();
 }

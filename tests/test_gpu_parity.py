@@ -1060,6 +1060,38 @@ def test_gemv_q16_batched_full_range(m, k, nb, fam):
     np.testing.assert_array_equal(got, O.gemv_q16_batched(W, X, m, k, nb))
 
 
+GEMV_WS = [(64, 512, 8), (1000, 1024, 13), (16, 32768, 2), (300, 512, 1), (130, 1000, 8)]
+
+
+@pytest.mark.parametrize("m,k,nb", GEMV_WS, ids=[f"{m}x{k}b{nb}" for m, k, nb in GEMV_WS])
+def test_gemv_q16_ws_dev(m, k, nb):
+    """det_gemv_q16_ws_dev: the caller's workspace (garbage-filled, exactly
+    det_gemv_workspace_bytes), a workspace one byte short and none at all
+    (both take the one-vector kernel) give the oracle's output, twice in a
+    row on poisoned outputs; 130 x 1000 (K % 512 != 0) needs no workspace."""
+    L = M.lib()
+    W, X = O.gen_q16(0x6E5 ^ (m * k + nb), m * k, nb * k, shift=0)
+    want = O.gemv_q16_batched(W, X, m, k, nb).reshape(nb, m)
+    need = L.det_gemv_workspace_bytes(m, k, nb)
+    assert (need > 0) == (nb >= 2 and k % 512 == 0)
+    s = M.Stream()
+    dW, dX, dY = M.DeviceBuffer.from_array(W), M.DeviceBuffer.from_array(X), M.DeviceBuffer(nb * m * 4)
+    ws = M.DeviceBuffer(max(need, 256))
+    for ws_ptr, ws_bytes in ((ws.ptr, need), (ws.ptr, need - 1), (None, 0)):
+        for rep in range(2):
+            note(f"det_gemv_q16_ws_dev {m}x{k} nb={nb} ws_bytes={ws_bytes} rep={rep}")
+            ws.fill(0x3C + rep)
+            dY.fill(0xA5)
+            M.check(L.det_gemv_q16_ws_dev(dW.ptr, dX.ptr, dY.ptr, m, k, nb, ws_ptr, ws_bytes, s.ptr))
+            s.sync()
+            np.testing.assert_array_equal(dY.to_array(np.int32, (nb, m)), want)
+    assert L.det_gemv_q16_ws_dev(dW.ptr, dX.ptr, None, m, k, nb, ws.ptr, need, s.ptr) == M.DET_ERR_ARG
+    assert L.det_gemv_q16_ws_dev(dW.ptr, dX.ptr, dY.ptr, -1, k, nb, ws.ptr, need, s.ptr) == M.DET_ERR_ARG
+    for buf in (dW, dX, dY, ws):
+        buf.free()
+    s.destroy()
+
+
 @pytest.mark.parametrize("m,k", [(1, 1), (7, 9), (256, 256), (300, 1001), (4096, 4096)])
 def test_gemv_i16_shapes(m, k):
     W, x = O.gen_i16(0xDEADBEEF ^ (m * 3 + k), m * k, k)
