@@ -447,3 +447,44 @@ def test_pad_kernel_lane_algebra(rows, cols, mis):
     want = np.zeros((rows_out, dcols), np.uint8)
     want[:rows, :cols] = src.view(np.uint8)
     assert np.array_equal(_pad_model(src, mis, rows, cols, rows_out, dcols), want)
+
+
+# ------------------------------------------------------------------ batched GEMV W ring
+# gemv8_kernel (mind_amd/csrc/det_gemv_mfma.hip) streams W rows into a register
+# ring with buffer loads whose step offset is the uniform soffset, which the
+# range check does not cover: voffset = this lane's row / K-group base + 64 j,
+# soffset = 256 * step, the step clamped to the last of the wave's K half, so
+# the reloads past the end re-read that step.  Every load must stay inside
+# the lane's own W row.
+GEMV_DEPTH = 4
+
+
+def _gemv8_w_addresses(M, K):
+    nsteps = K // 64
+    half = nsteps // 2
+    blocks = (M + 63) // 64
+    b = np.arange(blocks)[:, None, None]
+    w = np.arange(8)[None, :, None]
+    lane = np.arange(64)[None, None, :]
+    rg, kh = w & 3, w >> 2
+    r, g = lane & 15, lane >> 4
+    myrow = np.minimum(b * 64 + rg * 16 + r, M - 1)
+    wbase = (myrow * K + 4 * g) * 4
+    sbeg = kh * half
+    steps = [sbeg + d for d in range(GEMV_DEPTH)]                                   # prologue
+    steps += [np.minimum(sbeg + ls + GEMV_DEPTH, sbeg + half - 1) for ls in range(half)]   # ring reloads
+    lo = hi = None
+    for st in steps:
+        for j in range(4):
+            addr = wbase + 64 * j + 256 * st
+            row_lo, row_hi = myrow * K * 4, (myrow + 1) * K * 4
+            assert (addr >= row_lo).all() and (addr + 16 <= row_hi).all()
+            lo = addr.min() if lo is None else min(lo, addr.min())
+            hi = (addr + 16).max() if hi is None else max(hi, (addr + 16).max())
+    return lo, hi
+
+
+@pytest.mark.parametrize("M,K", [(16, 512), (16384, 16384), (11922, 4096), (130, 32768), (100, 1024)])
+def test_gemv8_w_ring_stays_inside_each_row(M, K):
+    lo, hi = _gemv8_w_addresses(M, K)
+    assert lo >= 0 and hi <= M * K * 4
