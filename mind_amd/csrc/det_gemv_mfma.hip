@@ -103,12 +103,6 @@ __global__ __launch_bounds__(128) void prep_kernel(const int32_t *__restrict__ X
     if ((t & 15) == 0) part[(size_t)s * 8 + v] = cs;
 }
 
-__device__ __forceinline__ uint32_t residue2(uint32_t w2, uint32_t x2, uint32_t acc) {
-    // two 16-bit residues (lo16 w * lo16 x mod 2^16) added into acc
-    const v2u16 one = {1, 1};
-    return __builtin_amdgcn_udot2(__builtin_bit_cast(v2u16, w2) * __builtin_bit_cast(v2u16, x2), one, acc, false);
-}
-
 // One block = 8 waves (2 per SIMD, so one wave's LDS / MFMA latency hides
 // behind the other's VALU work) on 64 W rows: wave w takes rows
 // 16 (w & 3) .. +16 and K half (w >> 2).  The query operands of a chunk of CH
@@ -264,24 +258,30 @@ __global__ __launch_bounds__(THREADS8, 1) void gemv8_kernel(const int32_t *__res
             for (int j = 2; j < 4; ++j)
 #pragma unroll
                 for (int bp = 0; bp < 4; ++bp) XV[j][bp] = sxl[((d8 * 4 + j) * 4 + bp) * 4 + g];
+            // two 16-bit residues (lo16 w * lo16 x mod 2^16) per
+            // v_pk_mul_lo_u16, added into the vector's sum by v_dot2_u32_u16
+            // against (1, 1): a K group's 16 products are formed before its
+            // 16 sums, so no sum waits on the product just before it
+            const v2u16 one = {1, 1};
 #pragma unroll
             for (int j = 0; j < 4; ++j) {
-                const uint32_t L0 = L[j][0], L1 = L[j][1];
+                const v2u16 L0 = __builtin_bit_cast(v2u16, L[j][0]), L1 = __builtin_bit_cast(v2u16, L[j][1]);
                 v2u16 P[4][4];
 #pragma unroll
                 for (int bp = 0; bp < 4; ++bp) {
                     const uint4 xv = XV[j][bp];
-                    P[bp][0] = __builtin_bit_cast(v2u16, L0) * __builtin_bit_cast(v2u16, xv.x);
-                    P[bp][1] = __builtin_bit_cast(v2u16, L1) * __builtin_bit_cast(v2u16, xv.y);
-                    P[bp][2] = __builtin_bit_cast(v2u16, L0) * __builtin_bit_cast(v2u16, xv.z);
-                    P[bp][3] = __builtin_bit_cast(v2u16, L1) * __builtin_bit_cast(v2u16, xv.w);
+                    P[bp][0] = L0 * __builtin_bit_cast(v2u16, xv.x);
+                    P[bp][1] = L1 * __builtin_bit_cast(v2u16, xv.y);
+                    P[bp][2] = L0 * __builtin_bit_cast(v2u16, xv.z);
+                    P[bp][3] = L1 * __builtin_bit_cast(v2u16, xv.w);
                 }
-                const v2u16 one = {1, 1};
 #pragma unroll
-                for (int bp = 0; bp < 4; ++bp) {
-                    racc[2 * bp] = __builtin_amdgcn_udot2(P[bp][1], one, __builtin_amdgcn_udot2(P[bp][0], one, racc[2 * bp], false), false);
-                    racc[2 * bp + 1] = __builtin_amdgcn_udot2(P[bp][3], one, __builtin_amdgcn_udot2(P[bp][2], one, racc[2 * bp + 1], false), false);
-                }
+                for (int bp = 0; bp < 4; ++bp)
+#pragma unroll
+                    for (int h = 0; h < 2; ++h) {
+                        const uint32_t r = __builtin_amdgcn_udot2(P[bp][2 * h], one, racc[2 * bp + h], false);
+                        racc[2 * bp + h] = __builtin_amdgcn_udot2(P[bp][2 * h + 1], one, r, false);
+                    }
             }
         }
         __builtin_amdgcn_sched_barrier(0);
