@@ -1303,7 +1303,7 @@ __global__ __launch_bounds__(THREADS, 1) void gemm_i8_t256_kernel(const int8_t *
 }  // namespace i8g
 
 // Compute units of the current device (cached per device).
-static int cu_count() {
+int cu_count() {
     static int cached[64];
     int d = 0;
     if (hipGetDevice(&d) != hipSuccess || d < 0 || d >= 64) return 256;

@@ -34,6 +34,8 @@
 //    of the eight below K 2^16 < 2^32.  Sets with shift >= 2 only need their
 //    value mod 2^32.  The epilogue combines S, R and the bias terms in
 //    uint64 and keeps bits 16..47.
+#include <algorithm>
+
 #include "det_common.h"
 #include "det_kernels.h"
 
@@ -254,24 +256,32 @@ constexpr int RP_STRIDE = 72;
 // The residue is VALU work that no MFMA can do; giving it whole waves lets
 // the SIMD issue it back to back while the limb wave's MFMAs and LDS
 // traffic proceed beside it.
+template <bool SPLIT>
 __global__ __launch_bounds__(THREADS, 1) void q16x_kernel(
     const uint8_t *__restrict__ ws, Q16xWs L,
     const unsigned long long *__restrict__ rowsum, const unsigned long long *__restrict__ colsum, int ncs,
-    int32_t *__restrict__ C, int M, int N, int Kp, int tiles_m, int tiles_n, unsigned long long kc2) {
+    int32_t *__restrict__ C, int M, int N, int Kp, int tiles_m, int tiles_n, unsigned long long kc2, int kspl_arg,
+    unsigned long long *__restrict__ part) {
     __shared__ __attribute__((aligned(1024))) uint8_t smem[NST * STAGE];
 
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-    // tile order: XCD-contiguous ids, then groups of 8 row tiles
+    // tile order: XCD-contiguous ids, then groups of 8 row tiles; with
+    // SPLIT the kspl workgroups of a tile take consecutive ids and
+    // consecutive K ranges (as even as whole 64-k steps allow, at least one
+    // step each), and each writes its partial sums to part (compiled
+    // separately so the unsplit kernel keeps its own code)
+    const int kspl = SPLIT ? kspl_arg : 1;
     const int ntiles = tiles_m * tiles_n;
-    const int pid = xcd_remap(blockIdx.x, ntiles);
+    const int pid_all = xcd_remap(blockIdx.x, ntiles * kspl);
+    const int pid = pid_all / kspl, ks = pid_all - pid * kspl;
     constexpr int GM = 8;
     const int group = pid / (GM * tiles_n), first = group * GM;
     const int gsz = min(tiles_m - first, GM);
     const int inner = pid - group * GM * tiles_n;
     const int tm = first + inner % gsz, tn = inner / gsz;
     const int m0 = tm * BM, n0 = tn * BN;
-    const int nk = Kp / BK;
+    const int kt0 = ks * (Kp / BK) / kspl, nk = (ks + 1) * (Kp / BK) / kspl - kt0;   // kspl <= Kp / BK
     uint32_t *sR = (uint32_t *)smem;   // epilogue residue partials
 
     if (wave < 4) {
@@ -303,7 +313,7 @@ __global__ __launch_bounds__(THREADS, 1) void q16x_kernel(
             for (int j = 0; j < 12; ++j) {
                 const int b = 12 * wave + j;
                 const uint32_t step = b < 32 ? BK : 2 * BK;
-                dma16(rw, lds_addr(smem + buf * STAGE + b * 1024), (int)(doff[j] + (uint32_t)kt * step));
+                dma16(rw, lds_addr(smem + buf * STAGE + b * 1024), (int)(doff[j] + (uint32_t)(kt0 + kt) * step));
             }
         };
         const int fr = lane & 31, fh = lane >> 5;
@@ -371,8 +381,14 @@ __global__ __launch_bounds__(THREADS, 1) void q16x_kernel(
             const long long x = (long long)acc[0][r] + ((long long)acc[1][r] << 8) - (long long)R;
             const uint32_t y = (uint32_t)acc[2][r] + ((uint32_t)acc[3][r] << 8) + ((uint32_t)acc[4][r] << 16) +
                                ((uint32_t)acc[5][r] << 24);
-            const unsigned long long v =
-                (unsigned long long)x + ((unsigned long long)y << 16) + c * (rowsum[row] + cb) - kc2;
+            const unsigned long long sr = (unsigned long long)x + ((unsigned long long)y << 16);
+            if (SPLIT) {
+                // this K range's (S - R) mod 2^64; the bias terms and the
+                // final shift are applied once to the sum of the partials
+                part[((size_t)ks * M + row) * N + col] = sr;
+                continue;
+            }
+            const unsigned long long v = sr + c * (rowsum[row] + cb) - kc2;
             C[(size_t)row * N + col] = (int32_t)(uint32_t)(v >> 16);
         }
     } else {
@@ -448,7 +464,38 @@ __global__ __launch_bounds__(THREADS, 1) void q16x_kernel(
     }
 }
 
+// K split: C = bits 16..47 of the sum of the kspl partials (S - R over each
+// K range, mod 2^64) plus the bias terms c (row sum + column sum) - K c^2:
+// the same value the unsplit epilogue forms, as every term is a sum mod
+// 2^64 and only bits 16..47 are kept.
+__global__ __launch_bounds__(256) void split_reduce_kernel(const unsigned long long *__restrict__ part, int kspl,
+                                                           const unsigned long long *__restrict__ rowsum,
+                                                           const unsigned long long *__restrict__ colsum, int ncs,
+                                                           int32_t *__restrict__ C, int M, int N,
+                                                           unsigned long long kc2) {
+    const size_t i = (size_t)blockIdx.x * 256 + threadIdx.x, mn = (size_t)M * N;
+    if (i >= mn) return;
+    const int row = (int)(i / (size_t)N), col = (int)(i - (size_t)row * N);
+    unsigned long long v = 0, cb = 0;
+    for (int k = 0; k < kspl; ++k) v += part[(size_t)k * mn + i];
+    for (int k = 0; k < ncs; ++k) cb += colsum[(size_t)k * N + col];
+    v += 0x808080ull * (rowsum[row] + cb) - kc2;
+    C[i] = (int32_t)(uint32_t)(v >> 16);
+}
+
 }  // namespace q16x
+
+// K splits for grids of 64 x 64 tiles that fill at most half the CUs (one
+// workgroup per CU): as many as the CUs take, at most 8 and at most one per
+// 64-k step, then the fewest that keep the longest split's step count.
+int q16x_ksplit(int M, int N, int K, int cus) {
+    const long long tiles = (long long)((M + q16x::BM - 1) / q16x::BM) * ((N + q16x::BN - 1) / q16x::BN);
+    const int nk = (K + q16x::KP_ALIGN - 1) / q16x::KP_ALIGN;
+    if (2 * tiles > cus || nk < 2) return 1;
+    const int k = (int)std::min<long long>(std::min<long long>(8, cus / tiles), nk);
+    const int steps = (nk + k - 1) / k;   // K steps of the longest split
+    return (nk + steps - 1) / steps;
+}
 
 bool q16x_eligible(int M, int N, int K) {
     const long long Kp = ((long long)K + q16x::KP_ALIGN - 1) / q16x::KP_ALIGN * q16x::KP_ALIGN;
@@ -461,7 +508,9 @@ bool q16x_eligible(int M, int N, int K) {
 size_t q16x_workspace_bytes(int M, int N, int K) {
     const size_t Kp = (size_t)((K + q16x::KP_ALIGN - 1) / q16x::KP_ALIGN) * q16x::KP_ALIGN;
     const size_t b = 6 * ((size_t)M + N) * Kp + 8 * ((size_t)M + (size_t)q16x::q16_ncs((int)Kp) * N);
-    return (b + 255) & ~(size_t)255;
+    const int kspl = q16x_ksplit(M, N, K, cu_count());
+    const size_t partials = kspl > 1 ? (size_t)kspl * M * N * 8 : 0;   // [kspl][M][N] u64 after the sums
+    return ((b + 255) & ~(size_t)255) + partials;
 }
 
 hipError_t launch_gemm_q16x(const int32_t *A, const int32_t *B, int32_t *C, int M, int N, int K, bool b_is_t,
@@ -490,8 +539,22 @@ hipError_t launch_gemm_q16x(const int32_t *A, const int32_t *B, int32_t *C, int 
     L.alo = (uint32_t)((uint8_t *)Alo - Ap);
     L.blo = (uint32_t)((uint8_t *)Blo - Ap);
     L.bytes = (uint32_t)((uint8_t *)(Blo + b_plane) - Ap);
-    hipLaunchKernelGGL(q16x_kernel, dim3(tiles_m * tiles_n), dim3(THREADS), 0, s, Ap, L, rowsum, colsum, ncs, C,
-                       M, N, Kp, tiles_m, tiles_n, kc2);
+    const int kspl = q16x_ksplit(M, N, K, cu_count());
+    unsigned long long *part = nullptr;
+    if (kspl > 1) {   // after the sums region sized for the most partials (q16x_workspace_bytes)
+        const size_t b = 6 * ((size_t)M + N) * Kp + 8 * ((size_t)M + (size_t)q16_ncs(Kp) * N);
+        part = (unsigned long long *)((uint8_t *)ws + ((b + 255) & ~(size_t)255));
+    }
+    if (kspl == 1) {
+        hipLaunchKernelGGL(q16x_kernel<false>, dim3(tiles_m * tiles_n), dim3(THREADS), 0, s, Ap, L, rowsum, colsum,
+                           ncs, C, M, N, Kp, tiles_m, tiles_n, kc2, 1, part);
+    } else {
+        hipLaunchKernelGGL(q16x_kernel<true>, dim3(tiles_m * tiles_n * kspl), dim3(THREADS), 0, s, Ap, L, rowsum,
+                           colsum, ncs, C, M, N, Kp, tiles_m, tiles_n, kc2, kspl, part);
+        const size_t mn = (size_t)M * N;
+        hipLaunchKernelGGL(split_reduce_kernel, dim3((unsigned)((mn + 255) / 256)), dim3(256), 0, s, part, kspl, rowsum,
+                           colsum, ncs, C, M, N, kc2);
+    }
     return hipGetLastError();
 }
 

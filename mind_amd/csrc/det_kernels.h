@@ -10,6 +10,9 @@
 
 namespace det {
 
+// Compute units of the current device (cached per device; 256 if unknown).
+int cu_count();
+
 // The int16 and Q16 preps write column sums of B as at most MAX_CS exact
 // partials per column ([ncs][N], ncs <= MAX_CS); the GEMM epilogues add them.
 constexpr int MAX_CS = 16;

@@ -990,6 +990,51 @@ def test_gemm_q16_multi_tile(gen):
     np.testing.assert_array_equal(c.reshape(m, n), want)
 
 
+# Grids of 64 x 64 tiles that fill at most half the CUs run split in K (up to
+# 8 partial sums per tile over whole 64-k steps, reduced by a second
+# kernel): 256^3 (16 tiles, 4 splits of one step), 512^3 (64 tiles, 4 splits
+# of two), 100 x 512 x 70 (4 ragged tiles, 8 splits), 1000 x 128 x 33 (2
+# splits), 7 x 1000 x 130 (K off the 64 grid, 8 splits), 300 x 320 x 200 (5
+# splits of one step), 200 x 576 x 500 (5 uneven splits: 1, 2, 2, 2, 2 steps).
+Q_SPLIT = [(256, 256, 256), (512, 512, 512), (100, 512, 70), (1000, 128, 33), (7, 1000, 130), (300, 320, 200),
+           (200, 576, 500)]
+
+
+@pytest.mark.parametrize("m,k,n", Q_SPLIT, ids=[f"{m}x{k}x{n}" for m, k, n in Q_SPLIT])
+def test_gemm_q16_k_split(m, k, n):
+    """The K-split route against the oracle: saturating inputs through the
+    device workspace entry (the workspace, partials included, refilled with
+    garbage before each call), and full-range inputs through gemmqmm and the
+    B-transposed gemmq."""
+    L = M.lib()
+    a, b = O.gen_q16_sat(0x5A17 ^ (m * 7919 + k * 31 + n), m * k, k * n, shift=13)
+    want = O.gemm_q16(a, b, m, k, n).reshape(m, n)
+    wsb = L.det_workspace_bytes(M.DET_OP_Q16, m, k, n)
+    s = M.Stream()
+    da, db, dc = M.DeviceBuffer.from_array(a), M.DeviceBuffer.from_array(b), M.DeviceBuffer(m * n * 4)
+    ws = M.DeviceBuffer(wsb)
+    for rep in range(2):
+        note(f"det_matmul_ws_dev q16 split {m}x{k}x{n} rep={rep}")
+        ws.fill(0x6B + rep)
+        dc.fill(0xA5)
+        M.check(L.det_matmul_ws_dev(M.DET_OP_Q16, da.ptr, db.ptr, dc.ptr, m, k, n, ws.ptr, wsb, s.ptr))
+        s.sync()
+        np.testing.assert_array_equal(dc.to_array(np.int32, (m, n)), want)
+    for buf in (da, db, dc, ws):
+        buf.free()
+    s.destroy()
+    a, b = O.gen_q16(0x5A18 ^ (m * 7919 + k * 31 + n), m * k, k * n, shift=0)
+    want = O.gemm_q16(a, b, m, k, n)
+    note(f"gemmqmm / gemmq full-range split {m}x{k}x{n}")
+    c = np.zeros(m * n, np.int32)
+    call6("gemmqmm", a, b, c, m, k, n)
+    np.testing.assert_array_equal(c, want.ravel())
+    bt = np.ascontiguousarray(b.reshape(k, n).T)
+    c = np.zeros(m * n, np.int32)
+    call6("gemmq", a, bt, c, m, k, n)
+    np.testing.assert_array_equal(c, want.ravel())
+
+
 I16_SHAPES = [(1, 1, 1), (3, 5, 7), (64, 64, 64), (65, 127, 66), (200, 300, 100), (33, 2048, 17),
               (300, 1000, 270), (129, 16, 128)]
 
