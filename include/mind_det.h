@@ -249,11 +249,13 @@ int64_t det_fft_workspace_bytes(int64_t logn, int64_t batch);
  * multiples of 256 adds at most 1/8 per dimension (e.g. 1008^3), where the
  * padded panels run faster.  For int8 the workspace is
  * optional: without it such operands run a slower byte-load kernel;
- * det_matmul_ws_dev rejects a short workspace only for int16 / Q16.  The
- * figure holds for the current device: small Q16 grids split K over idle
- * compute units and keep their partial sums in the workspace, so the size
- * depends on the device's compute-unit count (ask on the device that runs
- * the call). */
+ * det_matmul_ws_dev rejects a short workspace only for int16 / Q16.  Q16
+ * shapes small enough for the direct kernel (16 x 16 output tiles filling at
+ * most 4 rounds of the compute units, rounds times K at most 4096, e.g.
+ * every cube up to 512^3) need none (0).  The figure holds for the current
+ * device: that rule, and the K split of mid-size Q16 grids that keeps its
+ * partial sums in the workspace, depend on the device's compute-unit count
+ * (ask on the device that runs the call). */
 int64_t det_workspace_bytes(int64_t op, int64_t m, int64_t k, int64_t n);
 int64_t det_matmul_ws_dev(int64_t op, const void *a, const void *b, int32_t *c, int64_t m, int64_t k, int64_t n,
                           void *ws, int64_t ws_bytes, void *stream);

@@ -361,6 +361,7 @@ static hipError_t launch_limb(const T *A, const T *B, int32_t *C, int M, int N, 
 
 hipError_t launch_gemm_q16(const int32_t *A, const int32_t *B, int32_t *C, int M, int N, int K, bool b_is_t,
                            void *ws, hipStream_t s) {
+    if (q16_small(M, N, K)) return launch_gemm_q16_small(A, B, C, M, N, K, b_is_t, s);
     if (q16x_eligible(M, N, K)) return launch_gemm_q16x(A, B, C, M, N, K, b_is_t, ws, s);
     return launch_limb<int32_t, 4, true>(A, B, C, M, N, K, b_is_t, ws, s);
 }

@@ -31,7 +31,15 @@ hipError_t launch_gemm_i8(const int8_t *A, const int8_t *B, int32_t *C, int M, i
 // halves (Q16) and exact row / column sums.
 size_t limb_workspace_bytes(int M, int N, int K, int np, bool q16);
 size_t q16x_workspace_bytes(int M, int N, int K);   // the second-generation Q16 kernel's layout
+// Small Q16 shapes (det_gemm_q16s.hip): one direct launch, no workspace,
+// when the 16x16 output tiles fill at most Q16_SMALL_ROUNDS rounds of the
+// compute units and rounds times K is at most Q16_SMALL_TERMS.
+constexpr long long Q16_SMALL_ROUNDS = 4, Q16_SMALL_TERMS = 4096;
+bool q16_small(int M, int N, int K);
+hipError_t launch_gemm_q16_small(const int32_t *A, const int32_t *B, int32_t *C, int M, int N, int K, bool b_is_t,
+                                 hipStream_t s);
 inline size_t q16_workspace_bytes(int M, int N, int K) {
+    if (q16_small(M, N, K)) return 0;
     const size_t a = limb_workspace_bytes(M, N, K, 4, true), b = q16x_workspace_bytes(M, N, K);
     return a > b ? a : b;
 }

@@ -612,7 +612,7 @@ def test_device_arena_shared_by_two_streams():
     # arena, ordered by its event, so interleaved calls of different shapes
     # must each give the oracle's C
     L = M.lib()
-    shapes = [(192, 160, 224), (320, 96, 128)]
+    shapes = [(1040, 160, 1024), (1024, 96, 1100)]   # limb kernel: both need the arena
     data = []
     for si, (m, k, n) in enumerate(shapes):
         a, b = O.gen_q16(0x7B0 + si, m * k, k * n, shift=0)
@@ -846,9 +846,10 @@ SWEEP_LIMB = [(op, *shape) for op in (M.DET_OP_Q16, M.DET_OP_I16) for shape in _
 
 @pytest.mark.parametrize("op,m,k,n", SWEEP_LIMB, ids=[f"op{op}-{m}x{k}x{n}" for op, m, k, n in SWEEP_LIMB])
 def test_gemm_limb_sweep(op, m, k, n):
-    """Seeded Q16 (saturating generator) and int16 shapes, full output against
-    the CPU restatement, through det_matmul_ws_dev with exactly the reported
-    workspace refilled with garbage first."""
+    """Seeded Q16 (saturating generator; direct or limb kernel by shape) and
+    int16 shapes, full output against the CPU restatement, through
+    det_matmul_ws_dev with exactly the reported workspace refilled with
+    garbage first."""
     if op == M.DET_OP_Q16:
         a, b = O.gen_q16_sat(0x11B ^ (m * 7919 + k * 31 + n), m * k, k * n, 13)
     else:
@@ -944,6 +945,42 @@ def test_gemm_q16_shapes(m, k, n, shift):
     np.testing.assert_array_equal(got, O.gemm_q16(a, b, m, k, n))
 
 
+# The direct kernel's edges: one K term, K across its 64-k slices and 256-k
+# chunks (63, 64, 65, 255, 256, 257, 1000), the longest K it takes for one
+# round of tiles (4096) and four rounds of 16 x 16 tiles (512 x 1024 x 512).
+Q_DIRECT = [(16, 1, 16), (17, 63, 15), (33, 64, 31), (40, 65, 48), (5, 255, 300), (256, 256, 256), (99, 257, 161),
+            (7, 1000, 130), (16, 4096, 16), (64, 4096, 48), (512, 1024, 512)]
+
+
+@pytest.mark.parametrize("m,k,n", Q_DIRECT, ids=[f"{m}x{k}x{n}" for m, k, n in Q_DIRECT])
+def test_gemm_q16_direct_route(m, k, n):
+    """Small shapes take the direct per-term kernel (no workspace): full-range
+    inputs through det_matmul_q16 and the B-transposed gemmq, saturating
+    inputs through the device workspace entry with no workspace at all."""
+    L = M.lib()
+    assert L.det_workspace_bytes(M.DET_OP_Q16, m, k, n) == 0
+    a, b = O.gen_q16(0x5D1 ^ (m * 7919 + k * 31 + n), m * k, k * n, shift=0)
+    want = O.gemm_q16(a, b, m, k, n).reshape(m, n)
+    note(f"det_matmul_q16 direct {m}x{k}x{n}")
+    np.testing.assert_array_equal(M.det_matmul_q16(a.reshape(m, k), b.reshape(k, n)), want)
+    bt = np.ascontiguousarray(b.reshape(k, n).T)
+    c = np.zeros(m * n, np.int32)
+    call6("gemmq", a, bt, c, m, k, n)
+    np.testing.assert_array_equal(c.reshape(m, n), want)
+    a, b = O.gen_q16_sat(0x5D2 ^ (m * 7919 + k * 31 + n), m * k, k * n, shift=13)
+    want = O.gemm_q16(a, b, m, k, n).reshape(m, n)
+    s = M.Stream()
+    da, db, dc = M.DeviceBuffer.from_array(a), M.DeviceBuffer.from_array(b), M.DeviceBuffer(m * n * 4)
+    dc.fill(0xA5)
+    note(f"det_matmul_ws_dev q16 direct {m}x{k}x{n} (no workspace)")
+    M.check(L.det_matmul_ws_dev(M.DET_OP_Q16, da.ptr, db.ptr, dc.ptr, m, k, n, None, 0, s.ptr))
+    s.sync()
+    np.testing.assert_array_equal(dc.to_array(np.int32, (m, n)), want)
+    for buf in (da, db, dc):
+        buf.free()
+    s.destroy()
+
+
 def test_gemm_q16_saturating_config_and_bt():
     m, k, n = 96, 257, 80
     a, b = O.gen_q16_sat(0x9A7, m * k, k * n, shift=13)
@@ -973,10 +1010,12 @@ def test_gemm_q16_long_k_flush():
     np.testing.assert_array_equal(M.det_matmul_q16(a.reshape(m, k), b.reshape(k, n)), O.gemm_q16(a, b, m, k, n))
 
 
+@pytest.mark.parametrize("shape", [(200, 1000, 136), (1100, 1000, 1000)], ids=["direct", "limb"])
 @pytest.mark.parametrize("gen", ["full", "sat"])
-def test_gemm_q16_multi_tile(gen):
-    # several 64x64 tiles, ragged in M and N, K not a multiple of 64
-    m, k, n = 200, 1000, 136
+def test_gemm_q16_multi_tile(gen, shape):
+    # several tiles, ragged in M and N, K not a multiple of 64 (the first
+    # shape on the direct kernel, the second on the limb kernel)
+    m, k, n = shape
     if gen == "full":
         a, b = O.gen_q16(0x51DE, m * k, k * n, shift=0)
     else:
@@ -990,19 +1029,22 @@ def test_gemm_q16_multi_tile(gen):
     np.testing.assert_array_equal(c.reshape(m, n), want)
 
 
-# Grids of 64 x 64 tiles that fill at most half the CUs run split in K (up to
-# 8 partial sums per tile over whole 64-k steps, reduced by a second
-# kernel): 256^3 (16 tiles, 4 splits of one step), 512^3 (64 tiles, 4 splits
-# of two), 100 x 512 x 70 (4 ragged tiles, 8 splits), 1000 x 128 x 33 (2
-# splits), 7 x 1000 x 130 (K off the 64 grid, 8 splits), 300 x 320 x 200 (5
-# splits of one step), 200 x 576 x 500 (5 uneven splits: 1, 2, 2, 2, 2 steps).
-Q_SPLIT = [(256, 256, 256), (512, 512, 512), (100, 512, 70), (1000, 128, 33), (7, 1000, 130), (300, 320, 200),
-           (200, 576, 500)]
+# Shapes whose 16x16 tiles times K are too much for the direct kernel run
+# the limb kernel; its grids of 64 x 64 tiles that fill at most half the CUs
+# run split in K (up to 8 partial sums per tile over whole 64-k steps,
+# reduced by a second kernel): 7 x 5000 x 130 (3 tiles, K off the 64 grid,
+# splits of 9-10 steps), 100 x 4200 x 70 (4 ragged tiles, uneven splits),
+# 200 x 4160 x 300 (20 tiles), 1000 x 4100 x 33 (16 tiles, one column), 512 x
+# 2048 x 512 (64 tiles, 4 splits of 8 steps); 1000 x 100 x 1000 and 1024 x
+# 128 x 1024 fill the chip (no split; the first ragged in M, N and K).
+Q_SPLIT = [(7, 5000, 130), (100, 4200, 70), (200, 4160, 300), (1000, 4100, 33), (512, 2048, 512), (1000, 100, 1000),
+           (1024, 128, 1024)]
 
 
 @pytest.mark.parametrize("m,k,n", Q_SPLIT, ids=[f"{m}x{k}x{n}" for m, k, n in Q_SPLIT])
 def test_gemm_q16_k_split(m, k, n):
-    """The K-split route against the oracle: saturating inputs through the
+    """The limb route (split in K where the grid is small) against the
+    oracle: saturating inputs through the
     device workspace entry (the workspace, partials included, refilled with
     garbage before each call), and full-range inputs through gemmqmm and the
     B-transposed gemmq."""
@@ -1010,6 +1052,7 @@ def test_gemm_q16_k_split(m, k, n):
     a, b = O.gen_q16_sat(0x5A17 ^ (m * 7919 + k * 31 + n), m * k, k * n, shift=13)
     want = O.gemm_q16(a, b, m, k, n).reshape(m, n)
     wsb = L.det_workspace_bytes(M.DET_OP_Q16, m, k, n)
+    assert wsb > 0   # the limb route (the direct kernel needs no workspace)
     s = M.Stream()
     da, db, dc = M.DeviceBuffer.from_array(a), M.DeviceBuffer.from_array(b), M.DeviceBuffer(m * n * 4)
     ws = M.DeviceBuffer(wsb)
@@ -1159,10 +1202,13 @@ def test_dev_api_poisoned_outputs_and_run_to_run():
         M.check(M.lib().det_matmul_i8_dev(da.ptr, db.ptr, dc.ptr, m, k, n, s.ptr))
         s.sync()
         np.testing.assert_array_equal(dc.to_array(np.int32, (m, n)), want)
+    m, k, n = 1040, 200, 1040   # a Q16 shape on the limb kernel (which needs the workspace)
     aq, bq = O.gen_q16_sat(0xD0D1, m * k, k * n)
     wq = O.gemm_q16(aq, bq, m, k, n)
     daq, dbq = M.DeviceBuffer.from_array(aq), M.DeviceBuffer.from_array(bq)
+    dc = M.DeviceBuffer(m * n * 4)
     ws_bytes = M.lib().det_workspace_bytes(M.DET_OP_Q16, m, k, n)
+    assert ws_bytes > 16
     ws = M.DeviceBuffer(ws_bytes)
     for rep in range(4):
         dc.fill(0xA5)
@@ -1181,8 +1227,8 @@ def test_dev_api_poisoned_outputs_and_run_to_run():
     s.destroy()
 
 
-@pytest.mark.parametrize("op,m,k,n", [("i16", 64, 5000, 96), ("i16", 300, 1000, 270), ("q16", 64, 3000, 100),
-                                      ("q16", 130, 4096, 70)])
+@pytest.mark.parametrize("op,m,k,n", [("i16", 64, 5000, 96), ("i16", 300, 1000, 270), ("q16", 64, 5000, 100),
+                                      ("q16", 130, 4160, 70)])
 def test_ws_dev_exact_workspace_with_garbage(op, m, k, n):
     # the exact reported workspace, refilled with garbage before every call:
     # the preps write every column-sum partial they later read (several

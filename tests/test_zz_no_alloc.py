@@ -1,9 +1,10 @@
 """det_matmul_scratch_dev (the entry point that allocates nothing) against
 det_matmul_ws_dev (the existing workspace entry point) through the C ABI:
 bit-identical outputs on two calls in a row, the second smaller, for the
-int16 and Q16 limb GEMMs (which always use the scratch) and int8 (which uses
-it only to repack operands into padded panels); a limb-GEMM shape beyond
-the fixed scratch is rejected before any launch.  The property the entry
+int16 and Q16 limb GEMMs (which use the scratch; the Q16 shapes here are too
+large for the direct kernel, which needs none) and int8 (which uses it only
+to repack operands into padded panels); a limb-GEMM shape beyond the fixed
+scratch is rejected before any launch.  The property the entry
 point exists for is checked directly: after one warm-up call per op, further
 calls leave the device's free memory unchanged, and one call per op captured
 into a HIP graph (capture fails on hipMalloc or any synchronising call)
@@ -65,8 +66,12 @@ def test_scratch_entry_matches_workspace_entry_twice(op):
     L, f = _bind()
     s = M.Stream()
     # the second call is smaller: it reuses the scratch the first one filled
-    _run_both(L, f, op, 320, 1088, 272, 0x5C1, s)
-    _run_both(L, f, op, 70, 200, 52, 0x5C2, s)
+    # (Q16: both split in K, the partial sums in the scratch too)
+    first, second = ((200, 4160, 300), (100, 4200, 70)) if op == M.DET_OP_Q16 else ((320, 1088, 272), (70, 200, 52))
+    if op == M.DET_OP_Q16:
+        assert L.det_workspace_bytes(op, *first) > L.det_workspace_bytes(op, *second) > 0
+    _run_both(L, f, op, *first, 0x5C1, s)
+    _run_both(L, f, op, *second, 0x5C2, s)
     s.destroy()
 
 
@@ -87,7 +92,7 @@ def test_scratch_entry_q16_1024_cubed_then_smaller():
     s = M.Stream()
     assert L.det_workspace_bytes(M.DET_OP_Q16, 1024, 1024, 1024) <= 32 << 20
     _run_both(L, f, M.DET_OP_Q16, 1024, 1024, 1024, 0x5C3, s)
-    _run_both(L, f, M.DET_OP_Q16, 96, 4000, 64, 0x5C4, s)
+    _run_both(L, f, M.DET_OP_Q16, 96, 4160, 64, 0x5C4, s)
     s.destroy()
 
 
@@ -134,10 +139,11 @@ def test_scratch_entry_allocates_nothing_and_captures_into_a_graph():
     L, f = _bind()
     H = _hip()
     s = M.Stream()
-    # one shape per op within the scratch; the int8 one off the 16-byte grid,
-    # so its panels come from the scratch
-    cases = [(M.DET_OP_Q16, 256, 512, 192, 0x5D1), (M.DET_OP_I16, 320, 1088, 272, 0x5D2),
-             (M.DET_OP_I8, 300, 1000, 77, 0x5D3)]
+    # one shape per op within the scratch (Q16: one on the limb kernel split
+    # in K, one on the direct kernel, which uses no scratch); the int8 one off
+    # the 16-byte grid, so its panels come from the scratch
+    cases = [(M.DET_OP_Q16, 200, 4160, 300, 0x5D1), (M.DET_OP_Q16, 256, 512, 192, 0x5D4),
+             (M.DET_OP_I16, 320, 1088, 272, 0x5D2), (M.DET_OP_I8, 300, 1000, 77, 0x5D3)]
     bufs = []
     for op, m, k, n, seed in cases:
         a, b, want = _inputs(op, m, k, n, seed)
