@@ -53,6 +53,8 @@ struct DevState {
     hipStream_t stream = nullptr;      // library stream for host-pointer calls
     void *io = nullptr;                // staging for host-pointer operands
     size_t io_bytes = 0;
+    void *pin = nullptr;               // pinned host staging for small host-pointer calls
+    void *pin_dev = nullptr;           // the same memory as the kernels address it
     void *ws = nullptr;                // limb-GEMM workspace
     size_t ws_bytes = 0;
     hipEvent_t ws_free = nullptr;      // recorded after the last workspace user
@@ -111,10 +113,11 @@ int64_t release_device(DevState &ds) {
     if (ds.stream) step(hipStreamSynchronize(ds.stream), "hipStreamSynchronize");
     if (ds.ws_free) step(hipEventSynchronize(ds.ws_free), "hipEventSynchronize");
     if (ds.io) step(hipFree(ds.io), "hipFree(staging)");
+    if (ds.pin) step(hipHostFree(ds.pin), "hipHostFree(staging)");
     if (ds.ws) step(hipFree(ds.ws), "hipFree(workspace)");
     if (ds.ws_free) step(hipEventDestroy(ds.ws_free), "hipEventDestroy");
     if (ds.stream) step(hipStreamDestroy(ds.stream), "hipStreamDestroy");
-    ds.io = ds.ws = nullptr;
+    ds.io = ds.ws = ds.pin = ds.pin_dev = nullptr;
     ds.io_bytes = ds.ws_bytes = 0;
     ds.ws_free = nullptr;
     ds.stream = nullptr;
@@ -128,7 +131,7 @@ int64_t release_all() {
     for (int d = 0; d < MAX_DEV; ++d) {
         DevState &ds = g_dev[d];
         std::lock_guard<std::mutex> lock(ds.mu);
-        if (!ds.stream && !ds.ws_free && !ds.io && !ds.ws) continue;
+        if (!ds.stream && !ds.ws_free && !ds.io && !ds.ws && !ds.pin) continue;
         hipError_t e = hipSetDevice(d);
         int64_t r = e == hipSuccess ? release_device(ds) : det_fail_hip(e, "hipSetDevice");
         if (r && rc == 0) rc = r;
@@ -137,6 +140,103 @@ int64_t release_all() {
     return rc;
 }
 
+
+// ------------------------------------------------ host-pointer transfers
+// Operands of a host-pointer call occupy one layout in the device staging
+// buffer `io` (each at a 256-byte offset).  When the whole layout fits in
+// PIN_BYTES it travels through a pinned host buffer of the same layout: the
+// CPU copies the inputs into it, one kernel moves the input span into `io`
+// (reading host memory over PCIe), and after the compute kernels another
+// moves the output span back; the stream is synchronised and the CPU copies
+// the outputs out.  A DMA copy costs about 10 us of latency here, from
+// pageable and pinned memory alike, so a small call with three or four of
+// them spent most of its time there; two kernels on the same stream cost a
+// few microseconds.  Larger layouts use hipMemcpyAsync on the caller's
+// buffers (PCIe bandwidth, no extra CPU copy); at about 3 MiB the two routes
+// measured even.
+constexpr size_t PIN_BYTES = 4u << 20;
+
+struct HostIn {
+    size_t off;
+    const void *src;
+    size_t bytes;
+};
+struct HostOut {
+    size_t off;
+    void *dst;
+    size_t bytes;
+};
+
+__global__ __launch_bounds__(256) void copy16_kernel(uint4 *__restrict__ dst, const uint4 *__restrict__ src,
+                                                     size_t n) {
+    for (size_t i = (size_t)blockIdx.x * 256 + threadIdx.x; i < n; i += (size_t)gridDim.x * 256) dst[i] = src[i];
+}
+
+hipError_t copy16(void *dst, const void *src, size_t bytes, hipStream_t s) {
+    const size_t n = (bytes + 15) / 16;
+    if (n == 0) return hipSuccess;
+    const size_t blocks = (n + 255) / 256;
+    hipLaunchKernelGGL(copy16_kernel, dim3((unsigned)(blocks < 1024 ? blocks : 1024)), dim3(256), 0, s, (uint4 *)dst,
+                       (const uint4 *)src, n);
+    return hipGetLastError();
+}
+
+// True when a layout of `span` bytes takes the pinned route (the buffer is
+// allocated on the first such call and kept until teardown).
+bool pinned_route(DevState &ds, size_t span, int64_t *rc) {
+    *rc = 0;
+    if (span > PIN_BYTES) return false;
+    if (!ds.pin) {
+        hipError_t e = hipHostMalloc(&ds.pin, PIN_BYTES, hipHostMallocDefault);
+        if (e == hipSuccess) e = hipHostGetDevicePointer(&ds.pin_dev, ds.pin, 0);
+        if (e != hipSuccess) {
+            if (ds.pin) (void)hipHostFree(ds.pin);
+            ds.pin = ds.pin_dev = nullptr;
+            *rc = det_fail_hip(e, "hipHostMalloc(staging)");
+            return false;
+        }
+    }
+    return true;
+}
+
+// Inputs into io (asynchronous on s).
+int64_t put_inputs(DevState &ds, bool pinned, const HostIn *in, int n_in, hipStream_t s) {
+    char *io = (char *)ds.io;
+    if (!pinned) {
+        for (int i = 0; i < n_in; ++i)
+            if (in[i].bytes) DET_HIP_CHECK(hipMemcpyAsync(io + in[i].off, in[i].src, in[i].bytes, hipMemcpyHostToDevice, s));
+        return 0;
+    }
+    size_t end = 0;
+    for (int i = 0; i < n_in; ++i) {
+        if (in[i].bytes) memcpy((char *)ds.pin + in[i].off, in[i].src, in[i].bytes);
+        if (in[i].off + in[i].bytes > end) end = in[i].off + in[i].bytes;
+    }
+    DET_HIP_CHECK(copy16(io, ds.pin_dev, end, s));
+    return 0;
+}
+
+// Outputs out of io, then wait for the stream.  The outputs' offsets are
+// 256-byte aligned, so the span copied back starts on a 16-byte boundary.
+int64_t get_outputs(DevState &ds, bool pinned, const HostOut *out, int n_out, hipStream_t s) {
+    char *io = (char *)ds.io;
+    if (!pinned) {
+        for (int i = 0; i < n_out; ++i)
+            if (out[i].bytes) DET_HIP_CHECK(hipMemcpyAsync(out[i].dst, io + out[i].off, out[i].bytes, hipMemcpyDeviceToHost, s));
+        DET_HIP_CHECK(hipStreamSynchronize(s));
+        return 0;
+    }
+    size_t lo = (size_t)-1, hi = 0;
+    for (int i = 0; i < n_out; ++i) {
+        if (out[i].off < lo) lo = out[i].off;
+        if (out[i].off + out[i].bytes > hi) hi = out[i].off + out[i].bytes;
+    }
+    if (hi > lo) DET_HIP_CHECK(copy16((char *)ds.pin_dev + lo, io + lo, hi - lo, s));
+    DET_HIP_CHECK(hipStreamSynchronize(s));
+    for (int i = 0; i < n_out; ++i)
+        if (out[i].bytes) memcpy(out[i].dst, (const char *)ds.pin + out[i].off, out[i].bytes);
+    return 0;
+}
 
 bool bad_dims(int64_t m, int64_t k, int64_t n) {
     return m < 0 || k < 0 || n < 0 || m > DIM_MAX || k > DIM_MAX || n > DIM_MAX;
@@ -224,20 +324,22 @@ int64_t gemm_host(Op op, int64_t a, int64_t b, int64_t c, int64_t m, int64_t k, 
     const size_t eb = elem_bytes(op);
     const size_t bytes_a = (size_t)m * k * eb, bytes_b = (size_t)k * n * eb, bytes_c = (size_t)m * n * 4;
     const size_t off_b = align256(bytes_a), off_c = off_b + align256(bytes_b);
-    if ((rc = ensure(&ds.io, &ds.io_bytes, off_c + align256(bytes_c)))) return rc;
-    if ((rc = ensure(&ds.ws, &ds.ws_bytes, ws_need(op, m, k, n)))) return rc;
+    const size_t span = off_c + align256(bytes_c), need = ws_need(op, m, k, n);
+    if ((rc = ensure(&ds.io, &ds.io_bytes, span))) return rc;
+    if ((rc = ensure(&ds.ws, &ds.ws_bytes, need))) return rc;
+    const bool pinned = pinned_route(ds, span, &rc);
+    if (rc) return rc;
     char *io = (char *)ds.io;
     hipStream_t s = ds.stream;
-    if (bytes_a) DET_HIP_CHECK(hipMemcpyAsync(io, (const void *)a, bytes_a, hipMemcpyHostToDevice, s));
-    if (bytes_b) DET_HIP_CHECK(hipMemcpyAsync(io + off_b, (const void *)b, bytes_b, hipMemcpyHostToDevice, s));
+    const HostIn in[2] = {{0, (const void *)a, bytes_a}, {off_b, (const void *)b, bytes_b}};
+    if ((rc = put_inputs(ds, pinned, in, 2, s))) return rc;
     // the workspace arena is shared with the device-pointer entry points:
     // start after its last user, and mark this stream as its next one
-    DET_HIP_CHECK(hipStreamWaitEvent(s, ds.ws_free, 0));
-    if ((rc = gemm_dev(op, io, io + off_b, io + off_c, m, k, n, ds.ws, s))) return rc;
-    DET_HIP_CHECK(hipEventRecord(ds.ws_free, s));
-    DET_HIP_CHECK(hipMemcpyAsync((void *)c, io + off_c, bytes_c, hipMemcpyDeviceToHost, s));
-    DET_HIP_CHECK(hipStreamSynchronize(s));
-    return 0;
+    if (need) DET_HIP_CHECK(hipStreamWaitEvent(s, ds.ws_free, 0));
+    if ((rc = gemm_dev(op, io, io + off_b, io + off_c, m, k, n, need ? ds.ws : nullptr, s))) return rc;
+    if (need) DET_HIP_CHECK(hipEventRecord(ds.ws_free, s));
+    const HostOut out[1] = {{off_c, (void *)c, bytes_c}};
+    return get_outputs(ds, pinned, out, 1, s);
 }
 
 // Q16 GEMV over nb vectors on device pointers: groups of up to 8 vectors go
@@ -277,11 +379,14 @@ int64_t gemv_host(bool q16, int64_t w, int64_t x, int64_t y, int64_t m, int64_t 
     const size_t eb = q16 ? 4 : 2;
     const size_t bytes_w = (size_t)m * k * eb, bytes_x = (size_t)nb * k * eb, bytes_y = (size_t)nb * m * 4;
     const size_t off_x = align256(bytes_w), off_y = off_x + align256(bytes_x);
-    if ((rc = ensure(&ds.io, &ds.io_bytes, off_y + align256(bytes_y)))) return rc;
+    const size_t span = off_y + align256(bytes_y);
+    if ((rc = ensure(&ds.io, &ds.io_bytes, span))) return rc;
+    const bool pinned = pinned_route(ds, span, &rc);
+    if (rc) return rc;
     char *io = (char *)ds.io;
     hipStream_t s = ds.stream;
-    if (bytes_w) DET_HIP_CHECK(hipMemcpyAsync(io, (const void *)w, bytes_w, hipMemcpyHostToDevice, s));
-    if (bytes_x) DET_HIP_CHECK(hipMemcpyAsync(io + off_x, (const void *)x, bytes_x, hipMemcpyHostToDevice, s));
+    const HostIn in[2] = {{0, (const void *)w, bytes_w}, {off_x, (const void *)x, bytes_x}};
+    if ((rc = put_inputs(ds, pinned, in, 2, s))) return rc;
     if (k == 0) DET_HIP_CHECK(zero_i32((int32_t *)(io + off_y), (size_t)nb * m, s));
     else if (q16) {
         const int32_t *dW = (const int32_t *)io, *dX = (const int32_t *)(io + off_x);
@@ -295,9 +400,8 @@ int64_t gemv_host(bool q16, int64_t w, int64_t x, int64_t y, int64_t m, int64_t 
     } else
         DET_HIP_CHECK(det::launch_gemv_i16((const int16_t *)io, (const int16_t *)(io + off_x),
                                            (int32_t *)(io + off_y), (int)m, (int)k, s));
-    DET_HIP_CHECK(hipMemcpyAsync((void *)y, io + off_y, bytes_y, hipMemcpyDeviceToHost, s));
-    DET_HIP_CHECK(hipStreamSynchronize(s));
-    return 0;
+    const HostOut out[1] = {{off_y, (void *)y, bytes_y}};
+    return get_outputs(ds, pinned, out, 1, s);
 }
 
 // Host-pointer vector reductions: (int64)(int32)sum; len <= 0 or a NULL
@@ -313,16 +417,19 @@ int64_t dot_host(int op, int64_t a, int64_t b, int64_t len) {
     if ((rc = ensure_stream(ds))) return rc;
     const size_t eb = op == det::DOT_I16 ? 2 : 4, bytes = (size_t)len * eb;
     const size_t off_b = align256(bytes), off_o = off_b + align256(bytes);
-    if ((rc = ensure(&ds.io, &ds.io_bytes, off_o + 256))) return rc;
+    const size_t span = off_o + 256;
+    if ((rc = ensure(&ds.io, &ds.io_bytes, span))) return rc;
+    const bool pinned = pinned_route(ds, span, &rc);
+    if (rc) return rc;
     char *io = (char *)ds.io;
     hipStream_t s = ds.stream;
-    DET_HIP_CHECK(hipMemcpyAsync(io, (const void *)a, bytes, hipMemcpyHostToDevice, s));
-    DET_HIP_CHECK(hipMemcpyAsync(io + off_b, (const void *)b, bytes, hipMemcpyHostToDevice, s));
+    const HostIn in[2] = {{0, (const void *)a, bytes}, {off_b, (const void *)b, bytes}};
+    if ((rc = put_inputs(ds, pinned, in, 2, s))) return rc;
     DET_HIP_CHECK(det::launch_dot(op, io, io + off_b, len, (uint32_t *)(io + off_o), s));
-    uint32_t out = 0;
-    DET_HIP_CHECK(hipMemcpyAsync(&out, io + off_o, 4, hipMemcpyDeviceToHost, s));
-    DET_HIP_CHECK(hipStreamSynchronize(s));
-    return (int64_t)(int32_t)out;
+    uint32_t res = 0;
+    const HostOut out[1] = {{off_o, &res, 4}};
+    if ((rc = get_outputs(ds, pinned, out, 1, s))) return rc;
+    return (int64_t)(int32_t)res;
 }
 
 // Host-pointer strict-FP f32 rows: y[r] = metric met of (W row r, x).
@@ -337,16 +444,18 @@ int64_t f32_rows_host(const float *w, const float *x, float *y, int64_t rows, in
     if ((rc = ensure_stream(ds))) return rc;
     const size_t bytes_w = (size_t)rows * cols * 4, bytes_x = (size_t)cols * 4, bytes_y = (size_t)rows * 4;
     const size_t off_x = align256(bytes_w), off_y = off_x + align256(bytes_x);
-    if ((rc = ensure(&ds.io, &ds.io_bytes, off_y + align256(bytes_y)))) return rc;
+    const size_t span = off_y + align256(bytes_y);
+    if ((rc = ensure(&ds.io, &ds.io_bytes, span))) return rc;
+    const bool pinned = pinned_route(ds, span, &rc);
+    if (rc) return rc;
     char *io = (char *)ds.io;
     hipStream_t s = ds.stream;
-    DET_HIP_CHECK(hipMemcpyAsync(io, w, bytes_w, hipMemcpyHostToDevice, s));
-    DET_HIP_CHECK(hipMemcpyAsync(io + off_x, x, bytes_x, hipMemcpyHostToDevice, s));
+    const HostIn in[2] = {{0, w, bytes_w}, {off_x, x, bytes_x}};
+    if ((rc = put_inputs(ds, pinned, in, 2, s))) return rc;
     DET_HIP_CHECK(det::launch_rows_f32((const float *)io, (const float *)(io + off_x), (float *)(io + off_y), rows,
                                        cols, met, s));
-    DET_HIP_CHECK(hipMemcpyAsync(y, io + off_y, bytes_y, hipMemcpyDeviceToHost, s));
-    DET_HIP_CHECK(hipStreamSynchronize(s));
-    return 0;
+    const HostOut out[1] = {{off_y, y, bytes_y}};
+    return get_outputs(ds, pinned, out, 1, s);
 }
 
 // The reference's packing of an f32 result: its bits, zero-extended to int64.
@@ -418,23 +527,24 @@ int64_t fft_host(int64_t re, int64_t im, int64_t tw, int64_t logn, int64_t n, in
     if ((rc = ensure_stream(ds))) return rc;
     const size_t bytes = (size_t)batch * n * 8, bytes_tw = n >= 4 ? (size_t)n * 8 : 0;
     const size_t off_im = align256(bytes), off_tw = off_im + align256(bytes);
-    if ((rc = ensure(&ds.io, &ds.io_bytes, off_tw + align256(bytes_tw) + 256))) return rc;
+    const size_t span = off_tw + align256(bytes_tw) + 256;
+    if ((rc = ensure(&ds.io, &ds.io_bytes, span))) return rc;
     const size_t need = det::fft_workspace_bytes((int)logn, batch);
     if ((rc = ensure(&ds.ws, &ds.ws_bytes, need))) return rc;
+    const bool pinned = pinned_route(ds, span, &rc);
+    if (rc) return rc;
     char *io = (char *)ds.io;
     hipStream_t s = ds.stream;
-    DET_HIP_CHECK(hipMemcpyAsync(io, (const void *)re, bytes, hipMemcpyHostToDevice, s));
-    DET_HIP_CHECK(hipMemcpyAsync(io + off_im, (const void *)im, bytes, hipMemcpyHostToDevice, s));
-    if (bytes_tw) DET_HIP_CHECK(hipMemcpyAsync(io + off_tw, (const void *)tw, bytes_tw, hipMemcpyHostToDevice, s));
+    const HostIn in[3] = {{0, (const void *)re, bytes}, {off_im, (const void *)im, bytes},
+                          {off_tw, (const void *)tw, bytes_tw}};
+    if ((rc = put_inputs(ds, pinned, in, 3, s))) return rc;
     if (need) DET_HIP_CHECK(hipStreamWaitEvent(s, ds.ws_free, 0));
     int64_t *dre = (int64_t *)io, *dim = (int64_t *)(io + off_im);
     DET_HIP_CHECK(det::launch_fft_q16(dre, dim, dre, dim, (const int64_t *)(io + off_tw), (int)logn, batch,
                                       need ? ds.ws : nullptr, s));
     if (need) DET_HIP_CHECK(hipEventRecord(ds.ws_free, s));
-    DET_HIP_CHECK(hipMemcpyAsync((void *)re, io, bytes, hipMemcpyDeviceToHost, s));
-    DET_HIP_CHECK(hipMemcpyAsync((void *)im, io + off_im, bytes, hipMemcpyDeviceToHost, s));
-    DET_HIP_CHECK(hipStreamSynchronize(s));
-    return 0;
+    const HostOut out[2] = {{0, (void *)re, bytes}, {off_im, (void *)im, bytes}};
+    return get_outputs(ds, pinned, out, 2, s);
 }
 
 }  // namespace

@@ -538,6 +538,47 @@ def test_fft_argument_conventions():
 
 # ------------------------------------------------------------------ concurrency
 
+# Host-pointer calls whose operand layout (inputs, output, each rounded up to
+# 256 bytes) fits in 4 MiB travel through the library's pinned staging buffer
+# and two copy kernels; larger ones use DMA copies of the caller's buffers.
+# One call on each side of the limit per family, checked whole, then the small
+# one again (the pinned buffer keeps the large call's bytes past its end).
+HOST_ROUTES = [("gemmi8", 768, 3 << 20), ("gemmi8", 1024, 6 << 20), ("gemvq", 2048, 2 << 20), ("gemvq", 8192, 8 << 20),
+               ("dotq", 1 << 18, 2 << 20), ("dotq", 1 << 20, 8 << 20), ("fft256", 600, 3 << 20), ("fft256", 2000, 8 << 20)]
+
+
+@pytest.mark.parametrize("sym,size,span", HOST_ROUTES, ids=[f"{s}-{n}" for s, n, _ in HOST_ROUTES])
+def test_host_staging_routes(sym, size, span):
+    L = M.lib()
+    small = {"gemmi8": 64, "gemvq": 64, "dotq": 1000, "fft256": 3}[sym]
+    for n in (size, small):
+        note(f"host {sym} size={n} (layout ~{span >> 20} MiB when large)")
+        if sym == "gemmi8":
+            a, b = O.gen_i8(0x4A5 ^ n, n * n, n * n)
+            c = np.full(n * n, 0x5A5A5A5A, np.int32)
+            assert L.gemmi8(addr(a), addr(b), addr(c), n, n, n) == 0
+            rows = _sample_rows(n, 16)
+            np.testing.assert_array_equal(c.reshape(n, n)[rows], O.gemm_i8_rows(a, b, n, n, n, rows))
+        elif sym == "gemvq":
+            k = 256
+            W, x = O.gen_q16(0x4A6 ^ n, n * k, k, shift=0)
+            y = np.full(n, 0x5A5A5A5A, np.int32)
+            assert L.gemvq(addr(W), addr(x), addr(y), n, k) == 0
+            np.testing.assert_array_equal(y, O.gemv_q16(W, x, n, k))
+        elif sym == "dotq":
+            a, b = O.gen_q16(0x4A7 ^ n, n, n, shift=0)
+            assert M.dot_q16(a, b) == O.dot_q16(a, b)
+        else:
+            logn, nfft = 8, 256
+            x = np.random.default_rng(n).integers(-(1 << 30), 1 << 30, (2, n, nfft))
+            re, im = np.ascontiguousarray(x[0]), np.ascontiguousarray(x[1])
+            tw = O.fft_twiddles(nfft)
+            got = M.fft_q16(re, im, tw, logn)
+            sel = sorted({0, n // 2, n - 1})
+            want = _fft_oracle_batch(re[sel], im[sel], tw, logn)
+            assert np.array_equal(got[0][sel], want[0]) and np.array_equal(got[1][sel], want[1])
+
+
 def test_host_abi_concurrent_callers():
     # The host-pointer entry points are called from several threads at once
     # (ctypes releases the GIL): one device mutex serialises them, the
