@@ -1434,6 +1434,7 @@ static bool i8_edge_underfills(int M, int N, int K) {
 }
 
 size_t i8_workspace_bytes(int M, int N, int K, bool aligned) {
+    if (i8_small(M, N, K)) return 0;
     const size_t Mp = round256(M), Kp = round256(K), Np = round256(N);
     const bool grid16 = K % 16 == 0 && N % 16 == 0 && aligned;
     if (K == 0 || Mp * Kp >= 0x80000000ull || Kp * Np >= 0x80000000ull) return 0;
@@ -1503,6 +1504,7 @@ static void launch_i8_on_grid(const int8_t *A, const int8_t *B, int32_t *C, int 
 hipError_t launch_gemm_i8(const int8_t *A, const int8_t *B, int32_t *C, int M, int N, int K, void *ws,
                           hipStream_t s) {
     using namespace i8g;
+    if (i8_small(M, N, K)) return launch_gemm_i8_small(A, B, C, M, N, K, s);
     const bool aligned = (((uintptr_t)A & 15) == 0) && (((uintptr_t)B & 15) == 0);
     const size_t pad = i8_workspace_bytes(M, N, K, aligned);
     if (i8_fast(A, B, M, N, K) && !(pad && ws)) {

@@ -721,6 +721,31 @@ def test_gemm_i8_repack_rule_leaves_small_grids_alone():
         assert L.det_workspace_bytes(M.DET_OP_I8, m, k, n) > 0, (m, k, n)
 
 
+# Shapes whose 16x16 output tiles fit one round of the CUs take the direct
+# v_dot4 kernel while K <= 512, or K <= 4096 when M, N or K is not a multiple
+# of 128 (any alignment, no workspace); just past either bound the MFMA
+# kernels take over (256x640x256, 16x4097x16, 272x16x256: 17 x 16 tiles).
+I8_DIRECT = [(16, 16, 16), (1, 4096, 1), (16, 4096, 16), (256, 512, 256), (255, 4096, 255), (17, 33, 65),
+             (5, 1000, 300)]
+I8_DIRECT_EDGE = [(256, 640, 256), (16, 4097, 16), (272, 16, 256)]
+
+
+@pytest.mark.parametrize("m,k,n", I8_DIRECT + I8_DIRECT_EDGE, ids=[f"{m}x{k}x{n}" for m, k, n in I8_DIRECT + I8_DIRECT_EDGE])
+def test_gemm_i8_direct_route(m, k, n):
+    L = M.lib()
+    if (m, k, n) in I8_DIRECT:
+        assert L.det_workspace_bytes(M.DET_OP_I8, m, k, n) == 0
+    a, b = O.gen_i8(0x1D5 ^ (m * 1000003 + k * 1009 + n), m * k, k * n)
+    want = O.gemm_i8(a, b, m, k, n).reshape(m, n)
+    note(f"det_matmul_i8 direct-route boundary {m}x{k}x{n}")
+    np.testing.assert_array_equal(M.det_matmul_i8(a.reshape(m, k), b.reshape(k, n)), want)
+    # extreme operands: every product is 127 * 127, 127 * -128 or -128 * -128
+    a2 = np.where(np.arange(m * k) % 3 == 0, -128, 127).astype(np.int8)
+    b2 = np.where(np.arange(k * n) % 5 == 0, 127, -128).astype(np.int8)
+    np.testing.assert_array_equal(M.det_matmul_i8(a2.reshape(m, k), b2.reshape(k, n)),
+                                  O.gemm_i8(a2, b2, m, k, n).reshape(m, n))
+
+
 @pytest.mark.parametrize("m,k,n", I8_SHAPES, ids=[f"{m}x{k}x{n}" for m, k, n in I8_SHAPES])
 def test_gemm_i8_shapes(m, k, n):
     a, b = O.gen_i8(0xDEADBEEF00000000 ^ (m * 1000003 + k * 1009 + n), m * k, k * n)

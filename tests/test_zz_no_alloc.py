@@ -76,14 +76,16 @@ def test_scratch_entry_matches_workspace_entry_twice(op):
 
 
 def test_scratch_entry_int8_repack_twice():
-    # both shapes are off the 16-byte grid (K % 16 != 0): their padded panels
-    # come from the scratch, the second call's smaller ones over the first's
+    # both shapes are off the 16-byte grid (K % 16 != 0) and too large for
+    # the direct kernel: their padded panels come from the scratch, the
+    # second call's smaller ones over the first's
     L, f = _bind()
     s = M.Stream()
-    for shape in ((300, 1000, 77), (37, 100, 53)):
+    for shape in ((1000, 1000, 77), (700, 200, 90)):
         assert 0 < L.det_workspace_bytes(M.DET_OP_I8, *shape) <= 32 << 20
-    _run_both(L, f, M.DET_OP_I8, 300, 1000, 77, 0x5C5, s)
-    _run_both(L, f, M.DET_OP_I8, 37, 100, 53, 0x5C6, s)
+    assert L.det_workspace_bytes(M.DET_OP_I8, 1000, 1000, 77) > L.det_workspace_bytes(M.DET_OP_I8, 700, 200, 90)
+    _run_both(L, f, M.DET_OP_I8, 1000, 1000, 77, 0x5C5, s)
+    _run_both(L, f, M.DET_OP_I8, 700, 200, 90, 0x5C6, s)
     s.destroy()
 
 
@@ -143,7 +145,7 @@ def test_scratch_entry_allocates_nothing_and_captures_into_a_graph():
     # in K, one on the direct kernel, which uses no scratch); the int8 one off
     # the 16-byte grid, so its panels come from the scratch
     cases = [(M.DET_OP_Q16, 200, 4160, 300, 0x5D1), (M.DET_OP_Q16, 256, 512, 192, 0x5D4),
-             (M.DET_OP_I16, 320, 1088, 272, 0x5D2), (M.DET_OP_I8, 300, 1000, 77, 0x5D3)]
+             (M.DET_OP_I16, 320, 1088, 272, 0x5D2), (M.DET_OP_I8, 1000, 1000, 77, 0x5D3)]
     bufs = []
     for op, m, k, n, seed in cases:
         a, b, want = _inputs(op, m, k, n, seed)
