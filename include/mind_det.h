@@ -239,8 +239,12 @@ int64_t det_fft_q16_dev(int64_t *re, int64_t *im, const int64_t *tw, int64_t log
 int64_t det_fft_q16_oop_dev(const int64_t *in_re, const int64_t *in_im, int64_t *out_re, int64_t *out_im,
                             const int64_t *tw, int64_t logn, int64_t n, int64_t batch, void *stream);
 int64_t det_fft_workspace_bytes(int64_t logn, int64_t batch);
-/* Workspace bytes op (DET_OP_*) needs at this shape.  int8 needs one only
- * when K or N is not a multiple of 16: its operands are then repacked into
+/* Workspace bytes op (DET_OP_*) needs at this shape.  int8 needs none for
+ * tiny shapes (16 x 16 output tiles within one round of the compute units,
+ * K <= 512, or K <= 4096 unless M, N and K are multiples of 128: every cube
+ * up to 256^3), which a direct kernel takes at any alignment.  Otherwise it
+ * needs one only when K or N is not a multiple of 16: its operands are then
+ * repacked into
  * aligned zero-padded panels of Mp*Kp + Kp*Np bytes (M, K, N rounded up to
  * 256).  int8 operands that are not 16-byte aligned are repacked the same
  * way when the workspace given holds that size, and so are aligned shapes
