@@ -239,27 +239,28 @@ int64_t det_fft_q16_dev(int64_t *re, int64_t *im, const int64_t *tw, int64_t log
 int64_t det_fft_q16_oop_dev(const int64_t *in_re, const int64_t *in_im, int64_t *out_re, int64_t *out_im,
                             const int64_t *tw, int64_t logn, int64_t n, int64_t batch, void *stream);
 int64_t det_fft_workspace_bytes(int64_t logn, int64_t batch);
-/* Workspace bytes op (DET_OP_*) needs at this shape.  int8 needs none for
- * tiny shapes (16 x 16 output tiles within one round of the compute units,
- * K <= 512, or K <= 4096 unless M, N and K are multiples of 128: every cube
- * up to 256^3), which a direct kernel takes at any alignment.  Otherwise it
- * needs one only when K or N is not a multiple of 16: its operands are then
- * repacked into
- * aligned zero-padded panels of Mp*Kp + Kp*Np bytes (M, K, N rounded up to
- * 256).  int8 operands that are not 16-byte aligned are repacked the same
- * way when the workspace given holds that size, and so are aligned shapes
- * of at least 256 rows and columns that no 128-row kernel takes, whose
- * 256 x 256 tiles would not fill one round of the GPU and whose padding to
- * multiples of 256 adds at most 1/8 per dimension (e.g. 1008^3), where the
- * padded panels run faster.  For int8 the workspace is
- * optional: without it such operands run a slower byte-load kernel;
- * det_matmul_ws_dev rejects a short workspace only for int16 / Q16.  Q16
- * shapes small enough for the direct kernel (16 x 16 output tiles filling at
- * most 4 rounds of the compute units, rounds times K at most 4096, e.g.
- * every cube up to 512^3) need none (0).  The figure holds for the current
- * device: that rule, and the K split of mid-size Q16 grids that keeps its
- * partial sums in the workspace, depend on the device's compute-unit count
- * (ask on the device that runs the call). */
+/* Workspace bytes op (DET_OP_*) needs at this shape (0 = none).
+ *  - Tiny shapes run direct kernels that need none: int8 when its 16 x 16
+ *    output tiles fit one round of the compute units and K <= 512, or
+ *    K <= 4096 unless M, N and K are all multiples of 128 (every cube up to
+ *    256^3, at any alignment); int16 under the same tile bound with
+ *    K <= 4096; Q16 when those tiles fill at most 4 rounds and rounds times
+ *    K is at most 4096 (every cube up to 512^3).
+ *  - Otherwise int8 needs one only when K or N is not a multiple of 16: its
+ *    operands are then repacked into aligned zero-padded panels of
+ *    Mp*Kp + Kp*Np bytes (M, K, N rounded up to 256).  int8 operands that
+ *    are not 16-byte aligned are repacked the same way when the workspace
+ *    given holds that size, and so are aligned shapes of at least 256 rows
+ *    and columns that no 128-row kernel takes, whose 256 x 256 tiles would
+ *    not fill one round of the GPU and whose padding to multiples of 256 adds
+ *    at most 1/8 per dimension (e.g. 1008^3), where the padded panels run
+ *    faster.  For int8 the workspace is optional: without it such operands
+ *    run a slower byte-load kernel; det_matmul_ws_dev rejects a short
+ *    workspace only for int16 / Q16.
+ *  - The figure holds for the current device: the rules above and the K
+ *    split of mid-size Q16 grids (which keeps its partial sums in the
+ *    workspace) depend on the device's compute-unit count, so ask on the
+ *    device that runs the call. */
 int64_t det_workspace_bytes(int64_t op, int64_t m, int64_t k, int64_t n);
 int64_t det_matmul_ws_dev(int64_t op, const void *a, const void *b, int32_t *c, int64_t m, int64_t k, int64_t n,
                           void *ws, int64_t ws_bytes, void *stream);

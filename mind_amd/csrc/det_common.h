@@ -15,6 +15,7 @@ namespace det {
 typedef long v2i64 __attribute__((ext_vector_type(2)));
 typedef int v4i32 __attribute__((ext_vector_type(4)));
 typedef unsigned short v2u16 __attribute__((ext_vector_type(2)));
+typedef short v2i16 __attribute__((ext_vector_type(2)));
 
 // ---------------------------------------------------------------- MFMA
 // v_mfma_i32_16x16x64_i8: D[16x16] += A[16x64] * B[64x16], int8 in, i32 out.

@@ -367,12 +367,14 @@ hipError_t launch_gemm_q16(const int32_t *A, const int32_t *B, int32_t *C, int M
 }
 
 size_t i16_workspace_bytes(int M, int N, int K) {
+    if (i16_small(M, N, K)) return 0;
     const size_t a = limb_workspace_bytes(M, N, K, 2, false), b = i16x_workspace_bytes(M, N, K);
     return a > b ? a : b;
 }
 
 hipError_t launch_gemm_i16(const int16_t *A, const int16_t *B, int32_t *C, int M, int N, int K, void *ws,
                            hipStream_t s) {
+    if (i16_small(M, N, K)) return launch_gemm_i16_small(A, B, C, M, N, K, s);
     if (i16x_eligible(M, N, K)) return launch_gemm_i16x(A, B, C, M, N, K, ws, s);
     return launch_limb<int16_t, 2, false>(A, B, C, M, N, K, false, ws, s);
 }

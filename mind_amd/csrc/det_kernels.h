@@ -24,13 +24,18 @@ constexpr int MAX_CS = 16;
 // N, K, aligned) bytes (0 for every other shape; with ws == NULL they take
 // the byte-load or edge kernel instead).
 size_t i8_workspace_bytes(int M, int N, int K, bool aligned);
-// Tiny int8 shapes (det_gemm_i8s.hip): one direct v_dot4 launch, no
+// Tiny int8 shapes (det_gemm_small.hip): one direct v_dot4 launch, no
 // workspace, any alignment, when the 16x16 output tiles fit one round of the
 // compute units and K <= I8_SMALL_K, or K <= I8_SMALL_K_ODD for shapes the
 // full-tile MFMA kernels do not take (M, N or K not a multiple of 128).
 constexpr long long I8_SMALL_K = 512, I8_SMALL_K_ODD = 4096;
 bool i8_small(int M, int N, int K);
 hipError_t launch_gemm_i8_small(const int8_t *A, const int8_t *B, int32_t *C, int M, int N, int K, hipStream_t s);
+// The same for int16 (v_dot2 kernel), K <= I16_SMALL_K.
+constexpr long long I16_SMALL_K = 4096;
+bool i16_small(int M, int N, int K);
+hipError_t launch_gemm_i16_small(const int16_t *A, const int16_t *B, int32_t *C, int M, int N, int K,
+                                 hipStream_t s);
 hipError_t launch_gemm_i8(const int8_t *A, const int8_t *B, int32_t *C, int M, int N, int K, void *ws,
                           hipStream_t s);
 

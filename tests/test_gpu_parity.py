@@ -1144,6 +1144,29 @@ def test_gemm_q16_k_split(m, k, n):
     np.testing.assert_array_equal(c, want.ravel())
 
 
+# int16 shapes whose 16x16 output tiles fit one round of the CUs take the
+# direct v_dot2 kernel while K <= 4096 (no workspace); just past either
+# bound (16x4097x16, 272x16x256) the limb-interleaved MFMA GEMM takes over.
+I16_DIRECT = [(16, 16, 16), (1, 4096, 1), (16, 4096, 16), (255, 4096, 255), (17, 33, 65), (256, 256, 256)]
+I16_DIRECT_EDGE = [(16, 4097, 16), (272, 16, 256)]
+
+
+@pytest.mark.parametrize("m,k,n", I16_DIRECT + I16_DIRECT_EDGE,
+                         ids=[f"{m}x{k}x{n}" for m, k, n in I16_DIRECT + I16_DIRECT_EDGE])
+def test_gemm_i16_direct_route(m, k, n):
+    L = M.lib()
+    assert (L.det_workspace_bytes(M.DET_OP_I16, m, k, n) == 0) == ((m, k, n) in I16_DIRECT)
+    a, b = O.gen_i16(0x1D6 ^ (m * 1000003 + k * 1009 + n), m * k, k * n)
+    note(f"det_matmul_i16 direct-route boundary {m}x{k}x{n}")
+    np.testing.assert_array_equal(M.det_matmul_i16(a.reshape(m, k), b.reshape(k, n)),
+                                  O.gemm_i16(a, b, m, k, n).reshape(m, n))
+    # extreme operands: products of 32767 and -32768, sums that wrap
+    a2 = np.where(np.arange(m * k) % 3 == 0, -32768, 32767).astype(np.int16)
+    b2 = np.where(np.arange(k * n) % 5 == 0, 32767, -32768).astype(np.int16)
+    np.testing.assert_array_equal(M.det_matmul_i16(a2.reshape(m, k), b2.reshape(k, n)),
+                                  O.gemm_i16(a2, b2, m, k, n).reshape(m, n))
+
+
 I16_SHAPES = [(1, 1, 1), (3, 5, 7), (64, 64, 64), (65, 127, 66), (200, 300, 100), (33, 2048, 17),
               (300, 1000, 270), (129, 16, 128)]
 
