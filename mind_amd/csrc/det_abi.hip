@@ -55,6 +55,7 @@ struct DevState {
     size_t io_bytes = 0;
     void *pin = nullptr;               // pinned host staging for small host-pointer calls
     void *pin_dev = nullptr;           // the same memory as the kernels address it
+    bool pin_failed = false;           // pinned allocation refused: small calls copy directly
     void *ws = nullptr;                // limb-GEMM workspace
     size_t ws_bytes = 0;
     hipEvent_t ws_free = nullptr;      // recorded after the last workspace user
@@ -118,6 +119,7 @@ int64_t release_device(DevState &ds) {
     if (ds.ws_free) step(hipEventDestroy(ds.ws_free), "hipEventDestroy");
     if (ds.stream) step(hipStreamDestroy(ds.stream), "hipStreamDestroy");
     ds.io = ds.ws = ds.pin = ds.pin_dev = nullptr;
+    ds.pin_failed = false;
     ds.io_bytes = ds.ws_bytes = 0;
     ds.ws_free = nullptr;
     ds.stream = nullptr;
@@ -182,17 +184,19 @@ hipError_t copy16(void *dst, const void *src, size_t bytes, hipStream_t s) {
 }
 
 // True when a layout of `span` bytes takes the pinned route (the buffer is
-// allocated on the first such call and kept until teardown).
-bool pinned_route(DevState &ds, size_t span, int64_t *rc) {
-    *rc = 0;
-    if (span > PIN_BYTES) return false;
+// allocated on the first such call and kept until teardown).  If the pinned
+// allocation is refused, this device's small calls copy directly instead
+// (the same results, the DMA route's latency).
+bool pinned_route(DevState &ds, size_t span) {
+    if (span > PIN_BYTES || ds.pin_failed) return false;
     if (!ds.pin) {
         hipError_t e = hipHostMalloc(&ds.pin, PIN_BYTES, hipHostMallocDefault);
         if (e == hipSuccess) e = hipHostGetDevicePointer(&ds.pin_dev, ds.pin, 0);
         if (e != hipSuccess) {
             if (ds.pin) (void)hipHostFree(ds.pin);
             ds.pin = ds.pin_dev = nullptr;
-            *rc = det_fail_hip(e, "hipHostMalloc(staging)");
+            ds.pin_failed = true;
+            (void)hipGetLastError();   // the refusal is handled: clear it
             return false;
         }
     }
@@ -327,8 +331,7 @@ int64_t gemm_host(Op op, int64_t a, int64_t b, int64_t c, int64_t m, int64_t k, 
     const size_t span = off_c + align256(bytes_c), need = ws_need(op, m, k, n);
     if ((rc = ensure(&ds.io, &ds.io_bytes, span))) return rc;
     if ((rc = ensure(&ds.ws, &ds.ws_bytes, need))) return rc;
-    const bool pinned = pinned_route(ds, span, &rc);
-    if (rc) return rc;
+    const bool pinned = pinned_route(ds, span);
     char *io = (char *)ds.io;
     hipStream_t s = ds.stream;
     const HostIn in[2] = {{0, (const void *)a, bytes_a}, {off_b, (const void *)b, bytes_b}};
@@ -381,8 +384,7 @@ int64_t gemv_host(bool q16, int64_t w, int64_t x, int64_t y, int64_t m, int64_t 
     const size_t off_x = align256(bytes_w), off_y = off_x + align256(bytes_x);
     const size_t span = off_y + align256(bytes_y);
     if ((rc = ensure(&ds.io, &ds.io_bytes, span))) return rc;
-    const bool pinned = pinned_route(ds, span, &rc);
-    if (rc) return rc;
+    const bool pinned = pinned_route(ds, span);
     char *io = (char *)ds.io;
     hipStream_t s = ds.stream;
     const HostIn in[2] = {{0, (const void *)w, bytes_w}, {off_x, (const void *)x, bytes_x}};
@@ -419,8 +421,7 @@ int64_t dot_host(int op, int64_t a, int64_t b, int64_t len) {
     const size_t off_b = align256(bytes), off_o = off_b + align256(bytes);
     const size_t span = off_o + 256;
     if ((rc = ensure(&ds.io, &ds.io_bytes, span))) return rc;
-    const bool pinned = pinned_route(ds, span, &rc);
-    if (rc) return rc;
+    const bool pinned = pinned_route(ds, span);
     char *io = (char *)ds.io;
     hipStream_t s = ds.stream;
     const HostIn in[2] = {{0, (const void *)a, bytes}, {off_b, (const void *)b, bytes}};
@@ -446,8 +447,7 @@ int64_t f32_rows_host(const float *w, const float *x, float *y, int64_t rows, in
     const size_t off_x = align256(bytes_w), off_y = off_x + align256(bytes_x);
     const size_t span = off_y + align256(bytes_y);
     if ((rc = ensure(&ds.io, &ds.io_bytes, span))) return rc;
-    const bool pinned = pinned_route(ds, span, &rc);
-    if (rc) return rc;
+    const bool pinned = pinned_route(ds, span);
     char *io = (char *)ds.io;
     hipStream_t s = ds.stream;
     const HostIn in[2] = {{0, w, bytes_w}, {off_x, x, bytes_x}};
@@ -531,8 +531,7 @@ int64_t fft_host(int64_t re, int64_t im, int64_t tw, int64_t logn, int64_t n, in
     if ((rc = ensure(&ds.io, &ds.io_bytes, span))) return rc;
     const size_t need = det::fft_workspace_bytes((int)logn, batch);
     if ((rc = ensure(&ds.ws, &ds.ws_bytes, need))) return rc;
-    const bool pinned = pinned_route(ds, span, &rc);
-    if (rc) return rc;
+    const bool pinned = pinned_route(ds, span);
     char *io = (char *)ds.io;
     hipStream_t s = ds.stream;
     const HostIn in[3] = {{0, (const void *)re, bytes}, {off_im, (const void *)im, bytes},
