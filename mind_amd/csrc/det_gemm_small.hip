@@ -30,7 +30,7 @@
 #include "det_kernels.h"
 
 namespace det {
-namespace i8s {
+namespace tiny {
 
 constexpr int TM = 16, TN = 16, KS = 4, ROWB = 256, LDB = ROWB + 16, THREADS = TM * TN * KS;
 
@@ -104,10 +104,10 @@ __global__ __launch_bounds__(THREADS) void small_kernel(const T *__restrict__ A,
     }
 }
 
-}  // namespace i8s
+}  // namespace tiny
 
 static long long small_tiles(int M, int N) {
-    return (long long)((M + i8s::TM - 1) / i8s::TM) * ((N + i8s::TN - 1) / i8s::TN);
+    return (long long)((M + tiny::TM - 1) / tiny::TM) * ((N + tiny::TN - 1) / tiny::TN);
 }
 
 // The MFMA kernels win once their tiles have work to pipeline: over more
@@ -123,8 +123,8 @@ bool i8_small(int M, int N, int K) {
 }
 
 hipError_t launch_gemm_i8_small(const int8_t *A, const int8_t *B, int32_t *C, int M, int N, int K, hipStream_t s) {
-    const int tiles_n = (N + i8s::TN - 1) / i8s::TN;
-    hipLaunchKernelGGL(i8s::small_kernel<int8_t>, dim3((unsigned)small_tiles(M, N)), dim3(i8s::THREADS), 0, s, A, B,
+    const int tiles_n = (N + tiny::TN - 1) / tiny::TN;
+    hipLaunchKernelGGL(tiny::small_kernel<int8_t>, dim3((unsigned)small_tiles(M, N)), dim3(tiny::THREADS), 0, s, A, B,
                        C, M, N, K, tiles_n);
     return hipGetLastError();
 }
@@ -140,8 +140,8 @@ bool i16_small(int M, int N, int K) {
 
 hipError_t launch_gemm_i16_small(const int16_t *A, const int16_t *B, int32_t *C, int M, int N, int K,
                                  hipStream_t s) {
-    const int tiles_n = (N + i8s::TN - 1) / i8s::TN;
-    hipLaunchKernelGGL(i8s::small_kernel<int16_t>, dim3((unsigned)small_tiles(M, N)), dim3(i8s::THREADS), 0, s, A, B,
+    const int tiles_n = (N + tiny::TN - 1) / tiny::TN;
+    hipLaunchKernelGGL(tiny::small_kernel<int16_t>, dim3((unsigned)small_tiles(M, N)), dim3(tiny::THREADS), 0, s, A, B,
                        C, M, N, K, tiles_n);
     return hipGetLastError();
 }
