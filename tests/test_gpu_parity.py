@@ -726,7 +726,7 @@ def test_gemm_i8_repack_rule_leaves_small_grids_alone():
 # of 128 (any alignment, no workspace); just past either bound the MFMA
 # kernels take over (256x640x256, 16x4097x16, 272x16x256: 17 x 16 tiles).
 I8_DIRECT = [(16, 16, 16), (1, 4096, 1), (16, 4096, 16), (256, 512, 256), (255, 4096, 255), (17, 33, 65),
-             (5, 1000, 300)]
+             (5, 1000, 300), (4096, 7, 16), (1, 100, 4096)]
 I8_DIRECT_EDGE = [(256, 640, 256), (16, 4097, 16), (272, 16, 256)]
 
 
@@ -1015,7 +1015,7 @@ def test_gemm_q16_shapes(m, k, n, shift):
 # chunks (63, 64, 65, 255, 256, 257, 1000), the longest K it takes for one
 # round of tiles (4096) and four rounds of 16 x 16 tiles (512 x 1024 x 512).
 Q_DIRECT = [(16, 1, 16), (17, 63, 15), (33, 64, 31), (40, 65, 48), (5, 255, 300), (256, 256, 256), (99, 257, 161),
-            (7, 1000, 130), (16, 4096, 16), (64, 4096, 48), (512, 1024, 512)]
+            (7, 1000, 130), (16, 4096, 16), (64, 4096, 48), (512, 1024, 512), (1, 3, 16384), (16384, 2, 1)]
 
 
 @pytest.mark.parametrize("m,k,n", Q_DIRECT, ids=[f"{m}x{k}x{n}" for m, k, n in Q_DIRECT])
@@ -1147,7 +1147,8 @@ def test_gemm_q16_k_split(m, k, n):
 # int16 shapes whose 16x16 output tiles fit one round of the CUs take the
 # direct v_dot2 kernel while K <= 4096 (no workspace); just past either
 # bound (16x4097x16, 272x16x256) the limb-interleaved MFMA GEMM takes over.
-I16_DIRECT = [(16, 16, 16), (1, 4096, 1), (16, 4096, 16), (255, 4096, 255), (17, 33, 65), (256, 256, 256)]
+I16_DIRECT = [(16, 16, 16), (1, 4096, 1), (16, 4096, 16), (255, 4096, 255), (17, 33, 65), (256, 256, 256),
+              (4096, 9, 16), (1, 100, 4096)]
 I16_DIRECT_EDGE = [(16, 4097, 16), (272, 16, 256)]
 
 
