@@ -488,3 +488,46 @@ def _gemv8_w_addresses(M, K):
 def test_gemv8_w_ring_stays_inside_each_row(M, K):
     lo, hi = _gemv8_w_addresses(M, K)
     assert lo >= 0 and hi <= M * K * 4
+
+
+# ---------------------------------------------------------------- Q16 K split
+# det_gemm_q16x.hip: grids of 64 x 64 tiles that fill at most half the CUs
+# run kspl workgroups per tile (q16x_ksplit), workgroup ks over the 64-k
+# steps [ks NK / kspl, (ks + 1) NK / kspl) of NK = ceil(K / 64); its DMA
+# reaches step kt0 + min(kt + 2, nk - 1) at most.  Restated here: the ranges
+# must partition [0, NK) with at least one step each, the split count must
+# stay within 8 and the idle CUs, and no issued step may leave [0, NK).
+
+def _q16x_ksplit(M, N, K, cus):
+    tiles = ((M + 63) // 64) * ((N + 63) // 64)
+    nk = (K + 63) // 64
+    if 2 * tiles > cus or nk < 2:
+        return 1
+    k = min(8, cus // tiles, nk)
+    steps = (nk + k - 1) // k
+    return (nk + steps - 1) // steps
+
+
+@pytest.mark.parametrize("cus", [256, 80, 32])
+def test_q16x_k_split_ranges_partition_k(cus):
+    rng = np.random.default_rng(cus)
+    shapes = [(256, 256, 256), (512, 512, 512), (7, 5000, 130), (100, 4200, 70), (200, 4160, 300), (64, 64, 64),
+              (1000, 4100, 33), (512, 2048, 512), (1024, 1024, 1024), (1, 65535, 1)]
+    shapes += [tuple(int(v) for v in rng.integers(1, 3000, 3)) for _ in range(300)]
+    for M, K, N in shapes:
+        tiles = ((M + 63) // 64) * ((N + 63) // 64)
+        NK = (K + 63) // 64
+        kspl = _q16x_ksplit(M, N, K, cus)
+        assert 1 <= kspl <= 8 and (kspl == 1 or tiles * kspl <= cus), (M, K, N, kspl)
+        covered = []
+        for ks in range(kspl):
+            kt0 = ks * NK // kspl
+            nk = (ks + 1) * NK // kspl - kt0
+            assert nk >= 1, (M, K, N, ks)
+            issued = [kt0 + min(kt + 2, nk - 1) for kt in range(nk)] + [kt0, kt0 + (1 if nk > 1 else 0)]
+            assert 0 <= min(issued) and max(issued) < NK, (M, K, N, ks)
+            covered += list(range(kt0, kt0 + nk))
+        assert covered == list(range(NK)), (M, K, N)
+        # every split but the longest is at most one step shorter
+        lens = [(ks + 1) * NK // kspl - ks * NK // kspl for ks in range(kspl)]
+        assert max(lens) - min(lens) <= 1
