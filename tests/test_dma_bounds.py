@@ -531,3 +531,22 @@ def test_q16x_k_split_ranges_partition_k(cus):
         # every split but the longest is at most one step shorter
         lens = [(ks + 1) * NK // kspl - ks * NK // kspl for ks in range(kspl)]
         assert max(lens) - min(lens) <= 1
+
+
+# ---------------------------------------------------------------- tiny GEMMs
+# det_gemm_small.hip (int8 / int16) and det_gemm_q16s.hip stage A rows and B
+# columns as [16][row stride] in LDS; each thread of a 16-lane group reads
+# 16 K-contiguous bytes of its own column c at the same k.  With the padded
+# strides (272 bytes for int8 / int16, 260 dwords for Q16) the 16 columns'
+# 16-byte reads land on 64 distinct 4-byte banks, and every row start stays
+# 16-byte aligned.
+
+@pytest.mark.parametrize("stride_bytes", [272, 260 * 4], ids=["int8_int16", "q16"])
+def test_tiny_kernel_lds_reads_conflict_free(stride_bytes):
+    assert stride_bytes % 16 == 0
+    for k_bytes in range(0, 256, 16):
+        banks = []
+        for c in range(16):
+            d0 = (c * stride_bytes + k_bytes) // 4
+            banks += [(d0 + e) % 64 for e in range(4)]
+        assert sorted(banks) == list(range(64)), k_bytes

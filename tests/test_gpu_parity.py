@@ -746,6 +746,42 @@ def test_gemm_i8_direct_route(m, k, n):
                                   O.gemm_i8(a2, b2, m, k, n).reshape(m, n))
 
 
+def _tiny_sweep(count, seed):
+    rng = np.random.default_rng(seed)
+    out = []
+    for _ in range(count):
+        m, n = (int(v) for v in rng.integers(1, 300, 2))
+        k = int(rng.choice([int(rng.integers(1, 300)), int(rng.integers(300, 4097))]))
+        out.append((m, k, n))
+    return out
+
+
+TINY_SWEEP = _tiny_sweep(24, 0x7151)
+
+
+@pytest.mark.parametrize("m,k,n", TINY_SWEEP, ids=[f"{m}x{k}x{n}" for m, k, n in TINY_SWEEP])
+def test_tiny_shapes_every_op(m, k, n):
+    """Seeded small shapes (M, N < 300, K up to 4096) through int8, int16 and
+    Q16 (row-major and transposed B), whichever kernel each routes to, full
+    output against the oracle."""
+    seed = 0x7152 ^ (m * 1000003 + k * 1009 + n)
+    a, b = O.gen_i8(seed, m * k, k * n)
+    note(f"tiny sweep int8 {m}x{k}x{n}")
+    np.testing.assert_array_equal(M.det_matmul_i8(a.reshape(m, k), b.reshape(k, n)),
+                                  O.gemm_i8(a, b, m, k, n).reshape(m, n))
+    a, b = O.gen_i16(seed, m * k, k * n)
+    note(f"tiny sweep int16 {m}x{k}x{n}")
+    np.testing.assert_array_equal(M.det_matmul_i16(a.reshape(m, k), b.reshape(k, n)),
+                                  O.gemm_i16(a, b, m, k, n).reshape(m, n))
+    a, b = O.gen_q16_sat(seed, m * k, k * n, 13)
+    want = O.gemm_q16(a, b, m, k, n)
+    note(f"tiny sweep q16 {m}x{k}x{n}")
+    np.testing.assert_array_equal(M.det_matmul_q16(a.reshape(m, k), b.reshape(k, n)), want.reshape(m, n))
+    c = np.zeros(m * n, np.int32)
+    call6("gemmq", a, np.ascontiguousarray(b.reshape(k, n).T), c, m, k, n)
+    np.testing.assert_array_equal(c, want.ravel())
+
+
 @pytest.mark.parametrize("m,k,n", I8_SHAPES, ids=[f"{m}x{k}x{n}" for m, k, n in I8_SHAPES])
 def test_gemm_i8_shapes(m, k, n):
     a, b = O.gen_i8(0xDEADBEEF00000000 ^ (m * 1000003 + k * 1009 + n), m * k, k * n)
