@@ -157,6 +157,10 @@ int64_t release_all() {
 // buffers (PCIe bandwidth, no extra CPU copy); at about 3 MiB the two routes
 // measured even.
 constexpr size_t PIN_BYTES = 4u << 20;
+// Outputs up to this size are written by the compute kernels straight into
+// the pinned buffer (plain stores over PCIe), which saves the copy-back
+// launch; larger ones come back through the copy kernel at full PCIe rate.
+constexpr size_t OUT_DIRECT_BYTES = 256u << 10;
 
 struct HostIn {
     size_t off;
@@ -220,9 +224,18 @@ int64_t put_inputs(DevState &ds, bool pinned, const HostIn *in, int n_in, hipStr
     return 0;
 }
 
-// Outputs out of io, then wait for the stream.  The outputs' offsets are
-// 256-byte aligned, so the span copied back starts on a 16-byte boundary.
-int64_t get_outputs(DevState &ds, bool pinned, const HostOut *out, int n_out, hipStream_t s) {
+// Where a compute kernel writes an output of `bytes` at layout offset `off`:
+// the pinned buffer itself for small outputs on the pinned route (`direct`),
+// else the device staging buffer.
+void *out_ptr(DevState &ds, bool pinned, size_t off, size_t bytes, bool *direct) {
+    *direct = pinned && bytes <= OUT_DIRECT_BYTES;
+    return (*direct ? (char *)ds.pin_dev : (char *)ds.io) + off;
+}
+
+// Outputs out of io (or already in the pinned buffer when `direct`), then
+// wait for the stream.  The outputs' offsets are 256-byte aligned, so the
+// span copied back starts on a 16-byte boundary.
+int64_t get_outputs(DevState &ds, bool pinned, const HostOut *out, int n_out, hipStream_t s, bool direct = false) {
     char *io = (char *)ds.io;
     if (!pinned) {
         for (int i = 0; i < n_out; ++i)
@@ -235,7 +248,7 @@ int64_t get_outputs(DevState &ds, bool pinned, const HostOut *out, int n_out, hi
         if (out[i].off < lo) lo = out[i].off;
         if (out[i].off + out[i].bytes > hi) hi = out[i].off + out[i].bytes;
     }
-    if (hi > lo) DET_HIP_CHECK(copy16((char *)ds.pin_dev + lo, io + lo, hi - lo, s));
+    if (hi > lo && !direct) DET_HIP_CHECK(copy16((char *)ds.pin_dev + lo, io + lo, hi - lo, s));
     DET_HIP_CHECK(hipStreamSynchronize(s));
     for (int i = 0; i < n_out; ++i)
         if (out[i].bytes) memcpy(out[i].dst, (const char *)ds.pin + out[i].off, out[i].bytes);
@@ -339,10 +352,12 @@ int64_t gemm_host(Op op, int64_t a, int64_t b, int64_t c, int64_t m, int64_t k, 
     // the workspace arena is shared with the device-pointer entry points:
     // start after its last user, and mark this stream as its next one
     if (need) DET_HIP_CHECK(hipStreamWaitEvent(s, ds.ws_free, 0));
-    if ((rc = gemm_dev(op, io, io + off_b, io + off_c, m, k, n, need ? ds.ws : nullptr, s))) return rc;
+    bool direct = false;
+    void *dc = out_ptr(ds, pinned, off_c, bytes_c, &direct);
+    if ((rc = gemm_dev(op, io, io + off_b, dc, m, k, n, need ? ds.ws : nullptr, s))) return rc;
     if (need) DET_HIP_CHECK(hipEventRecord(ds.ws_free, s));
     const HostOut out[1] = {{off_c, (void *)c, bytes_c}};
-    return get_outputs(ds, pinned, out, 1, s);
+    return get_outputs(ds, pinned, out, 1, s, direct);
 }
 
 // Q16 GEMV over nb vectors on device pointers: groups of up to 8 vectors go
@@ -389,7 +404,9 @@ int64_t gemv_host(bool q16, int64_t w, int64_t x, int64_t y, int64_t m, int64_t 
     hipStream_t s = ds.stream;
     const HostIn in[2] = {{0, (const void *)w, bytes_w}, {off_x, (const void *)x, bytes_x}};
     if ((rc = put_inputs(ds, pinned, in, 2, s))) return rc;
-    if (k == 0) DET_HIP_CHECK(zero_i32((int32_t *)(io + off_y), (size_t)nb * m, s));
+    bool direct = false;
+    int32_t *dy = (int32_t *)out_ptr(ds, pinned, off_y, bytes_y, &direct);
+    if (k == 0) DET_HIP_CHECK(zero_i32(dy, (size_t)nb * m, s));
     else if (q16) {
         const int32_t *dW = (const int32_t *)io, *dX = (const int32_t *)(io + off_x);
         const size_t need = gemv_ws_need(dW, dX, m, k, nb);
@@ -397,13 +414,12 @@ int64_t gemv_host(bool q16, int64_t w, int64_t x, int64_t y, int64_t m, int64_t 
         // the workspace arena is shared with the device-pointer entry points
         // (other streams): start after its last user, then mark this stream
         if (need) DET_HIP_CHECK(hipStreamWaitEvent(s, ds.ws_free, 0));
-        DET_HIP_CHECK(gemv_q16_any(dW, dX, (int32_t *)(io + off_y), m, k, nb, need ? ds.ws : nullptr, s));
+        DET_HIP_CHECK(gemv_q16_any(dW, dX, dy, m, k, nb, need ? ds.ws : nullptr, s));
         if (need) DET_HIP_CHECK(hipEventRecord(ds.ws_free, s));
     } else
-        DET_HIP_CHECK(det::launch_gemv_i16((const int16_t *)io, (const int16_t *)(io + off_x),
-                                           (int32_t *)(io + off_y), (int)m, (int)k, s));
+        DET_HIP_CHECK(det::launch_gemv_i16((const int16_t *)io, (const int16_t *)(io + off_x), dy, (int)m, (int)k, s));
     const HostOut out[1] = {{off_y, (void *)y, bytes_y}};
-    return get_outputs(ds, pinned, out, 1, s);
+    return get_outputs(ds, pinned, out, 1, s, direct);
 }
 
 // Host-pointer vector reductions: (int64)(int32)sum; len <= 0 or a NULL
@@ -452,10 +468,11 @@ int64_t f32_rows_host(const float *w, const float *x, float *y, int64_t rows, in
     hipStream_t s = ds.stream;
     const HostIn in[2] = {{0, w, bytes_w}, {off_x, x, bytes_x}};
     if ((rc = put_inputs(ds, pinned, in, 2, s))) return rc;
-    DET_HIP_CHECK(det::launch_rows_f32((const float *)io, (const float *)(io + off_x), (float *)(io + off_y), rows,
-                                       cols, met, s));
+    bool direct = false;
+    float *dy = (float *)out_ptr(ds, pinned, off_y, bytes_y, &direct);
+    DET_HIP_CHECK(det::launch_rows_f32((const float *)io, (const float *)(io + off_x), dy, rows, cols, met, s));
     const HostOut out[1] = {{off_y, y, bytes_y}};
-    return get_outputs(ds, pinned, out, 1, s);
+    return get_outputs(ds, pinned, out, 1, s, direct);
 }
 
 // The reference's packing of an f32 result: its bits, zero-extended to int64.
