@@ -161,6 +161,13 @@ constexpr size_t PIN_BYTES = 4u << 20;
 // the pinned buffer (plain stores over PCIe), which saves the copy-back
 // launch; larger ones come back through the copy kernel at full PCIe rate.
 constexpr size_t OUT_DIRECT_BYTES = 256u << 10;
+// Layouts up to this size whose kernel reads each input element only a few
+// times (the tiny-shape GEMM kernels with at most 16 output tiles, the
+// GEMVs) are read by the kernels straight from the pinned buffer too, which
+// saves the copy-in launch as well (measured: 1-2 us at 16^3 - 64^3; at
+// 128^3 the Q16 tiles' re-reads over PCIe cost more than the copy, and the
+// dots, whose many blocks then read over PCIe, gained nothing).
+constexpr size_t IN_DIRECT_BYTES = 64u << 10;
 
 struct HostIn {
     size_t off;
@@ -207,8 +214,9 @@ bool pinned_route(DevState &ds, size_t span) {
     return true;
 }
 
-// Inputs into io (asynchronous on s).
-int64_t put_inputs(DevState &ds, bool pinned, const HostIn *in, int n_in, hipStream_t s) {
+// Inputs into io (asynchronous on s), or only into the pinned buffer when
+// the kernels read them there (`direct`).
+int64_t put_inputs(DevState &ds, bool pinned, const HostIn *in, int n_in, hipStream_t s, bool direct = false) {
     char *io = (char *)ds.io;
     if (!pinned) {
         for (int i = 0; i < n_in; ++i)
@@ -220,7 +228,7 @@ int64_t put_inputs(DevState &ds, bool pinned, const HostIn *in, int n_in, hipStr
         if (in[i].bytes) memcpy((char *)ds.pin + in[i].off, in[i].src, in[i].bytes);
         if (in[i].off + in[i].bytes > end) end = in[i].off + in[i].bytes;
     }
-    DET_HIP_CHECK(copy16(io, ds.pin_dev, end, s));
+    if (!direct) DET_HIP_CHECK(copy16(io, ds.pin_dev, end, s));
     return 0;
 }
 
@@ -345,10 +353,16 @@ int64_t gemm_host(Op op, int64_t a, int64_t b, int64_t c, int64_t m, int64_t k, 
     if ((rc = ensure(&ds.io, &ds.io_bytes, span))) return rc;
     if ((rc = ensure(&ds.ws, &ds.ws_bytes, need))) return rc;
     const bool pinned = pinned_route(ds, span);
-    char *io = (char *)ds.io;
     hipStream_t s = ds.stream;
+    // the tiny-shape kernels over at most 16 output tiles read the inputs
+    // from the pinned buffer itself when the layout is small
+    const int M = (int)m, N = (int)n, K = (int)k;
+    const bool tiny = op == Op::I8 ? det::i8_small(M, N, K) : op == Op::I16 ? det::i16_small(M, N, K)
+                                                                            : det::q16_small(M, N, K);
+    const bool in_direct = pinned && tiny && span <= IN_DIRECT_BYTES && ((m + 15) / 16) * ((n + 15) / 16) <= 16;
+    char *io = in_direct ? (char *)ds.pin_dev : (char *)ds.io;
     const HostIn in[2] = {{0, (const void *)a, bytes_a}, {off_b, (const void *)b, bytes_b}};
-    if ((rc = put_inputs(ds, pinned, in, 2, s))) return rc;
+    if ((rc = put_inputs(ds, pinned, in, 2, s, in_direct))) return rc;
     // the workspace arena is shared with the device-pointer entry points:
     // start after its last user, and mark this stream as its next one
     if (need) DET_HIP_CHECK(hipStreamWaitEvent(s, ds.ws_free, 0));
@@ -400,10 +414,11 @@ int64_t gemv_host(bool q16, int64_t w, int64_t x, int64_t y, int64_t m, int64_t 
     const size_t span = off_y + align256(bytes_y);
     if ((rc = ensure(&ds.io, &ds.io_bytes, span))) return rc;
     const bool pinned = pinned_route(ds, span);
-    char *io = (char *)ds.io;
+    const bool in_direct = pinned && span <= IN_DIRECT_BYTES;   // W read once, x once per row group
+    char *io = in_direct ? (char *)ds.pin_dev : (char *)ds.io;
     hipStream_t s = ds.stream;
     const HostIn in[2] = {{0, (const void *)w, bytes_w}, {off_x, (const void *)x, bytes_x}};
-    if ((rc = put_inputs(ds, pinned, in, 2, s))) return rc;
+    if ((rc = put_inputs(ds, pinned, in, 2, s, in_direct))) return rc;
     bool direct = false;
     int32_t *dy = (int32_t *)out_ptr(ds, pinned, off_y, bytes_y, &direct);
     if (k == 0) DET_HIP_CHECK(zero_i32(dy, (size_t)nb * m, s));
