@@ -564,18 +564,21 @@ int64_t fft_host(int64_t re, int64_t im, int64_t tw, int64_t logn, int64_t n, in
     const size_t need = det::fft_workspace_bytes((int)logn, batch);
     if ((rc = ensure(&ds.ws, &ds.ws_bytes, need))) return rc;
     const bool pinned = pinned_route(ds, span);
-    char *io = (char *)ds.io;
+    // a few small transforms (no workspace: one read and one write per
+    // point, in place) run on the pinned buffer itself: no copy launches
+    const bool direct = pinned && need == 0 && span <= IN_DIRECT_BYTES;
+    char *io = direct ? (char *)ds.pin_dev : (char *)ds.io;
     hipStream_t s = ds.stream;
     const HostIn in[3] = {{0, (const void *)re, bytes}, {off_im, (const void *)im, bytes},
                           {off_tw, (const void *)tw, bytes_tw}};
-    if ((rc = put_inputs(ds, pinned, in, 3, s))) return rc;
+    if ((rc = put_inputs(ds, pinned, in, 3, s, direct))) return rc;
     if (need) DET_HIP_CHECK(hipStreamWaitEvent(s, ds.ws_free, 0));
     int64_t *dre = (int64_t *)io, *dim = (int64_t *)(io + off_im);
     DET_HIP_CHECK(det::launch_fft_q16(dre, dim, dre, dim, (const int64_t *)(io + off_tw), (int)logn, batch,
                                       need ? ds.ws : nullptr, s));
     if (need) DET_HIP_CHECK(hipEventRecord(ds.ws_free, s));
     const HostOut out[2] = {{0, (void *)re, bytes}, {off_im, (void *)im, bytes}};
-    return get_outputs(ds, pinned, out, 2, s);
+    return get_outputs(ds, pinned, out, 2, s, direct);
 }
 
 }  // namespace

@@ -432,7 +432,11 @@ def _fft_oracle_batch(re, im, tw, logn):
     return out_r, out_i
 
 
-FFT_CASES = [(logn, batch) for logn in range(0, 15) for batch in (1, 3, 37)] + [(8, 1000), (5, 513), (11, 9)]
+# batch <= 512 with 32 <= n <= 2048 takes the few-transform kernel (one
+# workgroup per transform), larger batches the batched one: both sides of
+# that bound are covered (512 / 513, 1000).
+FFT_CASES = [(logn, batch) for logn in range(0, 15) for batch in (1, 3, 37)] + [(8, 1000), (5, 513), (5, 512),
+                                                                              (10, 512), (11, 9)]
 
 
 @pytest.mark.parametrize("logn,batch", FFT_CASES, ids=[f"n{1 << l}_b{b}" for l, b in FFT_CASES])
