@@ -453,14 +453,19 @@ int64_t dot_host(int op, int64_t a, int64_t b, int64_t len) {
     const size_t span = off_o + 256;
     if ((rc = ensure(&ds.io, &ds.io_bytes, span))) return rc;
     const bool pinned = pinned_route(ds, span);
-    char *io = (char *)ds.io;
+    // a dot one block covers stores its sum with a plain store: straight into
+    // the pinned buffer, its inputs read from there too when they are small
+    const bool single = pinned && det::dot_single_block(len);
+    const bool in_direct = single && span <= IN_DIRECT_BYTES;
+    char *io = in_direct ? (char *)ds.pin_dev : (char *)ds.io;
     hipStream_t s = ds.stream;
     const HostIn in[2] = {{0, (const void *)a, bytes}, {off_b, (const void *)b, bytes}};
-    if ((rc = put_inputs(ds, pinned, in, 2, s))) return rc;
-    DET_HIP_CHECK(det::launch_dot(op, io, io + off_b, len, (uint32_t *)(io + off_o), s));
+    if ((rc = put_inputs(ds, pinned, in, 2, s, in_direct))) return rc;
+    uint32_t *dout = (uint32_t *)((single ? (char *)ds.pin_dev : (char *)ds.io) + off_o);
+    DET_HIP_CHECK(det::launch_dot(op, io, io + off_b, len, dout, s));
     uint32_t res = 0;
     const HostOut out[1] = {{off_o, &res, 4}};
-    if ((rc = get_outputs(ds, pinned, out, 1, s))) return rc;
+    if ((rc = get_outputs(ds, pinned, out, 1, s, single))) return rc;
     return (int64_t)(int32_t)res;
 }
 

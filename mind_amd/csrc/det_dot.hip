@@ -16,7 +16,9 @@
 // unsigned difference of the larger and the smaller value, and the int16
 // product is exact in 32 bits.  Sums are uint32 with wrap-around.  Integer
 // addition mod 2^32 is associative and commutative, so the grid-wide sum
-// (one integer atomic per block) is the same number in any order.
+// (one integer atomic per block) is the same number in any order.  A dot
+// that one block covers stores its sum instead (no atomic, so no zeroing
+// launch, and the output may be host memory).
 #include "det_common.h"
 #include "det_kernels.h"
 
@@ -24,6 +26,7 @@ namespace det {
 namespace dot {
 
 constexpr int THREADS = 256;
+constexpr int64_t PER_THREAD = 64;   // elements per thread at which another block is added
 
 template <int OP>
 __device__ __forceinline__ uint32_t term(uint32_t a, uint32_t b) {
@@ -76,7 +79,8 @@ __global__ __launch_bounds__(THREADS) void dot_kernel(const void *__restrict__ A
         uint32_t s = 0;
 #pragma unroll
         for (int w = 0; w < THREADS / 64; ++w) s += part[w];
-        atomicAdd(out, s);
+        if (gridDim.x == 1) *out = s;
+        else atomicAdd(out, s);
     }
 }
 
@@ -84,14 +88,16 @@ __global__ void zero_u32(uint32_t *p) { *p = 0; }
 
 }  // namespace dot
 
-// out: one uint32 of device memory, overwritten with sum mod 2^32.
+bool dot_single_block(int64_t n) { return n <= (int64_t)dot::THREADS * dot::PER_THREAD; }
+
+// out: one uint32, overwritten with sum mod 2^32 (device memory; host memory
+// too when dot_single_block(n)).
 hipError_t launch_dot(int op, const void *a, const void *b, int64_t n, uint32_t *out, hipStream_t s) {
     using namespace dot;
-    hipLaunchKernelGGL(zero_u32, dim3(1), dim3(1), 0, s, out);
+    if (n <= 0 || !dot_single_block(n)) hipLaunchKernelGGL(zero_u32, dim3(1), dim3(1), 0, s, out);
     if (n <= 0) return hipGetLastError();
     const bool vec = (((uintptr_t)a | (uintptr_t)b) & 15) == 0;
-    const int64_t per_thread = 64;   // elements per thread at full grid
-    const int64_t blocks = (n + THREADS * per_thread - 1) / (THREADS * per_thread);
+    const int64_t blocks = (n + THREADS * PER_THREAD - 1) / (THREADS * PER_THREAD);
     const dim3 grid((unsigned)(blocks < 1024 ? blocks : 1024));
     switch (op) {
     case DOT_Q16: hipLaunchKernelGGL(dot_kernel<DOT_Q16>, grid, dim3(THREADS), 0, s, a, b, n, out, vec); break;

@@ -90,6 +90,9 @@ hipError_t launch_gemv_q16_mfma(const int32_t *W, const int32_t *X, int32_t *Y, 
 // (DOT_I16); *out (one device uint32) is overwritten.
 enum { DOT_Q16 = 0, DOT_L1 = 1, DOT_I16 = 2 };
 hipError_t launch_dot(int op, const void *a, const void *b, int64_t n, uint32_t *out, hipStream_t s);
+// True when one block covers the dot (n <= 16384): it then stores its sum
+// (no atomic, no zeroing launch), so *out may be host memory.
+bool dot_single_block(int64_t n);
 // Strict-FP f32: y[r] = metric met of W row r and x on the reference's
 // pinned 8-lane schedule: F32_DOT (no fused multiply-add, fixed fold order),
 // F32_L1 (sum of sign-cleared differences), F32_LINF (max, NaN skipped),

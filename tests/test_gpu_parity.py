@@ -108,7 +108,9 @@ def test_canary_dot_i16(canaries, sym):
     assert O.sha256_i64_le(getattr(M.lib(), sym)(addr(a), addr(b), len(a))) == w["avx2"]
 
 
-DOT_LENS = [0, 1, 3, 4, 5, 7, 8, 9, 17, 4093, 65536, 1 << 20]
+# 16384 is the longest dot one block covers (a plain store of the sum);
+# 16385 takes two blocks and the atomic
+DOT_LENS = [0, 1, 3, 4, 5, 7, 8, 9, 17, 4093, 16383, 16384, 16385, 65536, 1 << 20]
 
 
 @pytest.mark.parametrize("n", DOT_LENS)
@@ -133,8 +135,8 @@ def test_dots_vs_oracle(n, fam):
         assert M.dot_i16(a16[1:], b16[1:]) == O.dot_i16(a16[1:], b16[1:])
 
 
-def test_dot_dev_entry_point():
-    n = 100003
+@pytest.mark.parametrize("n", [100003, 16384, 5])
+def test_dot_dev_entry_point(n):
     a, b = O.gen_q16(0xDE7, n, n, shift=0)
     a16, b16 = O.gen_i16(0xDE8, n, n)
     s = M.Stream()
