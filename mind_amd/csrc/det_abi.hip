@@ -20,11 +20,15 @@
 // reference's mind_last_error (src/ffi/mod.rs:173).  A NULL pointer or a
 // non-positive size with nothing to compute follows the reference's Track A
 // convention and returns 0 (runtime-support/mind_intrinsics.c:1537-1539).
+#include <algorithm>
+#include <condition_variable>
 #include <cstdio>
 #include <cstdlib>
 #include <cstring>
 #include <mutex>
 #include <string>
+#include <thread>
+#include <vector>
 
 #include "det_common.h"
 #include "det_kernels.h"
@@ -44,6 +48,10 @@ void put_err(const char *a, const char *b = nullptr) {
 
 constexpr int MAX_DEV = 64;
 constexpr int64_t DIM_MAX = 0x7fffffff;
+// Pinned ring of large host-pointer transfers (see ring_h2d): RING_SLOTS
+// chunks of up to RING_CHUNK bytes each.
+constexpr int RING_SLOTS = 4;
+constexpr size_t RING_CHUNK = 16u << 20;
 
 // Per-device state.  `mu` serialises the host-pointer entry points on that
 // device (like the reference's dispatch lock, runtime-support/
@@ -56,6 +64,12 @@ struct DevState {
     void *pin = nullptr;               // pinned host staging for small host-pointer calls
     void *pin_dev = nullptr;           // the same memory as the kernels address it
     bool pin_failed = false;           // pinned allocation refused: small calls copy directly
+    char *ring = nullptr;              // pinned chunks of large host-pointer transfers
+    char *ring_dev = nullptr;          // the same memory as the copy kernels address it
+    hipEvent_t ring_ev[RING_SLOTS] = {};   // the last copy that used each chunk
+    bool ring_used[RING_SLOTS] = {};
+    unsigned ring_next = 0;            // the chunk the next transfer piece takes
+    bool ring_failed = false;          // ring allocation refused: large calls copy directly
     void *ws = nullptr;                // limb-GEMM workspace
     size_t ws_bytes = 0;
     hipEvent_t ws_free = nullptr;      // recorded after the last workspace user
@@ -113,11 +127,23 @@ int64_t release_device(DevState &ds) {
     };
     if (ds.stream) step(hipStreamSynchronize(ds.stream), "hipStreamSynchronize");
     if (ds.ws_free) step(hipEventSynchronize(ds.ws_free), "hipEventSynchronize");
-    if (ds.io) step(hipFree(ds.io), "hipFree(staging)");
-    if (ds.pin) step(hipHostFree(ds.pin), "hipHostFree(staging)");
-    if (ds.ws) step(hipFree(ds.ws), "hipFree(workspace)");
+    // The events and the stream go first: a recorded event keeps the copy
+    // queued before it alive in the runtime, and with it the buffer that copy
+    // wrote, whose memory would then come back only some time after hipFree.
+    for (int i = 0; i < RING_SLOTS; ++i) {
+        if (ds.ring_ev[i]) step(hipEventDestroy(ds.ring_ev[i]), "hipEventDestroy(ring)");
+        ds.ring_ev[i] = nullptr;
+        ds.ring_used[i] = false;
+    }
     if (ds.ws_free) step(hipEventDestroy(ds.ws_free), "hipEventDestroy");
     if (ds.stream) step(hipStreamDestroy(ds.stream), "hipStreamDestroy");
+    if (ds.io) step(hipFree(ds.io), "hipFree(staging)");
+    if (ds.pin) step(hipHostFree(ds.pin), "hipHostFree(staging)");
+    if (ds.ring) step(hipHostFree(ds.ring), "hipHostFree(ring)");
+    ds.ring = ds.ring_dev = nullptr;
+    ds.ring_next = 0;
+    ds.ring_failed = false;
+    if (ds.ws) step(hipFree(ds.ws), "hipFree(workspace)");
     ds.io = ds.ws = ds.pin = ds.pin_dev = nullptr;
     ds.pin_failed = false;
     ds.io_bytes = ds.ws_bytes = 0;
@@ -133,7 +159,7 @@ int64_t release_all() {
     for (int d = 0; d < MAX_DEV; ++d) {
         DevState &ds = g_dev[d];
         std::lock_guard<std::mutex> lock(ds.mu);
-        if (!ds.stream && !ds.ws_free && !ds.io && !ds.ws && !ds.pin) continue;
+        if (!ds.stream && !ds.ws_free && !ds.io && !ds.ws && !ds.pin && !ds.ring) continue;
         hipError_t e = hipSetDevice(d);
         int64_t r = e == hipSuccess ? release_device(ds) : det_fail_hip(e, "hipSetDevice");
         if (r && rc == 0) rc = r;
@@ -153,8 +179,9 @@ int64_t release_all() {
 // the outputs out.  A DMA copy costs about 10 us of latency here, from
 // pageable and pinned memory alike, so a small call with three or four of
 // them spent most of its time there; two kernels on the same stream cost a
-// few microseconds.  Larger layouts use hipMemcpyAsync on the caller's
-// buffers (PCIe bandwidth, no extra CPU copy); at about 3 MiB the two routes
+// few microseconds.  In larger layouts each buffer of 1 MiB or more travels
+// through the pinned ring below and smaller ones by hipMemcpyAsync on the
+// caller's buffer; at about 3 MiB the pinned route and direct copies
 // measured even.
 constexpr size_t PIN_BYTES = 4u << 20;
 // Outputs up to this size are written by the compute kernels straight into
@@ -194,6 +221,182 @@ hipError_t copy16(void *dst, const void *src, size_t bytes, hipStream_t s) {
     return hipGetLastError();
 }
 
+// ---------------------------------------------- large transfers: the ring
+// From the caller's pageable buffers the runtime's copies run at about
+// 30 GB/s host to device and 18 GB/s back here, against 57 GB/s each way
+// from pinned memory.  Buffers of at least RING_MIN bytes therefore travel
+// in pieces through a ring of pinned chunks: the CPU copies a piece into
+// its chunk while the DMA of the previous pieces runs (and, device to host,
+// copies a landed piece out while later ones are in flight).  One CPU thread
+// copies pageable memory at about 30 GB/s, so each piece's host copy is
+// split over COPY_THREADS threads: 53-54 GB/s each way for a 1 GiB buffer.
+constexpr size_t RING_MIN = 1u << 20;
+// Pieces shorter than this move between a chunk and device memory by the
+// copy kernel (a few microseconds of launch); longer ones by DMA, about 8%
+// faster per byte from host memory but about 10 us of latency per copy.
+constexpr size_t RING_DMA_MIN = 4u << 20;
+constexpr int COPY_THREADS = 4;
+constexpr size_t COPY_SPLIT = 512u << 10;   // host copies at least this long are split
+
+// The caller and COPY_THREADS - 1 workers share each host copy.  Workers
+// start on first use and stop at teardown or unload; one copy runs at a
+// time (the caller of another waits).
+class CopyPool {
+  public:
+    ~CopyPool() { stop(); }
+    void copy(void *dst, const void *src, size_t bytes) {
+        if (bytes < COPY_SPLIT) {
+            memcpy(dst, src, bytes);
+            return;
+        }
+        std::lock_guard<std::mutex> job(job_mu_);
+        std::unique_lock<std::mutex> lk(mu_);
+        if (workers_.empty()) start();
+        const size_t parts = std::min<size_t>(workers_.size() + 1, (bytes + COPY_SPLIT / 2 - 1) / (COPY_SPLIT / 2));
+        dst_ = (char *)dst;
+        src_ = (const char *)src;
+        bytes_ = bytes;
+        piece_ = ((bytes + parts - 1) / parts + 4095) & ~(size_t)4095;
+        npieces_ = (bytes + piece_ - 1) / piece_;
+        next_ = 0;
+        pending_ = npieces_;
+        work_cv_.notify_all();
+        while (next_ < npieces_) run_one(lk);
+        done_cv_.wait(lk, [&] { return pending_ == 0; });
+    }
+    void stop() {
+        std::lock_guard<std::mutex> job(job_mu_);
+        {
+            std::lock_guard<std::mutex> lk(mu_);
+            quit_ = true;
+        }
+        work_cv_.notify_all();
+        for (auto &t : workers_) t.join();
+        workers_.clear();
+        quit_ = false;
+    }
+
+  private:
+    // called with mu_ held; copies piece next_ with mu_ released
+    void run_one(std::unique_lock<std::mutex> &lk) {
+        const size_t i = next_++, o = i * piece_;
+        char *d = dst_ + o;
+        const char *sp = src_ + o;
+        const size_t n = std::min(piece_, bytes_ - o);
+        lk.unlock();
+        memcpy(d, sp, n);
+        lk.lock();
+        if (--pending_ == 0) done_cv_.notify_all();
+    }
+    void start() {   // mu_ held; a thread that cannot start leaves the copy to fewer
+        for (int t = 1; t < COPY_THREADS; ++t) {
+            try {
+                workers_.emplace_back([this] {
+                    std::unique_lock<std::mutex> lk(mu_);
+                    for (;;) {
+                        work_cv_.wait(lk, [&] { return quit_ || next_ < npieces_; });
+                        if (quit_) return;
+                        run_one(lk);
+                    }
+                });
+            } catch (...) {
+                break;
+            }
+        }
+    }
+    std::mutex job_mu_, mu_;
+    std::condition_variable work_cv_, done_cv_;
+    std::vector<std::thread> workers_;
+    char *dst_ = nullptr;
+    const char *src_ = nullptr;
+    size_t bytes_ = 0, piece_ = 0, npieces_ = 0, next_ = 0, pending_ = 0;
+    bool quit_ = false;
+};
+CopyPool g_pool;
+
+// True when this device's ring exists (allocated on the first large call and
+// kept until teardown).  If the pinned allocation is refused, large calls
+// copy the caller's buffers directly instead (the same results, the
+// runtime's pageable rate).
+bool ring_ready(DevState &ds) {
+    if (ds.ring) return true;
+    if (ds.ring_failed) return false;
+    hipError_t e = hipHostMalloc((void **)&ds.ring, RING_SLOTS * RING_CHUNK, hipHostMallocDefault);
+    if (e == hipSuccess) e = hipHostGetDevicePointer((void **)&ds.ring_dev, ds.ring, 0);
+    for (int i = 0; i < RING_SLOTS && e == hipSuccess; ++i)
+        e = hipEventCreateWithFlags(&ds.ring_ev[i], hipEventDisableTiming);
+    if (e != hipSuccess) {
+        for (int i = 0; i < RING_SLOTS; ++i) {
+            if (ds.ring_ev[i]) (void)hipEventDestroy(ds.ring_ev[i]);
+            ds.ring_ev[i] = nullptr;
+        }
+        if (ds.ring) (void)hipHostFree(ds.ring);
+        ds.ring = nullptr;
+        ds.ring_failed = true;
+        (void)hipGetLastError();   // the refusal is handled: clear it
+        return false;
+    }
+    return true;
+}
+
+// Piece length of a ring transfer of `bytes`: about a quarter of the
+// buffer (so the copies of a mid-size buffer overlap too), 1 MiB to
+// RING_CHUNK.
+size_t ring_piece(size_t bytes) {
+    const size_t q = ((bytes + 3) / 4 + ((1u << 20) - 1)) & ~(size_t)((1u << 20) - 1);
+    return std::min(RING_CHUNK, q);
+}
+
+// Host -> device through the ring, asynchronous on s: each piece waits for
+// its chunk's previous copy, is copied in by the CPU, and its DMA queued.
+int64_t ring_h2d(DevState &ds, char *dst, const char *src, size_t bytes, hipStream_t s) {
+    const size_t piece = ring_piece(bytes);
+    for (size_t o = 0; o < bytes; o += piece) {
+        const size_t n = std::min(piece, bytes - o);
+        const unsigned sl = ds.ring_next++ % RING_SLOTS;
+        char *chunk = ds.ring + (size_t)sl * RING_CHUNK;
+        if (ds.ring_used[sl]) DET_HIP_CHECK(hipEventSynchronize(ds.ring_ev[sl]));
+        g_pool.copy(chunk, src + o, n);
+        if (n < RING_DMA_MIN) DET_HIP_CHECK(copy16(dst + o, ds.ring_dev + (size_t)sl * RING_CHUNK, n, s));
+        else DET_HIP_CHECK(hipMemcpyAsync(dst + o, chunk, n, hipMemcpyHostToDevice, s));
+        DET_HIP_CHECK(hipEventRecord(ds.ring_ev[sl], s));
+        ds.ring_used[sl] = true;
+    }
+    return 0;
+}
+
+// Device -> host through the ring, after the work queued on s: up to
+// RING_SLOTS pieces in flight; each landed piece is copied out by the CPU
+// and its chunk refilled with the next piece.  A chunk's earlier user is a
+// copy queued on s before (ordered by the stream) or a piece whose host
+// copy has finished, so no piece waits for anything but its own DMA.
+int64_t ring_d2h(DevState &ds, char *dst, const char *src, size_t bytes, hipStream_t s) {
+    const size_t piece = ring_piece(bytes), np = (bytes + piece - 1) / piece;
+    const unsigned first = ds.ring_next;
+    ds.ring_next += (unsigned)np;
+    auto issue = [&](size_t i) -> int64_t {
+        const unsigned sl = (first + (unsigned)i) % RING_SLOTS;
+        const size_t o = i * piece;
+        const size_t n = std::min(piece, bytes - o);
+        if (n < RING_DMA_MIN) DET_HIP_CHECK(copy16(ds.ring_dev + (size_t)sl * RING_CHUNK, src + o, n, s));
+        else DET_HIP_CHECK(hipMemcpyAsync(ds.ring + (size_t)sl * RING_CHUNK, src + o, n, hipMemcpyDeviceToHost, s));
+        DET_HIP_CHECK(hipEventRecord(ds.ring_ev[sl], s));
+        ds.ring_used[sl] = true;
+        return 0;
+    };
+    int64_t rc = 0;
+    for (size_t i = 0; i < np && i < (size_t)RING_SLOTS; ++i)
+        if ((rc = issue(i))) return rc;
+    for (size_t i = 0; i < np; ++i) {
+        const unsigned sl = (first + (unsigned)i) % RING_SLOTS;
+        DET_HIP_CHECK(hipEventSynchronize(ds.ring_ev[sl]));
+        const size_t o = i * piece;
+        g_pool.copy(dst + o, ds.ring + (size_t)sl * RING_CHUNK, std::min(piece, bytes - o));
+        if (i + RING_SLOTS < np && (rc = issue(i + RING_SLOTS))) return rc;
+    }
+    return 0;
+}
+
 // True when a layout of `span` bytes takes the pinned route (the buffer is
 // allocated on the first such call and kept until teardown).  If the pinned
 // allocation is refused, this device's small calls copy directly instead
@@ -219,8 +422,14 @@ bool pinned_route(DevState &ds, size_t span) {
 int64_t put_inputs(DevState &ds, bool pinned, const HostIn *in, int n_in, hipStream_t s, bool direct = false) {
     char *io = (char *)ds.io;
     if (!pinned) {
-        for (int i = 0; i < n_in; ++i)
-            if (in[i].bytes) DET_HIP_CHECK(hipMemcpyAsync(io + in[i].off, in[i].src, in[i].bytes, hipMemcpyHostToDevice, s));
+        int64_t rc = 0;
+        for (int i = 0; i < n_in; ++i) {
+            if (in[i].bytes >= RING_MIN && ring_ready(ds)) {
+                if ((rc = ring_h2d(ds, io + in[i].off, (const char *)in[i].src, in[i].bytes, s))) return rc;
+            } else if (in[i].bytes) {
+                DET_HIP_CHECK(hipMemcpyAsync(io + in[i].off, in[i].src, in[i].bytes, hipMemcpyHostToDevice, s));
+            }
+        }
         return 0;
     }
     size_t end = 0;
@@ -246,8 +455,14 @@ void *out_ptr(DevState &ds, bool pinned, size_t off, size_t bytes, bool *direct)
 int64_t get_outputs(DevState &ds, bool pinned, const HostOut *out, int n_out, hipStream_t s, bool direct = false) {
     char *io = (char *)ds.io;
     if (!pinned) {
-        for (int i = 0; i < n_out; ++i)
-            if (out[i].bytes) DET_HIP_CHECK(hipMemcpyAsync(out[i].dst, io + out[i].off, out[i].bytes, hipMemcpyDeviceToHost, s));
+        int64_t rc = 0;
+        for (int i = 0; i < n_out; ++i) {
+            if (out[i].bytes >= RING_MIN && ring_ready(ds)) {
+                if ((rc = ring_d2h(ds, (char *)out[i].dst, io + out[i].off, out[i].bytes, s))) return rc;
+            } else if (out[i].bytes) {
+                DET_HIP_CHECK(hipMemcpyAsync(out[i].dst, io + out[i].off, out[i].bytes, hipMemcpyDeviceToHost, s));
+            }
+        }
         DET_HIP_CHECK(hipStreamSynchronize(s));
         return 0;
     }
@@ -895,7 +1110,11 @@ int64_t det_dot_dev(int64_t op, const void *a, const void *b, int64_t len, int32
 // process exit as well as at dlclose, and HIP calls made during process exit
 // abort under tools that intercept HIP (a profiler's per-thread state is
 // gone by then).  Callers that unload the library call it before dlclose.
-int64_t det_shutdown(void) { return release_all(); }
+int64_t det_shutdown(void) {
+    const int64_t rc = release_all();
+    g_pool.stop();
+    return rc;
+}
 const char *det_last_error(void) { return g_err; }
 const char *det_version(void) { return "mind-det-mi355x 0.1 (gfx950)"; }
 

@@ -546,7 +546,8 @@ def test_fft_argument_conventions():
 
 # Host-pointer calls whose operand layout (inputs, output, each rounded up to
 # 256 bytes) fits in 4 MiB travel through the library's pinned staging buffer
-# and two copy kernels; larger ones use DMA copies of the caller's buffers.
+# and two copy kernels; in larger ones each buffer of 1 MiB or more goes
+# through the pinned ring and smaller ones by DMA copies of the caller's buffer.
 # One call on each side of the limit per family, checked whole, then the small
 # one again (the pinned buffer keeps the large call's bytes past its end).
 HOST_ROUTES = [("gemmi8", 768, 3 << 20), ("gemmi8", 1024, 6 << 20), ("gemvq", 2048, 2 << 20), ("gemvq", 8192, 8 << 20),
@@ -585,6 +586,63 @@ def test_host_staging_routes(sym, size, span):
             assert np.array_equal(got[0][sel], want[0]) and np.array_equal(got[1][sel], want[1])
 
 
+# Buffers of 1 MiB and more travel in pieces through a ring of four pinned
+# 16 MiB chunks (the CPU copies a piece while earlier pieces' DMA runs; up to
+# four threads share each host copy).  Cases: lengths that end mid-chunk,
+# operands at element offsets (not 16-byte aligned), an output of more
+# pieces than chunks (chunks refilled while others are in flight), ring and
+# direct buffers in one call, and a teardown between calls (ring and copy
+# threads rebuilt on the next call).
+def test_host_ring_transfers():
+    L = M.lib()
+
+    def gemv_case(seed):
+        rows, cols = 5003, 1001                      # W: 20.0 MB, 4 pieces
+        W, x = O.gen_q16(seed, rows * cols + 1, cols + 1, shift=0)
+        W, x = W[1:], x[1:]                          # 4 bytes off 16-byte alignment
+        y = np.full(rows, 0x5A5A5A5A, np.int32)
+        note(f"ring gemvq {rows}x{cols} seed={seed}")
+        assert L.gemvq(addr(W), addr(x), addr(y), rows, cols) == 0
+        np.testing.assert_array_equal(y, O.gemv_q16(W, x, rows, cols))
+
+    gemv_case(0x91)
+    # C = 67.2 MB: five 16 MiB pieces through four chunks; A and B (262 KB)
+    # copied directly in the same call; checked whole (exact in float64)
+    m, k, n = 4100, 64, 4100
+    a, b = O.gen_i8(0x92, m * k, k * n)
+    want = (a.reshape(m, k).astype(np.float64) @ b.reshape(k, n).astype(np.float64)).astype(np.int32)
+    buf = np.full(m * n + 1, 0x5A5A5A5A, np.int32)
+    c = buf[1:]                                      # output 4 bytes off alignment
+    note(f"ring gemmi8 {m}x{k}x{n} (C through the ring)")
+    assert L.gemmi8(addr(a), addr(b), addr(c), m, k, n) == 0
+    np.testing.assert_array_equal(c.reshape(m, n), want)
+    assert buf[0] == 0x5A5A5A5A
+    # both dot operands through the ring, odd length
+    ln = 5 * (1 << 20) + 3
+    da, db = O.gen_q16(0x93, ln + 1, ln, shift=0)
+    note(f"ring dotq len={ln}")
+    assert M.dot_q16(da[1:], db) == O.dot_q16(da[1:], db)
+    # strict f32 rows: W 24 MB
+    rows, cols = 3000, 2001
+    Wf, xf = O.gen_f32_unit(0x94, rows * cols, cols)
+    note(f"ring mmf32 {rows}x{cols}")
+    assert f32_same(M.matmul_rmajor_f32(Wf.reshape(rows, cols), xf), O.matmul_rmajor_f32(Wf, xf, rows, cols))
+    # FFT: re and im (4.3 MB each) in and out through the ring
+    nb, nfft = 2100, 256
+    x = np.random.default_rng(0x95).integers(-(1 << 30), 1 << 30, (2, nb, nfft))
+    re, im = np.ascontiguousarray(x[0]), np.ascontiguousarray(x[1])
+    tw = O.fft_twiddles(nfft)
+    note(f"ring fft256 batch={nb}")
+    got = M.fft_q16(re, im, tw, 8)
+    sel = [0, 1, nb // 2, nb - 2, nb - 1]
+    want_r, want_i = _fft_oracle_batch(re[sel], im[sel], tw, 8)
+    assert np.array_equal(got[0][sel], want_r) and np.array_equal(got[1][sel], want_i)
+    # teardown, then the ring and the copy threads again
+    note("ring after det_shutdown")
+    assert L.det_shutdown() == 0
+    gemv_case(0x96)
+
+
 def test_host_abi_concurrent_callers():
     # The host-pointer entry points are called from several threads at once
     # (ctypes releases the GIL): one device mutex serialises them, the
@@ -605,6 +663,8 @@ def test_host_abi_concurrent_callers():
     dq = O.dot_q16(da, db)
     Wf, xf = O.gen_f32_unit(0x7A6, 300 * 777, 777)
     yf = O.matmul_rmajor_f32(Wf, xf, 300, 777)
+    Wr, xr = O.gen_q16(0x7A7, 3000 * 1001, 1001)   # W 12 MB: the pinned ring
+    yr = O.gemv_q16(Wr, xr, 3000, 1001)
 
     def job_i8():
         c = np.empty(256 * 192, np.int32)
@@ -634,7 +694,12 @@ def test_host_abi_concurrent_callers():
         assert L.mmf32(addr(Wf), addr(xf), addr(yy), 300, 777) == 0
         return np.array_equal(yy.view(np.uint32), yf.view(np.uint32))
 
-    jobs = [job_i8, job_q16, job_gemv, job_fft, job_dot, job_f32]
+    def job_ring():
+        yy = np.empty(3000, np.int32)
+        assert L.gemvq(addr(Wr), addr(xr), addr(yy), 3000, 1001) == 0
+        return np.array_equal(yy, yr)
+
+    jobs = [job_i8, job_q16, job_gemv, job_fft, job_dot, job_f32, job_ring]
     results, errors = [], []
 
     def run(job):
@@ -644,14 +709,14 @@ def test_host_abi_concurrent_callers():
         except Exception as e:   # reported below, not lost in the thread
             errors.append((job.__name__, repr(e)))
 
-    note("host ABI: 6 threads x 5 calls")
+    note("host ABI: 7 threads x 5 calls")
     threads = [threading.Thread(target=run, args=(j,)) for j in jobs]
     for t in threads:
         t.start()
     for t in threads:
         t.join(timeout=120)
     assert not errors, errors
-    assert len(results) == 30 and all(ok for _, ok in results), [r for r in results if not r[1]]
+    assert len(results) == 35 and all(ok for _, ok in results), [r for r in results if not r[1]]
 
 
 def test_device_arena_shared_by_two_streams():

@@ -10,7 +10,11 @@ The library must be gone from the process after every dlclose, each round
 must give the 128+ MiB staging buffer back, and the level must stay flat from
 round to round: without the teardown each round would leave its staging
 buffer behind.  (The first kernel launch in a process costs the HIP runtime a
-one-time ~150 MiB of its own, which the first round's figure includes.)
+one-time ~150 MiB of its own, which the first round's figure includes.  The
+runtime can hand back the memory of a buffer last written by a DMA copy a few
+milliseconds after hipFree returns, so the reading after dlclose waits until
+free memory has stopped changing, for at most a second: a buffer that is never
+given back still fails.)
 """
 import os
 import subprocess
@@ -30,6 +34,15 @@ assert hip.hipSetDevice(0) == 0
 def free_mem():
     assert hip.hipMemGetInfo(ctypes.byref(free_b), ctypes.byref(total_b)) == 0
     return free_b.value
+def settled_free_mem():
+    import time
+    last, same, t0 = free_mem(), 0, time.monotonic()
+    while same < 5 and time.monotonic() - t0 < 1.0:
+        time.sleep(0.001)
+        now = free_mem()
+        same = same + 1 if now == last else 0
+        last = now
+    return last
 base = free_mem()
 M, K = 2048, 16384                      # W = 128 MiB of Q16
 rng = np.random.default_rng(7)
@@ -53,7 +66,7 @@ for it in range(20):
     del f, L
     _ctypes.dlclose(handle)
     loaded = os.path.realpath(lib_path) in open("/proc/self/maps").read()
-    after = free_mem()
+    after = settled_free_mem()
     print(f"round {it}: loaded {(base - held) >> 20} MiB below baseline, after dlclose {(base - after) >> 20} MiB, "
           f"still mapped {loaded}", flush=True)
     assert not loaded, "dlclose did not unload the library"
