@@ -132,9 +132,25 @@ def _hip():
 
 
 def _free_bytes(H):
-    free, total = ctypes.c_size_t(0), ctypes.c_size_t(0)
-    assert H.hipMemGetInfo(ctypes.byref(free), ctypes.byref(total)) == 0
-    return free.value
+    """Free device memory once it has stopped changing (five equal readings
+    1 ms apart, at most 1 s): the runtime can hand back the memory of a
+    buffer freed earlier in this process a few milliseconds late, which
+    must not read as an allocation by the call under test.  A buffer that
+    the call allocates and keeps still shows."""
+    import time
+
+    def read():
+        free, total = ctypes.c_size_t(0), ctypes.c_size_t(0)
+        assert H.hipMemGetInfo(ctypes.byref(free), ctypes.byref(total)) == 0
+        return free.value
+
+    last, same, t0 = read(), 0, time.monotonic()
+    while same < 5 and time.monotonic() - t0 < 1.0:
+        time.sleep(0.001)
+        now = read()
+        same = same + 1 if now == last else 0
+        last = now
+    return last
 
 
 def test_scratch_entry_allocates_nothing_and_captures_into_a_graph():
