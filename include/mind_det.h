@@ -280,9 +280,10 @@ int64_t det_matmul_scratch_dev(int64_t op, const void *a, const void *b, int32_t
                                void *stream);
 
 /* Runtime helpers (thin wrappers over HIP, so a caller needs no HIP headers). */
-/* Release the library's per-device state (its stream, event, host-call
- * staging buffer and workspace arena) after waiting for the work queued on
- * them; later calls recreate what they need.  The reference joins its thread
+/* Release the library's per-device state (its stream, events, host-call
+ * staging buffers: device, pinned and the pinned ring, and workspace arena)
+ * after waiting for the work queued on them, and join the host-copy
+ * threads; later calls recreate what they need.  The reference joins its thread
  * pool at unload (runtime-support/mind_intrinsics.c:2066-2080); here the
  * release is explicit: a caller that unloads the library calls det_shutdown()
  * before dlclose (an exit hook would run HIP calls during process exit, which
