@@ -1649,6 +1649,30 @@ def test_big_gemm_i16_limb_path():
     np.testing.assert_array_equal(C[rows], O.gemm_i16_rows(A, B, m, k, n, rows))
 
 
+def test_big_host_calls_through_the_ring():
+    # host-pointer calls whose buffers pass 4 GiB: the pinned ring's pieces
+    # then sit at offsets beyond 2^32 and each of its four chunks is reused
+    # about seventy times in one call; in (a 4.5 GiB W) and out (a 4.1 GiB C)
+    L = M.lib()
+    m, k = 73728, 16384
+    W, x = M.gen_q16(0xB16 ^ 6, m * k, k, 15)
+    assert W.nbytes > (1 << 32)
+    y = np.full(m, 0x5A5A5A5A, np.int32)
+    note(f"gemvq host {m}x{k} (W {W.nbytes >> 20} MiB through the ring)")
+    assert L.gemvq(addr(W), addr(x), addr(y), m, k) == 0
+    rows = np.unique(np.r_[_sample_rows(m, 12), (1 << 32) // (4 * k) - 1, (1 << 32) // (4 * k)])
+    np.testing.assert_array_equal(y[rows], O.gemv_q16_rows(W, x, m, k, 1, rows).ravel())
+    del W
+    m, k, n = 33024, 16, 33000
+    a, b = O.gen_i8(0xB16 ^ 7, m * k, k * n)
+    c = np.empty(m * n, np.int32)
+    assert c.nbytes > (1 << 32)
+    note(f"gemmi8 host {m}x{k}x{n} (C {c.nbytes >> 20} MiB through the ring)")
+    assert L.gemmi8(addr(a), addr(b), addr(c), m, k, n) == 0
+    rows = np.unique(np.r_[_sample_rows(m, 12), (1 << 32) // (4 * n) - 1, (1 << 32) // (4 * n)])
+    np.testing.assert_array_equal(c.reshape(m, n)[rows], O.gemm_i8_rows(a, b, m, k, n, rows))
+
+
 def test_big_matmul_rmajor_f32():
     rows_n, cols = BIG_M, 16384           # W = 2.5 GiB
     W, x = M.gen_f32_unit(0xB16 ^ 4, rows_n * cols, cols)
