@@ -188,10 +188,11 @@ constexpr size_t PIN_BYTES = 4u << 20;
 constexpr size_t OUT_DIRECT_BYTES = 256u << 10;
 // Layouts up to this size whose kernel reads each input element only a few
 // times (the tiny-shape GEMM kernels with at most 16 output tiles, the
-// GEMVs) are read by the kernels straight from the pinned buffer too, which
-// saves the copy-in launch as well (measured: 1-2 us at 16^3 - 64^3; at
-// 128^3 the Q16 tiles' re-reads over PCIe cost more than the copy, and the
-// dots, whose many blocks then read over PCIe, gained nothing).
+// one-block dots, the few-transform FFT) are read by the kernels straight
+// from the pinned buffer too, which saves the copy-in launch as well
+// (measured: 1-2 us at 16^3 - 64^3; at 128^3 the Q16 tiles' re-reads over
+// PCIe cost more than the copy).  The GEMVs, which read W once, do so on
+// the whole pinned route (gemv_host).
 constexpr size_t IN_DIRECT_BYTES = 64u << 10;
 
 struct HostIn {
@@ -551,7 +552,11 @@ int64_t gemv_host(bool q16, int64_t w, int64_t x, int64_t y, int64_t m, int64_t 
     const size_t span = off_y + align256(bytes_y);
     if ((rc = ensure(&ds.io, &ds.io_bytes, span))) return rc;
     const bool pinned = pinned_route(ds, span);
-    const bool in_direct = pinned && span <= IN_DIRECT_BYTES;   // W read once, x once per row group
+    // W is read once and x once per row group: on the pinned route the
+    // kernels read both straight from the pinned buffer at every size
+    // (measured against copying them in first: mmi16 512^2 36.9 -> 32.0 us,
+    // gemvq 1000^2 145 -> 120 us)
+    const bool in_direct = pinned;
     char *io = in_direct ? (char *)ds.pin_dev : (char *)ds.io;
     hipStream_t s = ds.stream;
     const HostIn in[2] = {{0, (const void *)w, bytes_w}, {off_x, (const void *)x, bytes_x}};
