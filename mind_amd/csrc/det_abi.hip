@@ -188,11 +188,13 @@ constexpr size_t PIN_BYTES = 4u << 20;
 constexpr size_t OUT_DIRECT_BYTES = 256u << 10;
 // Layouts up to this size whose kernel reads each input element only a few
 // times (the tiny-shape GEMM kernels with at most 16 output tiles, the
-// one-block dots, the few-transform FFT) are read by the kernels straight
-// from the pinned buffer too, which saves the copy-in launch as well
-// (measured: 1-2 us at 16^3 - 64^3; at 128^3 the Q16 tiles' re-reads over
-// PCIe cost more than the copy).  The GEMVs, which read W once, do so on
-// the whole pinned route (gemv_host).
+// one-block dots) are read by the kernels straight from the pinned buffer
+// too, which saves the copy-in launch as well (measured: 1-2 us at 16^3 -
+// 64^3; at 128^3 the Q16 tiles' re-reads over PCIe cost more than the copy,
+// and a one-block dot of 16384 terms, one workgroup reading 128 KiB over
+// PCIe, took 33 instead of 24 us).  The GEMVs, the strict-f32 rows and the
+// workspace-free FFTs, which read each input once, do so on the whole
+// pinned route.
 constexpr size_t IN_DIRECT_BYTES = 64u << 10;
 
 struct HostIn {
@@ -626,10 +628,12 @@ int64_t f32_rows_host(const float *w, const float *x, float *y, int64_t rows, in
     const size_t span = off_y + align256(bytes_y);
     if ((rc = ensure(&ds.io, &ds.io_bytes, span))) return rc;
     const bool pinned = pinned_route(ds, span);
-    char *io = (char *)ds.io;
+    // W read once: the kernel reads the inputs straight from the pinned
+    // buffer on the whole pinned route (512^2 56-61 -> 42-51 us)
+    char *io = pinned ? (char *)ds.pin_dev : (char *)ds.io;
     hipStream_t s = ds.stream;
     const HostIn in[2] = {{0, w, bytes_w}, {off_x, x, bytes_x}};
-    if ((rc = put_inputs(ds, pinned, in, 2, s))) return rc;
+    if ((rc = put_inputs(ds, pinned, in, 2, s, pinned))) return rc;
     bool direct = false;
     float *dy = (float *)out_ptr(ds, pinned, off_y, bytes_y, &direct);
     DET_HIP_CHECK(det::launch_rows_f32((const float *)io, (const float *)(io + off_x), dy, rows, cols, met, s));
@@ -713,7 +717,10 @@ int64_t fft_host(int64_t re, int64_t im, int64_t tw, int64_t logn, int64_t n, in
     const bool pinned = pinned_route(ds, span);
     // a few small transforms (no workspace: one read and one write per
     // point, in place) run on the pinned buffer itself: no copy launches
-    const bool direct = pinned && need == 0 && span <= IN_DIRECT_BYTES;
+    // the LDS kernels read each point once and write it once: in and out
+    // through the pinned buffer itself on the whole pinned route (batch 64
+    // of 256 points 41.5 -> 35.5 us)
+    const bool direct = pinned && need == 0;
     char *io = direct ? (char *)ds.pin_dev : (char *)ds.io;
     hipStream_t s = ds.stream;
     const HostIn in[3] = {{0, (const void *)re, bytes}, {off_im, (const void *)im, bytes},
