@@ -357,12 +357,18 @@ int64_t put_inputs(DevState &ds, bool pinned, const HostIn *in, int n_in, hipStr
         }
         return 0;
     }
-    size_t end = 0;
+    size_t end = 0, total = 0;
+    for (int i = 0; i < n_in; ++i) total += in[i].bytes;
+    // large layouts: each input's copy kernel is queued as soon as its host
+    // copy is done, so it runs while the CPU copies the next input
+    const bool staged = !direct && total >= (512u << 10);
     for (int i = 0; i < n_in; ++i) {
         if (in[i].bytes) g_pool.copy((char *)ds.pin + in[i].off, in[i].src, in[i].bytes);
+        if (staged && in[i].bytes)
+            DET_HIP_CHECK(copy16(io + in[i].off, (char *)ds.pin_dev + in[i].off, in[i].bytes, s));
         if (in[i].off + in[i].bytes > end) end = in[i].off + in[i].bytes;
     }
-    if (!direct) DET_HIP_CHECK(copy16(io, ds.pin_dev, end, s));
+    if (!direct && !staged) DET_HIP_CHECK(copy16(io, ds.pin_dev, end, s));
     return 0;
 }
 
