@@ -687,8 +687,8 @@ def main() -> int:
 
     world = int(os.environ.get("WORLD_SIZE", "1"))
     if args.gpus != 1 or world != 1:
-        print("bench.py measures one GPU only: every box in this build has one MI355X; multi-GPU "
-              "sharding of this path (row bands, no collectives) is described in DESIGN.md, not run.",
+        print("bench.py measures one GPU only: every box in this build has one MI355X; sharding this "
+              "path over several GPUs (row bands of the output, no collectives) is a design, not run.",
               file=sys.stderr)
         return 2
     # the vendor leg runs first, in a child process, before any HIP call here

@@ -13,8 +13,7 @@ the library's own device flags (hipcc cross-compiles; no GPU needed).
    s_buffer_atomic_*, s_dcache_wb*, s_dcache_discard*).  Stores go through
    the vector memory path only.
 
-This file names those instructions, so it is listed in .gpurunignore: it is
-a CPU test and never needs the GPU box."""
+It is a CPU test: it never needs a GPU."""
 import concurrent.futures as cf
 import glob
 import os
